@@ -1,0 +1,155 @@
+"""LUT-GEMV benchmark on one MI355X (BASELINE metric: LUT-GEMV HBM GB/s at
+8192x8192, % of the 8 TB/s HBM peak).
+
+A step is one GEMV y = W x over an 8192x8192 weight with batch 1.  The
+headline workload is the 4-bit format with per-128-group scales (BASELINE
+config 3); the other formats of the sweep are reported beside it.  Weights
+rotate over >= 512 MiB of distinct device copies so neither the 256 MB MALL
+nor the L2 holds them between launches.  The timed region is bracketed by
+torch.cuda.synchronize() and HIP events recorded on the stream the kernels
+are launched on; value = algorithmic bytes per GEMV / average time per GEMV.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--formats int4,ternary,...]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "LUT-GEMV HBM GB/s (% of peak) at 8192x8192; 1B-arch decode tokens/s bs=1"
+HBM_PEAK_GBPS = 8000.0
+ROTATE_BYTES = 512 * 2**20
+
+FORMATS = {"int4": 6, "ternary": 1, "binary": 2, "rrq2": 3, "rrq3": 4, "int8": 7}
+
+
+def gemv_bench(L, synth, torch, fmt, n, steps, warmup):
+    """Time `steps` GEMVs of an n x n weight of format fmt; returns a dict."""
+    group = 0 if fmt == L.FMT_TERNARY else 128
+    planes, scales, g = synth.make_weights(fmt, n, n, seed=1000 + fmt, group=group)
+    B = synth.algorithmic_bytes(fmt, n, n, group=g)
+    copies = max(2, -(-ROTATE_BYTES // B))
+    ws = [L.Weight.from_planes(fmt, planes, scales, n, n, g) for _ in range(copies)]
+    del planes
+    flags = L.ROTATE_FWHT256   # config 3 rotates every format's activations (fused in the kernel)
+    x = torch.from_numpy(synth.make_activations(n, seed=5)).cuda()
+    y = torch.empty(n, dtype=torch.float32, device="cuda")
+    stream = torch.cuda.current_stream()
+    for i in range(warmup):
+        ws[i % copies].gemv(x, y, flags=flags, stream=stream)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for i in range(steps):
+        ws[i % copies].gemv(x, y, flags=flags, stream=stream)
+    end.record(stream)
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    gbps = B / (ms * 1e-3) / 1e9
+    out = {"format": L.FORMAT_NAMES[fmt], "rows": n, "cols": n, "group": g, "rotation": flags,
+           "algorithmic_bytes": B, "us_per_gemv": round(ms * 1e3, 3), "GB_per_s": round(gbps, 1),
+           "frac_of_peak": round(gbps / HBM_PEAK_GBPS, 4), "weight_copies": copies,
+           "rotated_MiB": round(copies * B / 2**20, 1)}
+    for w in ws:
+        w.close()
+    return out
+
+
+def cpu_baseline(n, budget_s=10.0):
+    """The reference's own int4_gemv (oracle/_ref, scalar, 1 thread) on the
+    same n x n 4-bit GEMV, in its native 256-weight blocks, for ~budget_s."""
+    import oracle
+    from lutmac_amd import synth
+    rng = np.random.default_rng(7)
+    bpr = n // 256
+    nb = n * bpr
+    blocks = np.empty((nb, 132), np.uint8)
+    blocks[:, :128] = rng.integers(0, 256, (nb, 128), dtype=np.uint8)
+    blocks[:, 128:] = (np.abs(rng.standard_normal(nb)) * 0.02).astype(np.float32).view(np.uint8).reshape(nb, 4)
+    blocks = blocks.ravel()
+    x = synth.make_activations(n, seed=5)
+    y = np.zeros(n, np.float32)
+    R = oracle.ref()
+    kind = "reference" if R is not None else "port"
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        if R is not None:
+            R.ref_gemv(6, oracle._ptr(blocks), nb, oracle._ptr(x), oracle._ptr(y), n, n)
+        else:
+            oracle.lib().orc_int4_gemv(oracle._ptr(blocks), oracle._ptr(x), oracle._ptr(y), n, n)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s:
+            break
+    t = el / reps
+    B = synth.algorithmic_bytes(6, n, n, group=256)
+    return {"value": round(B / t / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": kind,
+            "sample": (f"{'oracle/_ref int4_gemv (reference lut_gemm_scalar.cpp:186-222)' if R else 'oracle int4 port'}"
+                       f" {n}x{n} batch 1, native 256-weight blocks, {reps} GEMVs in {el:.1f} s"
+                       f" ({t * 1e3:.1f} ms each), 1 thread"),
+            "ms_per_gemv": round(t * 1e3, 2)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--size", type=int, default=8192)
+    ap.add_argument("--formats", default="int4,ternary,binary,rrq2,rrq3,int8")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
+              "(see DESIGN.md for how the GEMV would shard)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import lutmac_amd as L
+    from lutmac_amd import synth
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+
+    names = [f for f in args.formats.split(",") if f]
+    sweep = {}
+    for name in names:
+        r = gemv_bench(L, synth, torch, FORMATS[name], args.size, args.steps, args.warmup)
+        sweep[name] = r
+        print(f"# {name}: {r['us_per_gemv']} us/GEMV, {r['GB_per_s']} GB/s "
+              f"({100 * r['frac_of_peak']:.1f}% of peak)", file=sys.stderr, flush=True)
+    head = sweep.get("int4") or sweep[names[0]]
+    cpu = None if args.no_cpu else cpu_baseline(args.size, args.cpu_seconds)
+    line = {
+        "metric": METRIC,
+        "value": head["GB_per_s"],
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["us_per_gemv"] / 1e3, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded uniform codes, |N(0,1)|*0.02 group scales, N(0,1) activations)",
+        "config": {"workload": f"LUT-GEMV {head['format']} {args.size}x{args.size} batch 1, "
+                               f"group {head['group']} (BASELINE config 3)",
+                   "rows": args.size, "cols": args.size, "format": head["format"],
+                   "group": head["group"], "batch": 1, "weight_copies": head["weight_copies"],
+                   "rotated_MiB": head["rotated_MiB"]},
+        "roofline": {"bound": "hbm", "achieved": head["GB_per_s"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": head["frac_of_peak"], "traffic": None},
+        "cpu_baseline": cpu,
+        "sweep": sweep,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,258 @@
+"""lutmac_amd -- MI355X-native bit-serial LUT-GEMV path for LutMac.
+
+Python host side over the C ABI in include/lutmac_hip.h (ctypes, no torch
+types in the ABI).  torch is used only for device memory and streams.  The
+shared library lutmac_amd/liblutmac_hip.so is built in-tree by
+``python -m lutmac_amd.build``; importing this package without it raises, so
+nothing can silently fall back to a CPU path.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liblutmac_hip.so")
+
+# lmx_format (include/lutmac_hip.h)
+FMT_TERNARY, FMT_BINARY, FMT_RRQ2, FMT_RRQ3, FMT_INT3, FMT_INT4, FMT_INT8 = range(1, 8)
+FORMAT_NAMES = {1: "ternary", 2: "binary", 3: "rrq2", 4: "rrq3", 5: "int3", 6: "int4", 7: "int8"}
+PLANES = {1: 2, 2: 1, 3: 2, 4: 3, 5: 3, 6: 4, 7: 8}
+STAGES = {1: 1, 2: 1, 3: 2, 4: 3, 5: 1, 6: 1, 7: 1}
+BLOCK_BYTES = {1: 68, 2: 36, 3: 72, 5: 100, 6: 132, 7: 260}
+
+ROTATE_NONE, ROTATE_FWHT256, ROTATE_FWHT_FULL = 0, 1, 2
+
+OK, ERR_INVALID_ARGUMENT, ERR_UNSUPPORTED_FORMAT, ERR_NO_DEVICE, ERR_OUT_OF_MEMORY, \
+    ERR_LAUNCH_FAILED, ERR_HIP = range(7)
+
+# Every symbol include/lutmac_hip.h declares (checked by the CPU tests).
+EXPORTS = [
+    "lmx_status_string", "lmx_last_error", "lmx_device_count", "lmx_version",
+    "lmx_format_info", "lmx_block_bytes", "lmx_blocks_to_planes", "lmx_planes_to_blocks",
+    "lmx_tile_bytes", "lmx_tile_planes", "lmx_untile_planes",
+    "lmx_weight_create", "lmx_weight_from_blocks", "lmx_weight_destroy", "lmx_weight_info",
+    "lmx_weight_read_tiles", "lmx_gemv", "lmx_linear", "lmx_fwht256",
+    "lmx_precompute_luts", "lmx_extract_indices",
+]
+
+
+class LmxError(RuntimeError):
+    def __init__(self, status, msg):
+        super().__init__(f"lmx status {status}: {msg}")
+        self.status = status
+
+
+class PlanesDesc(ctypes.Structure):
+    _fields_ = [("format", ctypes.c_int), ("rows", ctypes.c_size_t), ("cols", ctypes.c_size_t),
+                ("group", ctypes.c_size_t), ("planes", ctypes.c_void_p), ("scales", ctypes.c_void_p)]
+
+
+_p, _sz, _i, _u = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_uint
+_SIGS = {
+    "lmx_status_string": ([_i], ctypes.c_char_p),
+    "lmx_last_error": ([], ctypes.c_char_p),
+    "lmx_device_count": ([ctypes.POINTER(_i)], _i),
+    "lmx_version": ([], _i),
+    "lmx_format_info": ([_i, ctypes.POINTER(_i), ctypes.POINTER(_i)], _i),
+    "lmx_block_bytes": ([_i, ctypes.POINTER(_sz)], _i),
+    "lmx_blocks_to_planes": ([_i, _p, _sz, _sz, _sz, _p, _p], _i),
+    "lmx_planes_to_blocks": ([_i, _p, _p, _sz, _sz, _p, _sz], _i),
+    "lmx_tile_bytes": ([_i, _sz, _sz, ctypes.POINTER(_sz)], _i),
+    "lmx_tile_planes": ([_i, _p, _sz, _sz, _p], _i),
+    "lmx_untile_planes": ([_i, _p, _sz, _sz, _p], _i),
+    "lmx_weight_create": ([ctypes.POINTER(PlanesDesc), ctypes.POINTER(_p)], _i),
+    "lmx_weight_from_blocks": ([_i, _p, _sz, _sz, _sz, ctypes.POINTER(_p)], _i),
+    "lmx_weight_destroy": ([_p], _i),
+    "lmx_weight_info": ([_p, ctypes.POINTER(_i), ctypes.POINTER(_sz), ctypes.POINTER(_sz),
+                         ctypes.POINTER(_sz)], _i),
+    "lmx_weight_read_tiles": ([_p, _p, _sz], _i),
+    "lmx_gemv": ([_p, _p, _p, _sz, _u, _p], _i),
+    "lmx_linear": ([_p, _p, _p, _p, _sz, _p], _i),
+    "lmx_fwht256": ([_p, _sz, _p], _i),
+    "lmx_precompute_luts": ([_p, _sz, _u, _p, _p], _i),
+    "lmx_extract_indices": ([_p, _p, _sz, _p, _p, _p], _i),
+}
+
+_LIB = None
+
+
+def lib():
+    """The loaded C-ABI library; raises if it has not been built."""
+    global _LIB
+    if _LIB is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: build it with `python -m lutmac_amd.build`")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (args, res) in _SIGS.items():
+            f = getattr(L, name)
+            f.argtypes = args
+            f.restype = res
+        _LIB = L
+    return _LIB
+
+
+def check(status):
+    if status != OK:
+        raise LmxError(status, lib().lmx_last_error().decode(errors="replace"))
+
+
+def _np_ptr(a):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _dev_ptr(t):
+    """Device pointer of a torch tensor (None passes NULL)."""
+    if t is None:
+        return None
+    if not t.is_cuda:
+        raise ValueError("expected a device tensor")
+    if not t.is_contiguous():
+        raise ValueError("expected a contiguous tensor")
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def _stream_ptr(stream):
+    if stream is None:
+        import torch
+        stream = torch.cuda.current_stream()
+    return ctypes.c_void_p(stream.cuda_stream)
+
+
+# ---- host-only helpers -----------------------------------------------------
+
+def blocks_to_planes(fmt, blocks, rows, cols):
+    Kp = (cols + 255) // 256 * 256
+    planes = np.zeros(PLANES[fmt] * rows * Kp // 8, np.uint8)
+    scales = np.zeros(STAGES[fmt] * rows * (Kp // 256), np.float32)
+    blocks = np.ascontiguousarray(blocks, np.uint8)
+    check(lib().lmx_blocks_to_planes(fmt, _np_ptr(blocks), rows * (Kp // 256), rows, cols,
+                                     _np_ptr(planes), _np_ptr(scales)))
+    return planes, scales
+
+
+def planes_to_blocks(fmt, planes, scales, rows, cols):
+    nb = rows * ((cols + 255) // 256)
+    out = np.zeros(nb * BLOCK_BYTES[fmt], np.uint8)
+    planes = np.ascontiguousarray(planes, np.uint8)
+    scales = np.ascontiguousarray(scales, np.float32)
+    check(lib().lmx_planes_to_blocks(fmt, _np_ptr(planes), _np_ptr(scales), rows, cols,
+                                     _np_ptr(out), nb))
+    return out
+
+
+def tile_bytes(fmt, rows, cols):
+    n = ctypes.c_size_t()
+    check(lib().lmx_tile_bytes(fmt, rows, cols, ctypes.byref(n)))
+    return n.value
+
+
+def tile_planes(fmt, planes, rows, cols):
+    out = np.zeros(tile_bytes(fmt, rows, cols), np.uint8)
+    planes = np.ascontiguousarray(planes, np.uint8)
+    check(lib().lmx_tile_planes(fmt, _np_ptr(planes), rows, cols, _np_ptr(out)))
+    return out
+
+
+def untile_planes(fmt, tiles, rows, cols):
+    out = np.zeros(PLANES[fmt] * rows * cols // 8, np.uint8)
+    tiles = np.ascontiguousarray(tiles, np.uint8)
+    check(lib().lmx_untile_planes(fmt, _np_ptr(tiles), rows, cols, _np_ptr(out)))
+    return out
+
+
+def device_count():
+    n = ctypes.c_int()
+    lib().lmx_device_count(ctypes.byref(n))
+    return n.value
+
+
+# ---- device weights and compute ---------------------------------------------
+
+class Weight:
+    """Device weight handle (lmx_weight); destroyed with the object."""
+
+    def __init__(self, handle):
+        self._h = handle
+        fmt, rows, cols, nbytes = ctypes.c_int(), ctypes.c_size_t(), ctypes.c_size_t(), ctypes.c_size_t()
+        check(lib().lmx_weight_info(handle, ctypes.byref(fmt), ctypes.byref(rows), ctypes.byref(cols),
+                                    ctypes.byref(nbytes)))
+        self.format, self.rows, self.cols, self.device_bytes = fmt.value, rows.value, cols.value, nbytes.value
+
+    @classmethod
+    def from_planes(cls, fmt, planes, scales, rows, cols, group):
+        planes = np.ascontiguousarray(planes, np.uint8)
+        scales = np.ascontiguousarray(scales, np.float32)
+        d = PlanesDesc(fmt, rows, cols, group, planes.ctypes.data, scales.ctypes.data)
+        h = ctypes.c_void_p()
+        check(lib().lmx_weight_create(ctypes.byref(d), ctypes.byref(h)))
+        return cls(h)
+
+    @classmethod
+    def from_blocks(cls, fmt, blocks, rows, cols):
+        blocks = np.ascontiguousarray(blocks, np.uint8)
+        nb = rows * ((cols + 255) // 256)
+        h = ctypes.c_void_p()
+        check(lib().lmx_weight_from_blocks(fmt, _np_ptr(blocks), nb, rows, cols, ctypes.byref(h)))
+        return cls(h)
+
+    @property
+    def handle(self):
+        return self._h
+
+    def read_tiles(self):
+        out = np.zeros(tile_bytes(self.format, self.rows, self.cols), np.uint8)
+        check(lib().lmx_weight_read_tiles(self._h, _np_ptr(out), out.size))
+        return out
+
+    def gemv(self, x, y=None, flags=ROTATE_NONE, stream=None):
+        import torch
+        batch = x.numel() // self.cols
+        if y is None:
+            y = torch.empty(batch * self.rows, dtype=torch.float32, device=x.device)
+        check(lib().lmx_gemv(self._h, _dev_ptr(x), _dev_ptr(y), batch, flags, _stream_ptr(stream)))
+        return y
+
+    def linear(self, x, bias=None, y=None, stream=None):
+        import torch
+        batch = x.numel() // self.cols
+        if y is None:
+            y = torch.empty(batch * self.rows, dtype=torch.float32, device=x.device)
+        check(lib().lmx_linear(self._h, _dev_ptr(bias), _dev_ptr(x), _dev_ptr(y), batch,
+                               _stream_ptr(stream)))
+        return y
+
+    def close(self):
+        if self._h:
+            lib().lmx_weight_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def fwht256(x, stream=None):
+    """In-place blockwise FWHT-256 of a device tensor."""
+    check(lib().lmx_fwht256(_dev_ptr(x), x.numel(), _stream_ptr(stream)))
+    return x
+
+
+def precompute_luts(x, rotate=False, stream=None):
+    import torch
+    n = x.numel()
+    luts = torch.empty((n // 4) * 16, dtype=torch.float32, device=x.device)
+    check(lib().lmx_precompute_luts(_dev_ptr(x), n, ROTATE_FWHT256 if rotate else ROTATE_NONE,
+                                    _dev_ptr(luts), _stream_ptr(stream)))
+    return luts
+
+
+def extract_indices(sign_plane, zero_plane, n_groups, stream=None):
+    import torch
+    pos = torch.empty(n_groups, dtype=torch.uint8, device=sign_plane.device)
+    neg = torch.empty(n_groups, dtype=torch.uint8, device=sign_plane.device)
+    check(lib().lmx_extract_indices(_dev_ptr(sign_plane), _dev_ptr(zero_plane), n_groups,
+                                    _dev_ptr(pos), _dev_ptr(neg), _stream_ptr(stream)))
+    return pos, neg

@@ -1,0 +1,58 @@
+"""Build the in-tree HIP library (lutmac_amd/liblutmac_hip.so) for gfx950.
+
+Run as ``python -m lutmac_amd.build``.  Object files go to lutmac_amd/_build/
+(git-ignored); the shared library lands next to this file so it travels with
+the tree.  Every HIP translation unit is compiled with packed-FP32 code
+generation disabled (``-Xclang -target-feature -Xclang -packed-fp32-ops``).
+"""
+import os
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+CSRC = os.path.join(HERE, "csrc")
+OUT_DIR = os.path.join(HERE, "_build")
+LIB = os.path.join(HERE, "liblutmac_hip.so")
+ARCH = os.environ.get("LMX_OFFLOAD_ARCH", "gfx950")
+
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+COMMON = ["-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-result",
+          "-I", os.path.join(ROOT, "include"), "-I", CSRC]
+DEVICE = ["-x", "hip", f"--offload-arch={ARCH}",
+          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+          "-munsafe-fp-atomics"]
+
+SOURCES = [
+    ("lmx_kernels.hip", True),
+    ("lmx_capi.cpp", False),
+    ("lmx_repack.cpp", False),
+    ("lut_gemm_compat.cpp", False),
+]
+
+
+def _run(cmd, verbose):
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    subprocess.run(cmd, check=True)
+
+
+def build(verbose=True):
+    os.makedirs(OUT_DIR, exist_ok=True)
+    objs = []
+    for src, device in SOURCES:
+        path = os.path.join(CSRC, src)
+        if not os.path.exists(path):
+            continue
+        obj = os.path.join(OUT_DIR, src + ".o")
+        flags = COMMON + (DEVICE if device else ["-D__HIP_PLATFORM_AMD__"])
+        _run([HIPCC] + flags + ["-c", path, "-o", obj], verbose)
+        objs.append(obj)
+    tmp = LIB + ".tmp"
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp] + objs, verbose)
+    os.replace(tmp, LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    build(verbose="-q" not in sys.argv)

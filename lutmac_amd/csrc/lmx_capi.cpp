@@ -1,0 +1,424 @@
+// lmx_capi.cpp -- the C ABI (include/lutmac_hip.h): argument validation,
+// weight handles (repack + upload), launch configuration.  Nothing here
+// throws across the ABI; every failure returns an lmx_status and records a
+// thread-local message.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <new>
+#include <vector>
+
+#include "lmx_internal.hpp"
+
+namespace lmx {
+
+namespace {
+thread_local char g_err[512] = "";
+}
+
+int fail(int status, const char *fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  std::vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return status;
+}
+
+void clear_error() { g_err[0] = '\0'; }
+
+namespace {
+
+int hip_fail(hipError_t e, const char *what) {
+  if (e == hipErrorOutOfMemory) return fail(LMX_ERR_OUT_OF_MEMORY, "%s: %s", what, hipGetErrorString(e));
+  if (e == hipErrorNoDevice || e == hipErrorInvalidDevice)
+    return fail(LMX_ERR_NO_DEVICE, "%s: %s", what, hipGetErrorString(e));
+  return fail(LMX_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+int require_device(int *dev) {
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess || n <= 0) return fail(LMX_ERR_NO_DEVICE, "no HIP device visible");
+  e = hipGetDevice(dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  return LMX_OK;
+}
+
+// Workgroups wanted in flight: several per CU so HBM requests overlap.
+constexpr int kTargetGroups = 1024;
+
+int choose_kslice(int fmt, size_t Npad, size_t Kp) {
+  static const int env = [] {
+    const char *s = std::getenv("LMX_KSLICE");
+    return s ? std::atoi(s) : 0;
+  }();
+  FormatInfo fi;
+  format_info(fmt, &fi);
+  const size_t row_blocks = (Npad + kRowsPerGroup - 1) / kRowsPerGroup;
+  const int cand[3] = {1024, 512, 256};
+  if (env == 256 || env == 512 || (env == 1024 && fi.planes <= 4))
+    if (Kp % size_t(env) == 0) return env;
+  for (int ks : cand) {
+    if (ks == 1024 && fi.planes > 4) continue;
+    if (Kp % size_t(ks)) continue;
+    if (row_blocks * (Kp / size_t(ks)) >= size_t(kTargetGroups)) return ks;
+  }
+  return 256;
+}
+
+void free_weight(lmx_weight *w) {
+  if (!w) return;
+  if (w->d_planes) (void)hipFree(w->d_planes);
+  if (w->d_scales) (void)hipFree(w->d_scales);
+  if (w->d_partials) (void)hipFree(w->d_partials);
+  if (w->d_counters) (void)hipFree(w->d_counters);
+  if (w->d_xrot) (void)hipFree(w->d_xrot);
+  delete w;
+}
+
+// Shared tail of both constructors: canonical planes/scales on the host ->
+// device tile layout, scales transposed to [S][n_groups][Npad].
+int upload(int fmt, size_t rows, size_t cols, size_t group, const uint8_t *planes, size_t row_bytes,
+           const float *scales, size_t ng_src, lmx_weight **out) {
+  FormatInfo fi;
+  format_info(fmt, &fi);
+  int dev = 0;
+  int st = require_device(&dev);
+  if (st) return st;
+  lmx_weight *w = new (std::nothrow) lmx_weight;
+  if (!w) return fail(LMX_ERR_OUT_OF_MEMORY, "host allocation failed");
+  w->format = fmt;
+  w->device = dev;
+  w->rows = rows;
+  w->cols = cols;
+  w->Npad = round_up(rows, kWave);
+  w->Kp = round_up(cols, kRotChunk);
+  w->group = group ? group : w->Kp;
+  w->n_groups = (w->Kp + w->group - 1) / w->group;
+  w->tile_bytes = (w->Kp / kChunk) * fi.planes * w->Npad * 16;
+  w->scale_bytes = size_t(fi.stages) * w->n_groups * w->Npad * sizeof(float);
+  w->kslice = choose_kslice(fmt, w->Npad, w->Kp);
+
+  std::vector<uint8_t> tiles;
+  std::vector<float> sc;
+  try {
+    tiles.resize(w->tile_bytes);
+    sc.assign(w->scale_bytes / sizeof(float), 0.0f);
+  } catch (const std::bad_alloc &) {
+    delete w;
+    return fail(LMX_ERR_OUT_OF_MEMORY, "host staging allocation failed");
+  }
+  tile_planes(fmt, planes, rows, row_bytes, w->Npad, w->Kp, tiles.data());
+  for (int s = 0; s < fi.stages; ++s)
+    for (size_t r = 0; r < rows; ++r)
+      for (size_t g = 0; g < ng_src && g < w->n_groups; ++g)
+        sc[(size_t(s) * w->n_groups + g) * w->Npad + r] = scales[(size_t(s) * rows + r) * ng_src + g];
+
+  const size_t row_blocks = (w->Npad + kRowsPerGroup - 1) / kRowsPerGroup;
+  const size_t max_splits = w->Kp / kRotChunk;
+  hipError_t e;
+  if ((e = hipMalloc(&w->d_planes, w->tile_bytes)) != hipSuccess ||
+      (e = hipMalloc(reinterpret_cast<void **>(&w->d_scales), w->scale_bytes)) != hipSuccess ||
+      (e = hipMalloc(reinterpret_cast<void **>(&w->d_partials), max_splits * w->Npad * sizeof(float))) != hipSuccess ||
+      (e = hipMalloc(reinterpret_cast<void **>(&w->d_counters), row_blocks * sizeof(unsigned))) != hipSuccess ||
+      (e = hipMalloc(reinterpret_cast<void **>(&w->d_xrot), w->Kp * sizeof(float))) != hipSuccess) {
+    free_weight(w);
+    return hip_fail(e, "hipMalloc (weight)");
+  }
+  if ((e = hipMemcpy(w->d_planes, tiles.data(), w->tile_bytes, hipMemcpyHostToDevice)) != hipSuccess ||
+      (e = hipMemcpy(w->d_scales, sc.data(), w->scale_bytes, hipMemcpyHostToDevice)) != hipSuccess ||
+      (e = hipMemset(w->d_counters, 0, row_blocks * sizeof(unsigned))) != hipSuccess ||
+      (e = hipDeviceSynchronize()) != hipSuccess) {
+    free_weight(w);
+    return hip_fail(e, "upload (weight)");
+  }
+  *out = w;
+  return LMX_OK;
+}
+
+int check_weight(const lmx_weight *w) {
+  if (!w) return fail(LMX_ERR_INVALID_ARGUMENT, "weight handle is NULL");
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  if (dev != w->device)
+    return fail(LMX_ERR_INVALID_ARGUMENT, "weight lives on device %d, current device is %d", w->device, dev);
+  return LMX_OK;
+}
+
+bool is_pow2(size_t n) { return n && !(n & (n - 1)); }
+
+}  // namespace
+}  // namespace lmx
+
+using namespace lmx;
+
+extern "C" {
+
+const char *lmx_status_string(int status) {
+  switch (status) {
+  case LMX_OK: return "ok";
+  case LMX_ERR_INVALID_ARGUMENT: return "invalid argument";
+  case LMX_ERR_UNSUPPORTED_FORMAT: return "unsupported format";
+  case LMX_ERR_NO_DEVICE: return "no device";
+  case LMX_ERR_OUT_OF_MEMORY: return "out of memory";
+  case LMX_ERR_LAUNCH_FAILED: return "launch failed";
+  case LMX_ERR_HIP: return "HIP runtime error";
+  }
+  return "unknown status";
+}
+
+const char *lmx_last_error(void) { return g_err; }
+
+int lmx_version(void) { return 100; }
+
+int lmx_device_count(int *count) {
+  if (!count) return fail(LMX_ERR_INVALID_ARGUMENT, "count is NULL");
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  *count = (e == hipSuccess && n > 0) ? n : 0;
+  if (*count == 0) return fail(LMX_ERR_NO_DEVICE, "no HIP device visible");
+  return LMX_OK;
+}
+
+int lmx_format_info(int format, int *planes, int *stages) {
+  FormatInfo fi;
+  if (!format_info(format, &fi)) return fail(LMX_ERR_UNSUPPORTED_FORMAT, "unknown format %d", format);
+  if (planes) *planes = fi.planes;
+  if (stages) *stages = fi.stages;
+  return LMX_OK;
+}
+
+int lmx_block_bytes(int format, size_t *bytes) {
+  FormatInfo fi;
+  if (!format_info(format, &fi)) return fail(LMX_ERR_UNSUPPORTED_FORMAT, "unknown format %d", format);
+  if (!fi.block_bytes) return fail(LMX_ERR_UNSUPPORTED_FORMAT, "format %d has no reference block", format);
+  if (!bytes) return fail(LMX_ERR_INVALID_ARGUMENT, "bytes is NULL");
+  *bytes = fi.block_bytes;
+  return LMX_OK;
+}
+
+int lmx_blocks_to_planes(int format, const void *blocks, size_t num_blocks, size_t rows, size_t cols,
+                         uint8_t *planes, float *scales) {
+  FormatInfo fi;
+  if (!format_info(format, &fi) || !fi.block_bytes)
+    return fail(LMX_ERR_UNSUPPORTED_FORMAT, "format %d has no reference block", format);
+  if (!blocks || !planes || !scales || rows == 0 || cols == 0)
+    return fail(LMX_ERR_INVALID_ARGUMENT, "NULL pointer or empty shape");
+  if (num_blocks != rows * ((cols + 255) / 256))
+    return fail(LMX_ERR_INVALID_ARGUMENT, "num_blocks %zu != rows*ceil(cols/256) = %zu", num_blocks,
+                rows * ((cols + 255) / 256));
+  return blocks_to_planes(format, static_cast<const uint8_t *>(blocks), rows, cols, planes, scales);
+}
+
+int lmx_planes_to_blocks(int format, const uint8_t *planes, const float *scales, size_t rows, size_t cols,
+                         void *blocks, size_t num_blocks) {
+  FormatInfo fi;
+  if (!format_info(format, &fi) || !fi.block_bytes)
+    return fail(LMX_ERR_UNSUPPORTED_FORMAT, "format %d has no reference block", format);
+  if (!blocks || !planes || !scales || rows == 0 || cols == 0)
+    return fail(LMX_ERR_INVALID_ARGUMENT, "NULL pointer or empty shape");
+  if (num_blocks != rows * ((cols + 255) / 256))
+    return fail(LMX_ERR_INVALID_ARGUMENT, "num_blocks %zu != rows*ceil(cols/256)", num_blocks);
+  return planes_to_blocks(format, planes, scales, rows, cols, static_cast<uint8_t *>(blocks));
+}
+
+int lmx_tile_bytes(int format, size_t rows, size_t cols, size_t *bytes) {
+  FormatInfo fi;
+  if (!format_info(format, &fi)) return fail(LMX_ERR_UNSUPPORTED_FORMAT, "unknown format %d", format);
+  if (!bytes || rows == 0 || cols == 0) return fail(LMX_ERR_INVALID_ARGUMENT, "NULL pointer or empty shape");
+  *bytes = (round_up(cols, kRotChunk) / kChunk) * fi.planes * round_up(rows, kWave) * 16;
+  return LMX_OK;
+}
+
+int lmx_tile_planes(int format, const uint8_t *planes, size_t rows, size_t cols, uint8_t *tiles) {
+  FormatInfo fi;
+  if (!format_info(format, &fi)) return fail(LMX_ERR_UNSUPPORTED_FORMAT, "unknown format %d", format);
+  if (!planes || !tiles || rows == 0 || cols == 0 || cols % 8)
+    return fail(LMX_ERR_INVALID_ARGUMENT, "NULL pointer, empty shape or cols not a multiple of 8");
+  tile_planes(format, planes, rows, cols / 8, round_up(rows, kWave), round_up(cols, kRotChunk), tiles);
+  return LMX_OK;
+}
+
+int lmx_untile_planes(int format, const uint8_t *tiles, size_t rows, size_t cols, uint8_t *planes) {
+  FormatInfo fi;
+  if (!format_info(format, &fi)) return fail(LMX_ERR_UNSUPPORTED_FORMAT, "unknown format %d", format);
+  if (!planes || !tiles || rows == 0 || cols == 0 || cols % 8)
+    return fail(LMX_ERR_INVALID_ARGUMENT, "NULL pointer, empty shape or cols not a multiple of 8");
+  untile_planes(format, tiles, rows, cols / 8, round_up(rows, kWave), round_up(cols, kRotChunk), planes);
+  return LMX_OK;
+}
+
+int lmx_weight_create(const lmx_planes_desc *d, lmx_weight **out) {
+  if (!d || !out) return fail(LMX_ERR_INVALID_ARGUMENT, "desc or out is NULL");
+  *out = nullptr;
+  FormatInfo fi;
+  if (!format_info(d->format, &fi)) return fail(LMX_ERR_UNSUPPORTED_FORMAT, "unknown format %d", d->format);
+  if (!d->planes || !d->scales) return fail(LMX_ERR_INVALID_ARGUMENT, "planes or scales is NULL");
+  if (d->rows == 0 || d->cols == 0 || d->cols % 8)
+    return fail(LMX_ERR_INVALID_ARGUMENT, "rows/cols must be > 0 and cols a multiple of 8");
+  if (d->rows > (1u << 30) || d->cols > (1u << 28))
+    return fail(LMX_ERR_INVALID_ARGUMENT, "shape %zu x %zu too large", d->rows, d->cols);
+  size_t group = d->group;
+  if (group >= round_up(d->cols, kRotChunk)) group = 0;
+  if (group && group % kChunk)
+    return fail(LMX_ERR_INVALID_ARGUMENT, "group %zu must be a multiple of 128 (or 0 = per row)", d->group);
+  const size_t ng_src = group ? (d->cols + group - 1) / group : 1;
+  return upload(d->format, d->rows, d->cols, group, d->planes, d->cols / 8, d->scales, ng_src, out);
+}
+
+int lmx_weight_from_blocks(int format, const void *blocks, size_t num_blocks, size_t rows, size_t cols,
+                           lmx_weight **out) {
+  if (!out) return fail(LMX_ERR_INVALID_ARGUMENT, "out is NULL");
+  *out = nullptr;
+  FormatInfo fi;
+  if (!format_info(format, &fi) || !fi.block_bytes)
+    return fail(LMX_ERR_UNSUPPORTED_FORMAT, "format %d has no reference block", format);
+  if (!blocks || rows == 0 || cols == 0) return fail(LMX_ERR_INVALID_ARGUMENT, "NULL blocks or empty shape");
+  const size_t bpr = (cols + 255) / 256;
+  if (num_blocks != rows * bpr)
+    return fail(LMX_ERR_INVALID_ARGUMENT, "num_blocks %zu != rows*ceil(cols/256) = %zu", num_blocks, rows * bpr);
+  std::vector<uint8_t> planes;
+  std::vector<float> scales;
+  try {
+    planes.resize(size_t(fi.planes) * rows * bpr * 32);
+    scales.resize(size_t(fi.stages) * rows * bpr);
+  } catch (const std::bad_alloc &) {
+    return fail(LMX_ERR_OUT_OF_MEMORY, "host staging allocation failed");
+  }
+  int st = blocks_to_planes(format, static_cast<const uint8_t *>(blocks), rows, cols, planes.data(), scales.data());
+  if (st) return st;
+  return upload(format, rows, cols, 256, planes.data(), bpr * 32, scales.data(), bpr, out);
+}
+
+int lmx_weight_destroy(lmx_weight *w) {
+  free_weight(w);
+  return LMX_OK;
+}
+
+int lmx_weight_info(const lmx_weight *w, int *format, size_t *rows, size_t *cols, size_t *device_bytes) {
+  if (!w) return fail(LMX_ERR_INVALID_ARGUMENT, "weight handle is NULL");
+  if (format) *format = w->format;
+  if (rows) *rows = w->rows;
+  if (cols) *cols = w->cols;
+  if (device_bytes) *device_bytes = w->tile_bytes + w->scale_bytes;
+  return LMX_OK;
+}
+
+int lmx_weight_read_tiles(const lmx_weight *w, uint8_t *tiles, size_t bytes) {
+  int st = check_weight(w);
+  if (st) return st;
+  if (!tiles || bytes != w->tile_bytes)
+    return fail(LMX_ERR_INVALID_ARGUMENT, "tiles NULL or bytes %zu != %zu", bytes, w->tile_bytes);
+  hipError_t e = hipMemcpy(tiles, w->d_planes, bytes, hipMemcpyDeviceToHost);
+  if (e != hipSuccess) return hip_fail(e, "hipMemcpy (read tiles)");
+  return LMX_OK;
+}
+
+int lmx_gemv(const lmx_weight *w, const float *x, float *y, size_t batch, unsigned flags, void *stream) {
+  int st = check_weight(w);
+  if (st) return st;
+  if (!x || !y) return fail(LMX_ERR_INVALID_ARGUMENT, "x or y is NULL");
+  if (reinterpret_cast<size_t>(x) % 4 || reinterpret_cast<size_t>(y) % 4)
+    return fail(LMX_ERR_INVALID_ARGUMENT, "x and y must be 4-byte aligned");
+  if (batch == 0) return LMX_OK;
+  if (flags != LMX_ROTATE_NONE && flags != LMX_ROTATE_FWHT256 && flags != LMX_ROTATE_FWHT_FULL)
+    return fail(LMX_ERR_INVALID_ARGUMENT, "unknown flags 0x%x", flags);
+  if (flags == LMX_ROTATE_FWHT_FULL && (!is_pow2(w->cols) || w->cols < 256 || w->cols > 16384))
+    return fail(LMX_ERR_INVALID_ARGUMENT, "length-K FWHT needs cols a power of two in [256, 16384], got %zu",
+                w->cols);
+  GemvArgs a{};
+  a.planes = w->d_planes;
+  a.scales = w->d_scales;
+  a.bias = nullptr;
+  a.partials = w->d_partials;
+  a.counters = w->d_counters;
+  a.rows = int(w->rows);
+  a.Npad = int(w->Npad);
+  a.cols = int(w->cols);
+  a.Kp = int(w->Kp);
+  a.group_chunks = int(w->group / kChunk);
+  a.n_groups = int(w->n_groups);
+  a.kslice = w->kslice;
+  for (size_t b = 0; b < batch; ++b) {
+    a.x = x + b * w->cols;
+    a.y = y + b * w->rows;
+    a.rotate = flags == LMX_ROTATE_FWHT256 ? LMX_ROTATE_FWHT256 : LMX_ROTATE_NONE;
+    if (flags == LMX_ROTATE_FWHT_FULL) {
+      st = launch_fwht_full(a.x, w->d_xrot, w->cols, stream);
+      if (st) return st;
+      a.x = w->d_xrot;
+    }
+    st = launch_gemv(w->format, a, stream);
+    if (st) return st;
+  }
+  return LMX_OK;
+}
+
+int lmx_linear(const lmx_weight *w, const float *bias, const float *x, float *y, size_t batch, void *stream) {
+  int st = check_weight(w);
+  if (st) return st;
+  if (!x || !y) return fail(LMX_ERR_INVALID_ARGUMENT, "x or y is NULL");
+  if (batch == 0) return LMX_OK;
+  const bool rotate = w->format == LMX_FMT_TERNARY || w->format == LMX_FMT_BINARY ||
+                      w->format == LMX_FMT_RRQ2 || w->format == LMX_FMT_RRQ3;
+  GemvArgs a{};
+  a.planes = w->d_planes;
+  a.scales = w->d_scales;
+  a.bias = bias;
+  a.partials = w->d_partials;
+  a.counters = w->d_counters;
+  a.rows = int(w->rows);
+  a.Npad = int(w->Npad);
+  a.cols = int(w->cols);
+  a.Kp = int(w->Kp);
+  a.group_chunks = int(w->group / kChunk);
+  a.n_groups = int(w->n_groups);
+  a.kslice = w->kslice;
+  a.rotate = rotate ? LMX_ROTATE_FWHT256 : LMX_ROTATE_NONE;
+  for (size_t b = 0; b < batch; ++b) {
+    a.x = x + b * w->cols;
+    a.y = y + b * w->rows;
+    st = launch_gemv(w->format, a, stream);
+    if (st) return st;
+  }
+  return LMX_OK;
+}
+
+int lmx_fwht256(float *x, size_t n, void *stream) {
+  if (!x) return fail(LMX_ERR_INVALID_ARGUMENT, "x is NULL");
+  if (n % kRotChunk) return fail(LMX_ERR_INVALID_ARGUMENT, "n %zu is not a multiple of 256", n);
+  if (reinterpret_cast<size_t>(x) % 16) return fail(LMX_ERR_INVALID_ARGUMENT, "x must be 16-byte aligned");
+  int dev;
+  int st = require_device(&dev);
+  if (st) return st;
+  return launch_fwht256(x, n, stream);
+}
+
+int lmx_precompute_luts(const float *x, size_t n, unsigned flags, float *luts, void *stream) {
+  if (!x || !luts) return fail(LMX_ERR_INVALID_ARGUMENT, "x or luts is NULL");
+  if (flags != LMX_ROTATE_NONE && flags != LMX_ROTATE_FWHT256)
+    return fail(LMX_ERR_INVALID_ARGUMENT, "flags must be NONE or FWHT256");
+  if (flags == LMX_ROTATE_FWHT256 && n % kRotChunk)
+    return fail(LMX_ERR_INVALID_ARGUMENT, "rotated table build needs n a multiple of 256");
+  if (n > (size_t(1) << 30)) return fail(LMX_ERR_INVALID_ARGUMENT, "n too large");
+  int dev;
+  int st = require_device(&dev);
+  if (st) return st;
+  return launch_precompute_luts(x, n, flags, luts, stream);
+}
+
+int lmx_extract_indices(const uint8_t *sign_plane, const uint8_t *zero_plane, size_t n_groups, uint8_t *pos_idx,
+                        uint8_t *neg_idx, void *stream) {
+  if (!sign_plane || !zero_plane || !pos_idx || !neg_idx)
+    return fail(LMX_ERR_INVALID_ARGUMENT, "NULL pointer");
+  int dev;
+  int st = require_device(&dev);
+  if (st) return st;
+  return launch_extract_indices(sign_plane, zero_plane, n_groups, pos_idx, neg_idx, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,88 @@
+// lmx_internal.hpp -- shared definitions of the LUT-GEMV library (not part
+// of the C ABI).
+#pragma once
+
+#include <cstddef>
+#include <cstdint>
+#include <string>
+
+#include "lutmac_hip.h"
+
+namespace lmx {
+
+constexpr int kChunk = 128;        // k per chunk: one uint4 per plane per row
+constexpr int kRotChunk = 256;     // FWHT-256 block and device K padding
+constexpr int kWave = 64;          // lanes per wavefront (one row per lane)
+constexpr int kWavesPerGroup = 4;  // wavefronts per workgroup
+constexpr int kRowsPerGroup = kWave * kWavesPerGroup;
+
+inline size_t round_up(size_t v, size_t m) { return (v + m - 1) / m * m; }
+
+struct FormatInfo {
+  int planes;
+  int stages;
+  size_t block_bytes;  // reference AoS block size; 0 = no reference block
+};
+
+bool format_info(int fmt, FormatInfo *fi);
+
+// Sets the thread-local error message and returns `status`.
+int fail(int status, const char *fmt, ...);
+void clear_error();
+
+// ---- host repack (lmx_repack.cpp) ----------------------------------------
+int blocks_to_planes(int fmt, const uint8_t *blocks, size_t rows, size_t cols,
+                     uint8_t *planes, float *scales);
+int planes_to_blocks(int fmt, const uint8_t *planes, const float *scales,
+                     size_t rows, size_t cols, uint8_t *blocks);
+// planes: [P][rows][row_bytes]; tiles: [Kp/128][P][Npad][16].  Columns past
+// row_bytes*8 get the format's pad code (pad_byte), rows past `rows` zero.
+uint8_t pad_byte(int fmt, int plane);
+void tile_planes(int fmt, const uint8_t *planes, size_t rows, size_t row_bytes,
+                 size_t Npad, size_t Kp, uint8_t *tiles);
+void untile_planes(int fmt, const uint8_t *tiles, size_t rows, size_t row_bytes,
+                   size_t Npad, size_t Kp, uint8_t *planes);
+
+// ---- device launches (lmx_kernels.hip) -----------------------------------
+struct GemvArgs {
+  const void *planes;      // tiled planes
+  const float *scales;     // [S][n_groups][Npad]
+  const float *x;          // [cols]
+  float *y;                // [rows]
+  const float *bias;       // [rows] or null
+  float *partials;         // [splits][Npad]
+  unsigned *counters;      // [row_blocks]
+  int rows, Npad, cols, Kp;
+  int group_chunks;        // chunks per scale group
+  int n_groups;
+  int kslice;              // k per workgroup (multiple of 256, divides Kp)
+  unsigned rotate;         // LMX_ROTATE_NONE / LMX_ROTATE_FWHT256
+};
+
+int launch_gemv(int fmt, const GemvArgs &a, void *stream);
+int launch_fwht256(float *x, size_t n, void *stream);
+int launch_fwht_full(const float *x, float *out, size_t n, void *stream);
+int launch_precompute_luts(const float *x, size_t n, unsigned flags,
+                           float *luts, void *stream);
+int launch_extract_indices(const uint8_t *s, const uint8_t *z, size_t n_groups,
+                           uint8_t *pos, uint8_t *neg, void *stream);
+
+}  // namespace lmx
+
+// Device weight handle (opaque to C callers).
+struct lmx_weight {
+  int format = 0;
+  int device = 0;
+  size_t rows = 0, cols = 0;
+  size_t Npad = 0, Kp = 0;
+  size_t group = 0;        // scale group in k on the device (multiple of 128)
+  size_t n_groups = 0;     // Kp / group
+  size_t tile_bytes = 0;
+  size_t scale_bytes = 0;
+  int kslice = 0;          // chosen k-slice per workgroup
+  void *d_planes = nullptr;
+  float *d_scales = nullptr;
+  float *d_partials = nullptr;
+  unsigned *d_counters = nullptr;
+  float *d_xrot = nullptr;  // staging for LMX_ROTATE_FWHT_FULL (cols floats)
+};

@@ -1,0 +1,395 @@
+// lmx_kernels.hip -- gfx950 kernels of the bit-serial LUT-GEMV path.
+//
+// One GEMV = one launch of lut_gemv_kernel<FMT, CHUNKS>:
+//   * a workgroup owns 256 output rows (4 wavefronts, one row per lane) and a
+//     k-slice of CHUNKS*128 activations;
+//   * prologue (fused): each wavefront takes one 256-chunk of x, rotates it
+//     with an in-register FWHT-256 (butterflies across lanes via shuffles)
+//     when asked, and writes the 16-entry partial-sum table of every group
+//     of 4 activations straight into LDS (lane l owns group l of the chunk);
+//   * main loop: every lane streams its row's bit-planes (one 16-byte load
+//     per plane per 128-k chunk, 1 KiB contiguous per wavefront), turns each
+//     plane nibble into an LDS address with one v_perm and accumulates the
+//     looked-up partial sums in fp32.  All 64 lanes read the same 16-entry
+//     table at a time, so a lookup touches 16 consecutive dwords: no bank
+//     conflicts, broadcast for equal indices;
+//   * split-K: each workgroup writes one partial per row; the last workgroup
+//     of a row block (atomic ticket) sums the partials in split order, adds
+//     the bias and writes y, so results do not depend on scheduling.
+//
+// Per-format identities (T = group table, m_p = plane-p nibble, ~ = 4-bit
+// complement, xs = sum of the chunk's activations):
+//   ternary  T[~s&~z] - T[s&~z]                    (lut_gemm.hpp:79-99)
+//   binary   2*T[m] - T[15]
+//   RRQ-k    sum_i s_i * (2*T[m_i] - T[15])        (Int2Block::get generalised)
+//   int3     T[m0] + 2T[m1] - 4T[~m2]              ((q-4) with q = 4b2+2b1+b0)
+//   int4     T[m0] + 2T[m1] + 4T[m2] - 8T[~m3]     ((q-8))
+//   int8     sum_{b<7} 2^b T[m_b] - 128 T[m7]      (two's complement)
+#include <hip/hip_runtime.h>
+
+#include "lmx_internal.hpp"
+
+namespace lmx {
+
+typedef __attribute__((address_space(3))) float lds_f32;
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float lds_load(uint32_t byte_addr) {
+  return *(const lds_f32 *)(size_t)byte_addr;
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const float *p) {
+  return (uint32_t)(size_t)(const lds_f32 *)p;
+}
+
+// ---------------------------------------------------------------------------
+// Format traits: loaded planes P, accumulators NA, scale stages S.
+template <int FMT> struct Fmt;
+template <> struct Fmt<LMX_FMT_TERNARY> { static constexpr int P = 2, NA = 2, S = 1; static constexpr bool XS = false; };
+template <> struct Fmt<LMX_FMT_BINARY> { static constexpr int P = 1, NA = 1, S = 1; static constexpr bool XS = true; };
+template <> struct Fmt<LMX_FMT_RRQ2> { static constexpr int P = 2, NA = 2, S = 2; static constexpr bool XS = true; };
+template <> struct Fmt<LMX_FMT_RRQ3> { static constexpr int P = 3, NA = 3, S = 3; static constexpr bool XS = true; };
+template <> struct Fmt<LMX_FMT_INT3> { static constexpr int P = 3, NA = 3, S = 1; static constexpr bool XS = false; };
+template <> struct Fmt<LMX_FMT_INT4> { static constexpr int P = 4, NA = 4, S = 1; static constexpr bool XS = false; };
+template <> struct Fmt<LMX_FMT_INT8> { static constexpr int P = 8, NA = 8, S = 1; static constexpr bool XS = false; };
+
+// Plane words -> lookup words (one per accumulator).
+template <int FMT>
+__device__ __forceinline__ void lookup_words(const uint32_t *w, uint32_t *v) {
+  if constexpr (FMT == LMX_FMT_TERNARY) {
+    v[0] = ~(w[0] | w[1]);   // non-zero and positive
+    v[1] = w[0] & ~w[1];     // non-zero and negative
+  } else if constexpr (FMT == LMX_FMT_INT3) {
+    v[0] = w[0]; v[1] = w[1]; v[2] = ~w[2];
+  } else if constexpr (FMT == LMX_FMT_INT4) {
+    v[0] = w[0]; v[1] = w[1]; v[2] = w[2]; v[3] = ~w[3];
+  } else {
+#pragma unroll
+    for (int p = 0; p < Fmt<FMT>::P; ++p) v[p] = w[p];
+  }
+}
+
+// Chunk sums -> row accumulator.
+template <int FMT>
+__device__ __forceinline__ float finish_chunk(const float *A, float xs, const float *sc, float acc) {
+  if constexpr (FMT == LMX_FMT_TERNARY) {
+    return fmaf(sc[0], A[0] - A[1], acc);
+  } else if constexpr (FMT == LMX_FMT_BINARY) {
+    return fmaf(sc[0], 2.0f * A[0] - xs, acc);
+  } else if constexpr (FMT == LMX_FMT_RRQ2 || FMT == LMX_FMT_RRQ3) {
+#pragma unroll
+    for (int i = 0; i < Fmt<FMT>::S; ++i) acc = fmaf(sc[i], 2.0f * A[i] - xs, acc);
+    return acc;
+  } else if constexpr (FMT == LMX_FMT_INT3) {
+    return fmaf(sc[0], (A[0] + 2.0f * A[1]) - 4.0f * A[2], acc);
+  } else if constexpr (FMT == LMX_FMT_INT4) {
+    return fmaf(sc[0], ((A[0] + 2.0f * A[1]) + 4.0f * A[2]) - 8.0f * A[3], acc);
+  } else {
+    float s = A[0];
+#pragma unroll
+    for (int b = 1; b < 7; ++b) s = fmaf(float(1 << b), A[b], s);
+    return fmaf(sc[0], fmaf(-128.0f, A[7], s), acc);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Register FWHT-256: lane l holds x[4l..4l+3] of one 256-chunk.  Strides 1
+// and 2 are in-lane, strides 4..128 pair lane l with lane l^(h/4).  Every
+// output is produced by the same sequence of (a+b, a-b) as the reference's
+// scalar stage loop (transform_simd.cpp:14-23,26-45) followed by x(1/16),
+// so the result is bit-identical.
+__device__ __forceinline__ void fwht256_regs(float &x0, float &x1, float &x2, float &x3, int lane) {
+  float a0 = x0 + x1, a1 = x0 - x1, a2 = x2 + x3, a3 = x2 - x3;   // h = 1
+  x0 = a0 + a2; x2 = a0 - a2; x1 = a1 + a3; x3 = a1 - a3;          // h = 2
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {                               // h = 4d
+    const bool top = (lane & d) == 0;
+    float p0 = __shfl_xor(x0, d, 64), p1 = __shfl_xor(x1, d, 64);
+    float p2 = __shfl_xor(x2, d, 64), p3 = __shfl_xor(x3, d, 64);
+    x0 = top ? x0 + p0 : p0 - x0;
+    x1 = top ? x1 + p1 : p1 - x1;
+    x2 = top ? x2 + p2 : p2 - x2;
+    x3 = top ? x3 + p3 : p3 - x3;
+  }
+  x0 *= 0.0625f; x1 *= 0.0625f; x2 *= 0.0625f; x3 *= 0.0625f;
+}
+
+// 16 partial sums of (a0,a1,a2,a3), entry m adding a_j for set bit (3-j) in
+// the order a0,a1,a2,a3 from +0 (lut_gemm.hpp:30-44): bit-identical entries.
+__device__ __forceinline__ void group_table(float a0, float a1, float a2, float a3, float *t) {
+  const float s01 = a0 + a1, s02 = a0 + a2, s12 = a1 + a2, s23 = a2 + a3;
+  const float s012 = s01 + a2;
+  t[0] = 0.0f;   t[1] = a3;          t[2] = a2;          t[3] = s23;
+  t[4] = a1;     t[5] = a1 + a3;     t[6] = s12;         t[7] = s12 + a3;
+  t[8] = a0;     t[9] = a0 + a3;     t[10] = s02;        t[11] = s02 + a3;
+  t[12] = s01;   t[13] = s01 + a3;   t[14] = s012;       t[15] = s012 + a3;
+}
+
+// Loads the lane's 4 activations of a 256-chunk starting at k0 (zero past
+// cols), optionally rotated.
+__device__ __forceinline__ void load_x4(const float *__restrict__ x, int k0, int cols, int lane,
+                                        unsigned rotate, float &x0, float &x1, float &x2, float &x3) {
+  const int k = k0 + 4 * lane;
+  if (k + 3 < cols && (cols & 3) == 0 && ((size_t)x & 15) == 0) {
+    const float4 v = *reinterpret_cast<const float4 *>(x + k);
+    x0 = v.x; x1 = v.y; x2 = v.z; x3 = v.w;
+  } else {
+    x0 = k < cols ? x[k] : 0.0f;
+    x1 = k + 1 < cols ? x[k + 1] : 0.0f;
+    x2 = k + 2 < cols ? x[k + 2] : 0.0f;
+    x3 = k + 3 < cols ? x[k + 3] : 0.0f;
+  }
+  if (rotate == LMX_ROTATE_FWHT256) fwht256_regs(x0, x1, x2, x3, lane);
+}
+
+// ---------------------------------------------------------------------------
+template <int FMT, int CHUNKS>
+__global__ __launch_bounds__(kRowsPerGroup) void lut_gemv_kernel(GemvArgs a, int row_blocks, int splits) {
+  constexpr int P = Fmt<FMT>::P, NA = Fmt<FMT>::NA, S = Fmt<FMT>::S;
+  constexpr int KS = CHUNKS * kChunk;
+  __shared__ __attribute__((aligned(256))) float tables[KS / 4 * 16];
+  __shared__ float xsum[CHUNKS];
+  __shared__ unsigned ticket;
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int rb = blockIdx.x % row_blocks;
+  const int split = blockIdx.x / row_blocks;
+  const int k0 = split * KS;
+
+  // ---- prologue: x slice -> (FWHT) -> 16-entry tables in LDS -------------
+  for (int c2 = wave; c2 < KS / kRotChunk; c2 += kWavesPerGroup) {
+    float x0, x1, x2, x3;
+    load_x4(a.x, k0 + c2 * kRotChunk, a.cols, lane, a.rotate, x0, x1, x2, x3);
+    float t[16];
+    group_table(x0, x1, x2, x3, t);
+    float4 *dst = reinterpret_cast<float4 *>(tables + (c2 * 64 + lane) * 16);
+    dst[0] = make_float4(t[0], t[1], t[2], t[3]);
+    dst[1] = make_float4(t[4], t[5], t[6], t[7]);
+    dst[2] = make_float4(t[8], t[9], t[10], t[11]);
+    dst[3] = make_float4(t[12], t[13], t[14], t[15]);
+    if constexpr (Fmt<FMT>::XS) {
+      float s = t[15];
+#pragma unroll
+      for (int d = 16; d >= 1; d >>= 1) s += __shfl_xor(s, d, 64);
+      if ((lane & 31) == 0) xsum[c2 * 2 + (lane >> 5)] = s;
+    }
+  }
+  __syncthreads();
+
+  // ---- main loop: one row per lane --------------------------------------
+  const int row = rb * kRowsPerGroup + wave * kWave + lane;
+  const bool active = rb * kRowsPerGroup + wave * kWave < a.Npad;
+  float acc = 0.0f;
+  if (active) {
+    const u32x4 *__restrict__ pl = reinterpret_cast<const u32x4 *>(a.planes);
+    const size_t Npad = size_t(a.Npad);
+    const int c0 = k0 / kChunk;
+    u32x4 w[CHUNKS][P];
+    float sc[CHUNKS][S];
+#pragma unroll
+    for (int c = 0; c < CHUNKS; ++c) {
+#pragma unroll
+      for (int p = 0; p < P; ++p)
+        w[c][p] = __builtin_nontemporal_load(pl + (size_t(c0 + c) * P + p) * Npad + row);
+      const int g = (c0 + c) / a.group_chunks;
+#pragma unroll
+      for (int s = 0; s < S; ++s) sc[c][s] = a.scales[(size_t(s) * a.n_groups + g) * Npad + row];
+    }
+    const uint32_t tbase = lds_addr(tables);
+#pragma unroll
+    for (int c = 0; c < CHUNKS; ++c) {
+      float A[NA];
+#pragma unroll
+      for (int i = 0; i < NA; ++i) A[i] = 0.0f;
+      const uint32_t cbase = tbase + c * (32 * 64);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        uint32_t wi[P], v[NA];
+#pragma unroll
+        for (int p = 0; p < P; ++p)
+          wi[p] = w[c][p][i];
+        lookup_words<FMT>(wi, v);
+#pragma unroll
+        for (int q = 0; q < NA; ++q) {
+          const uint32_t hi = (v[q] >> 2) & 0x3C3C3C3Cu;  // byte b: 4*nibble of group 8i+2b
+          const uint32_t lo = (v[q] << 2) & 0x3C3C3C3Cu;  // byte b: 4*nibble of group 8i+2b+1
+          float t[8];
+#pragma unroll
+          for (int b = 0; b < 4; ++b) {
+            const uint32_t ah = __builtin_amdgcn_perm(cbase, hi, 0x0C060500u | b);
+            const uint32_t al = __builtin_amdgcn_perm(cbase, lo, 0x0C060500u | b);
+            t[2 * b] = lds_load(ah + (8 * i + 2 * b) * 64);
+            t[2 * b + 1] = lds_load(al + (8 * i + 2 * b + 1) * 64);
+          }
+          A[q] += ((t[0] + t[1]) + (t[2] + t[3])) + ((t[4] + t[5]) + (t[6] + t[7]));
+        }
+      }
+      float xs = 0.0f;
+      if constexpr (Fmt<FMT>::XS) xs = xsum[c];
+      acc = finish_chunk<FMT>(A, xs, sc[c], acc);
+    }
+  }
+
+  // ---- split-K reduction --------------------------------------------------
+  if (splits == 1) {
+    if (active && row < a.rows) a.y[row] = a.bias ? acc + a.bias[row] : acc;
+    return;
+  }
+  if (active) a.partials[size_t(split) * a.Npad + row] = acc;
+  __threadfence();
+  __syncthreads();
+  if (threadIdx.x == 0) ticket = atomicAdd(a.counters + rb, 1u);
+  __syncthreads();
+  if (ticket != unsigned(splits - 1)) return;
+  __threadfence();
+  const int r = rb * kRowsPerGroup + threadIdx.x;
+  if (r < a.rows) {
+    float s = 0.0f;
+    for (int k = 0; k < splits; ++k) s += __builtin_nontemporal_load(a.partials + size_t(k) * a.Npad + r);
+    a.y[r] = a.bias ? s + a.bias[r] : s;
+  }
+  if (threadIdx.x == 0) a.counters[rb] = 0u;
+}
+
+template <int FMT>
+static int launch_fmt(const GemvArgs &a, hipStream_t st) {
+  const int row_blocks = (a.Npad + kRowsPerGroup - 1) / kRowsPerGroup;
+  const int splits = a.Kp / a.kslice;
+  dim3 grid(row_blocks * splits), block(kRowsPerGroup);
+  switch (a.kslice) {
+  case 256: lut_gemv_kernel<FMT, 2><<<grid, block, 0, st>>>(a, row_blocks, splits); break;
+  case 512: lut_gemv_kernel<FMT, 4><<<grid, block, 0, st>>>(a, row_blocks, splits); break;
+  case 1024:
+    if constexpr (Fmt<FMT>::P <= 4) {
+      lut_gemv_kernel<FMT, 8><<<grid, block, 0, st>>>(a, row_blocks, splits);
+      break;
+    }
+    return fail(LMX_ERR_INVALID_ARGUMENT, "k-slice 1024 not built for format %d", FMT);
+  default:
+    return fail(LMX_ERR_INVALID_ARGUMENT, "unsupported k-slice %d", a.kslice);
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(LMX_ERR_LAUNCH_FAILED, "lut_gemv launch: %s", hipGetErrorString(e));
+  return LMX_OK;
+}
+
+int launch_gemv(int fmt, const GemvArgs &a, void *stream) {
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (fmt) {
+  case LMX_FMT_TERNARY: return launch_fmt<LMX_FMT_TERNARY>(a, st);
+  case LMX_FMT_BINARY: return launch_fmt<LMX_FMT_BINARY>(a, st);
+  case LMX_FMT_RRQ2: return launch_fmt<LMX_FMT_RRQ2>(a, st);
+  case LMX_FMT_RRQ3: return launch_fmt<LMX_FMT_RRQ3>(a, st);
+  case LMX_FMT_INT3: return launch_fmt<LMX_FMT_INT3>(a, st);
+  case LMX_FMT_INT4: return launch_fmt<LMX_FMT_INT4>(a, st);
+  case LMX_FMT_INT8: return launch_fmt<LMX_FMT_INT8>(a, st);
+  }
+  return fail(LMX_ERR_UNSUPPORTED_FORMAT, "unknown format %d", fmt);
+}
+
+// ---------------------------------------------------------------------------
+// Standalone FWHT-256 (apply_hadamard_rotation): one wavefront per chunk.
+__global__ __launch_bounds__(256) void fwht256_kernel(float *x, size_t n_chunks) {
+  const size_t c = size_t(blockIdx.x) * 4 + threadIdx.x / kWave;
+  const int lane = threadIdx.x & (kWave - 1);
+  if (c >= n_chunks) return;
+  float4 *p = reinterpret_cast<float4 *>(x + c * kRotChunk) + lane;
+  float4 v = *p;
+  fwht256_regs(v.x, v.y, v.z, v.w, lane);
+  *p = v;
+}
+
+int launch_fwht256(float *x, size_t n, void *stream) {
+  const size_t chunks = n / kRotChunk;
+  if (chunks == 0) return LMX_OK;
+  fwht256_kernel<<<dim3((chunks + 3) / 4), dim3(256), 0, static_cast<hipStream_t>(stream)>>>(x, chunks);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(LMX_ERR_LAUNCH_FAILED, "fwht256 launch: %s", hipGetErrorString(e));
+  return LMX_OK;
+}
+
+// Length-n orthonormal FWHT (n a power of two, 256 <= n <= 16384) in one
+// workgroup through LDS: out = H_n x / sqrt(n).
+__global__ __launch_bounds__(1024) void fwht_full_kernel(const float *x, float *out, int n, float scale) {
+  __shared__ float buf[16384];
+  for (int i = threadIdx.x; i < n; i += blockDim.x) buf[i] = x[i];
+  __syncthreads();
+  for (int h = 1; h < n; h <<= 1) {
+    for (int t = threadIdx.x; t < n / 2; t += blockDim.x) {
+      const int j = (t / h) * 2 * h + (t % h);
+      const float u = buf[j], v = buf[j + h];
+      buf[j] = u + v;
+      buf[j + h] = u - v;
+    }
+    __syncthreads();
+  }
+  for (int i = threadIdx.x; i < n; i += blockDim.x) out[i] = buf[i] * scale;
+}
+
+int launch_fwht_full(const float *x, float *out, size_t n, void *stream) {
+  fwht_full_kernel<<<dim3(1), dim3(1024), 0, static_cast<hipStream_t>(stream)>>>(
+      x, out, int(n), float(1.0 / __builtin_sqrt(double(n))));
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(LMX_ERR_LAUNCH_FAILED, "fwht_full launch: %s", hipGetErrorString(e));
+  return LMX_OK;
+}
+
+// ---------------------------------------------------------------------------
+// precompute_luts on the device with the GEMV's own table code.
+__global__ __launch_bounds__(256) void luts_kernel(const float *x, size_t n, unsigned rotate, float *luts) {
+  const size_t c = size_t(blockIdx.x) * 4 + threadIdx.x / kWave;  // 256-chunk
+  const int lane = threadIdx.x & (kWave - 1);
+  if (c * kRotChunk >= n) return;
+  float x0, x1, x2, x3;
+  const size_t k = c * kRotChunk + 4 * lane;
+  if (rotate == LMX_ROTATE_FWHT256) {
+    load_x4(x, int(c * kRotChunk), int(n), lane, rotate, x0, x1, x2, x3);
+  } else {
+    if (k + 3 >= n) return;  // whole groups only, as precompute_luts
+    x0 = x[k]; x1 = x[k + 1]; x2 = x[k + 2]; x3 = x[k + 3];
+  }
+  if (k + 3 >= n) return;
+  float t[16];
+  group_table(x0, x1, x2, x3, t);
+  float *dst = luts + (k / 4) * 16;
+#pragma unroll
+  for (int m = 0; m < 16; ++m) dst[m] = t[m];
+}
+
+int launch_precompute_luts(const float *x, size_t n, unsigned flags, float *luts, void *stream) {
+  const size_t chunks = (n + kRotChunk - 1) / kRotChunk;
+  if (chunks == 0) return LMX_OK;
+  luts_kernel<<<dim3((chunks + 3) / 4), dim3(256), 0, static_cast<hipStream_t>(stream)>>>(x, n, flags, luts);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(LMX_ERR_LAUNCH_FAILED, "precompute_luts launch: %s", hipGetErrorString(e));
+  return LMX_OK;
+}
+
+// ---------------------------------------------------------------------------
+// extract_indices on the device, with the same lookup-word and nibble
+// arithmetic the ternary GEMV uses (32-bit little-endian words of canonical
+// plane bytes; group 2j in the high nibble of byte j).
+__global__ __launch_bounds__(256) void indices_kernel(const uint8_t *s, const uint8_t *z, size_t n_groups,
+                                                      uint8_t *pos, uint8_t *neg) {
+  const size_t g = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (g >= n_groups) return;
+  const uint32_t w[2] = {uint32_t(s[g / 2]), uint32_t(z[g / 2])};
+  uint32_t v[2];
+  lookup_words<LMX_FMT_TERNARY>(w, v);
+  const uint32_t sh = (g & 1) ? 0u : 4u;
+  pos[g] = uint8_t((v[0] >> sh) & 15u);
+  neg[g] = uint8_t((v[1] >> sh) & 15u);
+}
+
+int launch_extract_indices(const uint8_t *s, const uint8_t *z, size_t n_groups, uint8_t *pos, uint8_t *neg,
+                           void *stream) {
+  if (n_groups == 0) return LMX_OK;
+  indices_kernel<<<dim3((n_groups + 255) / 256), dim3(256), 0, static_cast<hipStream_t>(stream)>>>(
+      s, z, n_groups, pos, neg);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(LMX_ERR_LAUNCH_FAILED, "extract_indices launch: %s", hipGetErrorString(e));
+  return LMX_OK;
+}
+
+}  // namespace lmx

@@ -1,0 +1,203 @@
+"""GPU parity of the HIP LUT-GEMV path against the CPU oracle and the
+reference's golden vectors, through the C ABI.
+
+Bars (north star): bit-exact for plane packing, table build, FWHT-256 and
+index generation; outputs within max |y - y_ref| <= 1e-5 * ||y_ref||_2
+(fp32 accumulation-order differences only).
+"""
+import numpy as np
+import pytest
+import torch
+
+import lutmac_amd as L
+import oracle
+from conftest import TOL, load_golden, rel_max_err
+from lutmac_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+FORMAT_FILES = {1: "ternary", 2: "binary", 3: "int2", 5: "int3", 6: "int4", 7: "int8"}
+ZERO_CODE_PLANE = {1: 1, 5: 2, 6: 3}
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def oracle_planes_gemv(fmt, planes, scales, rows, cols, group, x, rotate):
+    """Oracle over the same padded weight the device holds (pad codes in the
+    columns past `cols`, zero scales for groups past the source's)."""
+    Kp = -(-cols // 256) * 256
+    P, S = L.PLANES[fmt], L.STAGES[fmt]
+    padded = np.zeros((P, rows, Kp // 8), np.uint8)
+    if fmt in ZERO_CODE_PLANE:
+        padded[ZERO_CODE_PLANE[fmt]] = 0xFF
+    padded[:, :, :cols // 8] = planes.reshape(P, rows, cols // 8)
+    G = group or Kp
+    ng = Kp // G
+    sc = np.zeros((S, rows, ng), np.float32)
+    src = scales.reshape(S, rows, -1)
+    sc[:, :, :src.shape[2]] = src[:, :, :ng]
+    xp = np.zeros(Kp, np.float32)
+    xp[:cols] = x
+    if rotate == L.ROTATE_FWHT256:
+        xp = oracle.fwht256(xp)
+    elif rotate == L.ROTATE_FWHT_FULL:
+        xp = oracle.fwht_full(xp)
+    return oracle.planes_gemv(fmt, padded, sc, rows, Kp, G, xp)
+
+
+# ---- bit-exact primitives -----------------------------------------------------
+
+def test_fwht256_bitexact(cuda):
+    g = load_golden("tables_fwht.npz")
+    x = dev(g["x"])
+    L.fwht256(x)
+    torch.cuda.synchronize()
+    assert np.array_equal(x.cpu().numpy().view(np.uint32), g["x_rot"].view(np.uint32))
+    big = synth.make_activations(8192 * 4, seed=1)
+    xb = dev(big)
+    L.fwht256(xb)
+    assert np.array_equal(xb.cpu().numpy().view(np.uint32), oracle.fwht256(big).view(np.uint32))
+
+
+def test_precompute_luts_bitexact(cuda):
+    g = load_golden("tables_fwht.npz")
+    t = L.precompute_luts(dev(g["x"]))
+    assert np.array_equal(t.cpu().numpy().view(np.uint32), g["luts"].view(np.uint32))
+    t = L.precompute_luts(dev(g["x"]), rotate=True)   # the GEMV's fused FWHT + table path
+    assert np.array_equal(t.cpu().numpy().view(np.uint32), g["luts_rot"].view(np.uint32))
+    x = synth.make_activations(8192, seed=2, outliers=True)
+    t = L.precompute_luts(dev(x), rotate=True)
+    assert np.array_equal(t.cpu().numpy().view(np.uint32),
+                          oracle.precompute_luts(oracle.fwht256(x)).view(np.uint32))
+    x = np.array([1, 2, 3, 4, 5, 6], np.float32)     # ragged: whole groups only
+    t = L.precompute_luts(dev(x))
+    assert t.cpu().numpy().tolist() == [0, 4, 3, 7, 2, 6, 5, 9, 1, 5, 4, 8, 3, 7, 6, 10]
+
+
+def test_extract_indices_bitexact(cuda):
+    g = load_golden("indices.npz")
+    pos, neg = L.extract_indices(dev(g["sign"]), dev(g["zero"]), 256)
+    assert np.array_equal(pos.cpu().numpy(), g["pos"])
+    assert np.array_equal(neg.cpu().numpy(), g["neg"])
+    s = np.array([0b01000000, 0], np.uint8)
+    z = np.array([0b00100000, 0], np.uint8)
+    pos, neg = L.extract_indices(dev(s), dev(z), 1)
+    assert (int(pos[0]), int(neg[0])) == (0b1001, 0b0100)     # test_lut_gemm.cpp:57-88
+
+
+@pytest.mark.parametrize("fmt", sorted(FORMAT_FILES))
+def test_device_tiles_bitexact(cuda, fmt):
+    g = load_golden(f"blocks_{FORMAT_FILES[fmt]}.npz")
+    M, K = int(g["M"]), int(g["K"])
+    w = L.Weight.from_blocks(fmt, g["blocks"], M, K)
+    planes, _ = L.blocks_to_planes(fmt, g["blocks"], M, K)
+    Kp = -(-K // 256) * 256
+    assert np.array_equal(w.read_tiles(), L.tile_planes(fmt, planes, M, Kp))
+    assert np.array_equal(L.planes_to_blocks(fmt, L.untile_planes(fmt, w.read_tiles(), M, Kp),
+                                             L.blocks_to_planes(fmt, g["blocks"], M, K)[1], M, K),
+                          g["blocks"])
+
+
+# ---- GEMV parity ----------------------------------------------------------------
+
+@pytest.mark.parametrize("fmt", sorted(FORMAT_FILES))
+def test_linear_reference_blocks_golden(cuda, fmt):
+    """lut_linear on the reference's own quantized blocks (bias, batch 2)
+    against the reference's outputs."""
+    g = load_golden(f"blocks_{FORMAT_FILES[fmt]}.npz")
+    M, K = int(g["M"]), int(g["K"])
+    w = L.Weight.from_blocks(fmt, g["blocks"], M, K)
+    y = w.linear(dev(g["x"]), bias=dev(g["bias"])).cpu().numpy()
+    for b in range(2):
+        assert rel_max_err(y[b * M:(b + 1) * M], g["y"][b * M:(b + 1) * M]) < TOL
+    y0 = w.linear(dev(g["x"])).cpu().numpy()
+    assert rel_max_err(y0[:M], g["y_nobias"][:M]) < TOL
+
+
+@pytest.mark.parametrize("fmt", [1, 2, 3, 4, 5, 6, 7])
+@pytest.mark.parametrize("group", [0, 128, 256])
+@pytest.mark.parametrize("rows,cols", [(300, 640), (64, 2048), (1, 8), (513, 1536)])
+@pytest.mark.parametrize("rotate", [L.ROTATE_NONE, L.ROTATE_FWHT256])
+def test_gemv_formats(cuda, fmt, group, rows, cols, rotate):
+    planes, scales, _ = synth.make_weights(fmt, rows, cols, seed=rows + cols + fmt, group=group or 128)
+    if group == 0:
+        scales = np.ascontiguousarray(scales[:, :, :1])
+    x = synth.make_activations(cols, seed=cols, outliers=True)
+    w = L.Weight.from_planes(fmt, planes, scales, rows, cols, group)
+    y = w.gemv(dev(x), flags=rotate).cpu().numpy()
+    ref = oracle_planes_gemv(fmt, planes, scales, rows, cols, group, x, rotate)
+    assert rel_max_err(y, ref) < TOL
+
+
+def test_config1_int4_2048(cuda):
+    planes, scales, g = synth.make_weights(L.FMT_INT4, 2048, 2048, seed=1)
+    x = synth.make_activations(2048, seed=101)
+    w = L.Weight.from_planes(L.FMT_INT4, planes, scales, 2048, 2048, g)
+    y = w.gemv(dev(x)).cpu().numpy()
+    assert rel_max_err(y, oracle.planes_gemv(6, planes, scales, 2048, 2048, g, x)) < TOL
+    W = synth.dequant_f64(6, planes, scales, 2048, 2048, g)
+    assert rel_max_err(y, W @ x.astype(np.float64)) < TOL
+
+
+@pytest.mark.parametrize("name", sorted(synth.LLAMA_TERNARY_SHAPES))
+@pytest.mark.parametrize("rotate", [L.ROTATE_FWHT256, L.ROTATE_FWHT_FULL])
+def test_config2_ternary_shapes(cuda, name, rotate):
+    rows, cols = synth.LLAMA_TERNARY_SHAPES[name]
+    planes, scales, g = synth.make_weights(L.FMT_TERNARY, rows, cols, seed=rows * 7 + cols, group=0)
+    x = synth.make_activations(cols, seed=cols + 5, outliers=True)
+    w = L.Weight.from_planes(L.FMT_TERNARY, planes, scales, rows, cols, 0)
+    y = w.gemv(dev(x), flags=rotate).cpu().numpy()
+    assert rel_max_err(y, oracle_planes_gemv(1, planes, scales, rows, cols, 0, x, rotate)) < TOL
+
+
+@pytest.mark.parametrize("fmt", [L.FMT_BINARY, L.FMT_TERNARY, L.FMT_RRQ2, L.FMT_RRQ3, L.FMT_INT4, L.FMT_INT8])
+def test_config3_8192(cuda, fmt):
+    n = 8192
+    planes, scales, g = synth.make_weights(fmt, n, n, seed=30 + fmt, group=128)
+    x = synth.make_activations(n, seed=31)
+    w = L.Weight.from_planes(fmt, planes, scales, n, n, g)
+    xd = dev(x)
+    y = w.gemv(xd, flags=L.ROTATE_FWHT256).cpu().numpy()
+    assert rel_max_err(y, oracle.planes_gemv(fmt, planes, scales, n, n, g, oracle.fwht256(x))) < TOL
+    # size-independent properties at the full shape
+    y2 = w.gemv(xd, flags=L.ROTATE_FWHT256).cpu().numpy()
+    assert np.array_equal(y.view(np.uint32), y2.view(np.uint32))          # deterministic split-K
+    x2 = synth.make_activations(n, seed=32)
+    ya = w.gemv(dev(2.0 * x - 3.0 * x2), flags=L.ROTATE_FWHT256).cpu().numpy()
+    yb = w.gemv(dev(x2), flags=L.ROTATE_FWHT256).cpu().numpy()
+    assert rel_max_err(ya, 2.0 * y.astype(np.float64) - 3.0 * yb) < 1e-5 * 4  # linearity
+    assert not w.gemv(torch.zeros(n, device="cuda"), flags=L.ROTATE_FWHT256).any()
+
+
+def test_batch_rows_independent(cuda):
+    rows, cols, B = 700, 1024, 3
+    planes, scales, g = synth.make_weights(L.FMT_INT4, rows, cols, seed=77)
+    xs = np.stack([synth.make_activations(cols, seed=s) for s in range(B)])
+    w = L.Weight.from_planes(L.FMT_INT4, planes, scales, rows, cols, g)
+    y = w.gemv(dev(xs.ravel())).cpu().numpy().reshape(B, rows)
+    for b in range(B):
+        assert rel_max_err(y[b], oracle.planes_gemv(6, planes, scales, rows, cols, g, xs[b])) < TOL
+
+
+def test_qwen_ffn_shape(cuda):
+    # K = 8960 (35 x 256): the k-slice must divide the padded K.
+    rows, cols = 1536, 8960
+    planes, scales, g = synth.make_weights(L.FMT_INT4, rows, cols, seed=88)
+    x = synth.make_activations(cols, seed=89)
+    w = L.Weight.from_planes(L.FMT_INT4, planes, scales, rows, cols, g)
+    y = w.gemv(dev(x)).cpu().numpy()
+    assert rel_max_err(y, oracle.planes_gemv(6, planes, scales, rows, cols, g, x)) < TOL
+
+
+def test_gemv_rejects_bad_arguments(cuda):
+    planes, scales, g = synth.make_weights(L.FMT_INT4, 64, 256, seed=3)
+    w = L.Weight.from_planes(L.FMT_INT4, planes, scales, 64, 256, g)
+    x = torch.zeros(256, device="cuda")
+    with pytest.raises(L.LmxError) as e:
+        w.gemv(x, flags=7)
+    assert e.value.status == L.ERR_INVALID_ARGUMENT
+    w2 = L.Weight.from_planes(L.FMT_INT4, *synth.make_weights(L.FMT_INT4, 8, 768, seed=4)[:2], 8, 768, 128)
+    with pytest.raises(L.LmxError):
+        w2.gemv(torch.zeros(768, device="cuda"), flags=L.ROTATE_FWHT_FULL)   # 768 not a power of 2
