@@ -96,6 +96,27 @@ def cpu_baseline(n, budget_s=10.0):
             "ms_per_gemv": round(t * 1e3, 2)}
 
 
+def calibrate_copy(nbytes=35717120, steps=200):
+    """Plain device copy of a known size (torch's copy kernel), the yardstick
+    that scales rocprofv3's FETCH_SIZE / WRITE_SIZE counters to bytes."""
+    import torch
+    a = torch.empty(nbytes // 4, dtype=torch.float32, device="cuda").fill_(1.0)
+    b = torch.empty_like(a)
+    for _ in range(steps):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibrate_copy_bytes": nbytes, "steps": steps}), flush=True)
+
+
+def load_traffic(workload_key):
+    """HBM bytes per GEMV measured with rocprofv3 --pmc (profiles/traffic.json)."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f).get(workload_key, {}).get("bytes_per_gemv")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -105,7 +126,12 @@ def main():
     ap.add_argument("--formats", default="int4,ternary,binary,rrq2,rrq3,int8")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run a plain device copy of 35717120 bytes (counter calibration)")
     args = ap.parse_args()
+    if args.calibrate_copy:
+        calibrate_copy()
+        return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
               "(see DESIGN.md for how the GEMV would shard)", file=sys.stderr)
@@ -144,7 +170,8 @@ def main():
                    "group": head["group"], "batch": 1, "weight_copies": head["weight_copies"],
                    "rotated_MiB": head["rotated_MiB"]},
         "roofline": {"bound": "hbm", "achieved": head["GB_per_s"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": head["frac_of_peak"], "traffic": None},
+                     "frac": head["frac_of_peak"],
+                     "traffic": load_traffic(f"{head['format']}_{args.size}")},
         "cpu_baseline": cpu,
         "sweep": sweep,
     }

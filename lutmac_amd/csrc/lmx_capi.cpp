@@ -47,26 +47,29 @@ int require_device(int *dev) {
   return LMX_OK;
 }
 
-// Workgroups wanted in flight: several per CU so HBM requests overlap.
-constexpr int kTargetGroups = 1024;
+int env_int(const char *name, int dflt) {
+  const char *s = std::getenv(name);
+  return s ? std::atoi(s) : dflt;
+}
 
-int choose_kslice(int fmt, size_t Npad, size_t Kp) {
-  static const int env = [] {
-    const char *s = std::getenv("LMX_KSLICE");
-    return s ? std::atoi(s) : 0;
-  }();
-  FormatInfo fi;
-  format_info(fmt, &fi);
-  const size_t row_blocks = (Npad + kRowsPerGroup - 1) / kRowsPerGroup;
-  const int cand[3] = {1024, 512, 256};
-  if (env == 256 || env == 512 || (env == 1024 && fi.planes <= 4))
-    if (Kp % size_t(env) == 0) return env;
-  for (int ks : cand) {
-    if (ks == 1024 && fi.planes > 4) continue;
-    if (Kp % size_t(ks)) continue;
-    if (row_blocks * (Kp / size_t(ks)) >= size_t(kTargetGroups)) return ks;
-  }
+int choose_waves() {
+  static const int env = env_int("LMX_WAVES", 4);
+  return (env == 1 || env == 2 || env == 4) ? env : 4;
+}
+
+// k-slice per workgroup: 512 when the padded K allows it and the grid still
+// has at least 4 workgroups per CU, else 256.  LMX_KSLICE overrides.
+int choose_kslice(size_t Npad, size_t Kp, int waves) {
+  static const int env = env_int("LMX_KSLICE", 0);
+  if ((env == 256 || env == 512) && Kp % size_t(env) == 0) return env;
+  const size_t row_blocks = (Npad + kWave * waves - 1) / (kWave * waves);
+  if (Kp % 512 == 0 && row_blocks * (Kp / 512) >= 1024) return 512;
   return 256;
+}
+
+int choose_reduce() {
+  static const int env = env_int("LMX_REDUCE", kReduceTwoPass);
+  return (env == kReduceTicket || env == kReduceFenceAll) ? env : kReduceTwoPass;
 }
 
 void free_weight(lmx_weight *w) {
@@ -100,7 +103,9 @@ int upload(int fmt, size_t rows, size_t cols, size_t group, const uint8_t *plane
   w->n_groups = (w->Kp + w->group - 1) / w->group;
   w->tile_bytes = (w->Kp / kChunk) * fi.planes * w->Npad * 16;
   w->scale_bytes = size_t(fi.stages) * w->n_groups * w->Npad * sizeof(float);
-  w->kslice = choose_kslice(fmt, w->Npad, w->Kp);
+  w->waves = choose_waves();
+  w->kslice = choose_kslice(w->Npad, w->Kp, w->waves);
+  w->reduce = choose_reduce();
 
   std::vector<uint8_t> tiles;
   std::vector<float> sc;
@@ -117,7 +122,7 @@ int upload(int fmt, size_t rows, size_t cols, size_t group, const uint8_t *plane
       for (size_t g = 0; g < ng_src && g < w->n_groups; ++g)
         sc[(size_t(s) * w->n_groups + g) * w->Npad + r] = scales[(size_t(s) * rows + r) * ng_src + g];
 
-  const size_t row_blocks = (w->Npad + kRowsPerGroup - 1) / kRowsPerGroup;
+  const size_t row_blocks = w->Npad / kWave;  // enough counters for any waves-per-group choice
   const size_t max_splits = w->Kp / kRotChunk;
   hipError_t e;
   if ((e = hipMalloc(&w->d_planes, w->tile_bytes)) != hipSuccess ||
@@ -150,6 +155,18 @@ int check_weight(const lmx_weight *w) {
 }
 
 bool is_pow2(size_t n) { return n && !(n & (n - 1)); }
+
+// The GEMV kernel reads x with aligned float4 loads; an unaligned x or a
+// length that is not a multiple of 4 is first copied, zero-padded, into the
+// handle's staging buffer.
+int stage_if_needed(const lmx_weight *w, GemvArgs &a, void *stream) {
+  if (reinterpret_cast<size_t>(a.x) % 16 == 0 && w->cols % 4 == 0) return LMX_OK;
+  int st = launch_stage_x(a.x, w->cols, w->d_xrot, w->Kp, stream);
+  if (st) return st;
+  a.x = w->d_xrot;
+  a.cols = int(w->Kp);
+  return LMX_OK;
+}
 
 }  // namespace
 }  // namespace lmx
@@ -343,14 +360,19 @@ int lmx_gemv(const lmx_weight *w, const float *x, float *y, size_t batch, unsign
   a.group_chunks = int(w->group / kChunk);
   a.n_groups = int(w->n_groups);
   a.kslice = w->kslice;
+  a.reduce = w->reduce;
+  a.waves = w->waves;
   for (size_t b = 0; b < batch; ++b) {
     a.x = x + b * w->cols;
     a.y = y + b * w->rows;
+    a.cols = int(w->cols);
     a.rotate = flags == LMX_ROTATE_FWHT256 ? LMX_ROTATE_FWHT256 : LMX_ROTATE_NONE;
     if (flags == LMX_ROTATE_FWHT_FULL) {
       st = launch_fwht_full(a.x, w->d_xrot, w->cols, stream);
       if (st) return st;
       a.x = w->d_xrot;
+    } else if ((st = stage_if_needed(w, a, stream)) != LMX_OK) {
+      return st;
     }
     st = launch_gemv(w->format, a, stream);
     if (st) return st;
@@ -378,10 +400,14 @@ int lmx_linear(const lmx_weight *w, const float *bias, const float *x, float *y,
   a.group_chunks = int(w->group / kChunk);
   a.n_groups = int(w->n_groups);
   a.kslice = w->kslice;
+  a.reduce = w->reduce;
+  a.waves = w->waves;
   a.rotate = rotate ? LMX_ROTATE_FWHT256 : LMX_ROTATE_NONE;
   for (size_t b = 0; b < batch; ++b) {
     a.x = x + b * w->cols;
     a.y = y + b * w->rows;
+    a.cols = int(w->cols);
+    if ((st = stage_if_needed(w, a, stream)) != LMX_OK) return st;
     st = launch_gemv(w->format, a, stream);
     if (st) return st;
   }

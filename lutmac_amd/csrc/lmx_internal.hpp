@@ -13,8 +13,6 @@ namespace lmx {
 constexpr int kChunk = 128;        // k per chunk: one uint4 per plane per row
 constexpr int kRotChunk = 256;     // FWHT-256 block and device K padding
 constexpr int kWave = 64;          // lanes per wavefront (one row per lane)
-constexpr int kWavesPerGroup = 4;  // wavefronts per workgroup
-constexpr int kRowsPerGroup = kWave * kWavesPerGroup;
 
 inline size_t round_up(size_t v, size_t m) { return (v + m - 1) / m * m; }
 
@@ -57,10 +55,18 @@ struct GemvArgs {
   int n_groups;
   int kslice;              // k per workgroup (multiple of 256, divides Kp)
   unsigned rotate;         // LMX_ROTATE_NONE / LMX_ROTATE_FWHT256
+  int reduce;              // split-K reduction strategy (kReduce*)
+  int waves;               // wavefronts (64-row slabs) per workgroup: 1, 2 or 4
 };
+
+// Split-K reduction strategies.
+constexpr int kReduceTicket = 0;    // last workgroup of a row block sums (one release per group)
+constexpr int kReduceFenceAll = 1;  // same, with a device fence in every thread
+constexpr int kReduceTwoPass = 2;   // partials, then a separate reduce kernel
 
 int launch_gemv(int fmt, const GemvArgs &a, void *stream);
 int launch_fwht256(float *x, size_t n, void *stream);
+int launch_stage_x(const float *x, size_t n, float *out, size_t n_pad, void *stream);
 int launch_fwht_full(const float *x, float *out, size_t n, void *stream);
 int launch_precompute_luts(const float *x, size_t n, unsigned flags,
                            float *luts, void *stream);
@@ -80,6 +86,8 @@ struct lmx_weight {
   size_t tile_bytes = 0;
   size_t scale_bytes = 0;
   int kslice = 0;          // chosen k-slice per workgroup
+  int reduce = 0;          // split-K reduction strategy
+  int waves = 4;           // wavefronts per workgroup
   void *d_planes = nullptr;
   float *d_scales = nullptr;
   float *d_partials = nullptr;

@@ -125,29 +125,29 @@ __device__ __forceinline__ void group_table(float a0, float a1, float a2, float 
   t[12] = s01;   t[13] = s01 + a3;   t[14] = s012;       t[15] = s012 + a3;
 }
 
-// Loads the lane's 4 activations of a 256-chunk starting at k0 (zero past
-// cols), optionally rotated.
+// Loads the lane's 4 activations of a 256-chunk starting at k0, zero past
+// cols.  The caller guarantees x is 16-byte aligned and cols % 4 == 0 (the
+// host stages x otherwise), so this is one clamped float4 load and a select:
+// no branch, which keeps the wait for x separate from the weight stream.
 __device__ __forceinline__ void load_x4(const float *__restrict__ x, int k0, int cols, int lane,
-                                        unsigned rotate, float &x0, float &x1, float &x2, float &x3) {
+                                        float &x0, float &x1, float &x2, float &x3) {
   const int k = k0 + 4 * lane;
-  if (k + 3 < cols && (cols & 3) == 0 && ((size_t)x & 15) == 0) {
-    const float4 v = *reinterpret_cast<const float4 *>(x + k);
-    x0 = v.x; x1 = v.y; x2 = v.z; x3 = v.w;
-  } else {
-    x0 = k < cols ? x[k] : 0.0f;
-    x1 = k + 1 < cols ? x[k + 1] : 0.0f;
-    x2 = k + 2 < cols ? x[k + 2] : 0.0f;
-    x3 = k + 3 < cols ? x[k + 3] : 0.0f;
-  }
-  if (rotate == LMX_ROTATE_FWHT256) fwht256_regs(x0, x1, x2, x3, lane);
+  const float4 v = *reinterpret_cast<const float4 *>(x + min(k, cols - 4));
+  const bool in = k < cols;
+  x0 = in ? v.x : 0.0f;
+  x1 = in ? v.y : 0.0f;
+  x2 = in ? v.z : 0.0f;
+  x3 = in ? v.w : 0.0f;
 }
 
 // ---------------------------------------------------------------------------
-template <int FMT, int CHUNKS>
-__global__ __launch_bounds__(kRowsPerGroup) void lut_gemv_kernel(GemvArgs a, int row_blocks, int splits) {
+template <int FMT, int CHUNKS, int WAVES>
+__global__ __launch_bounds__(WAVES * kWave) void lut_gemv_kernel(GemvArgs a, int row_blocks, int splits) {
   constexpr int P = Fmt<FMT>::P, NA = Fmt<FMT>::NA, S = Fmt<FMT>::S;
   constexpr int KS = CHUNKS * kChunk;
-  __shared__ __attribute__((aligned(256))) float tables[KS / 4 * 16];
+  constexpr int ROWS = WAVES * kWave;
+  constexpr int C2 = KS / kRotChunk;  // 256-chunks of the slice
+  __shared__ __attribute__((aligned(16))) float tables[KS / 4 * 16];
   __shared__ float xsum[CHUNKS];
   __shared__ unsigned ticket;
 
@@ -156,11 +156,48 @@ __global__ __launch_bounds__(kRowsPerGroup) void lut_gemv_kernel(GemvArgs a, int
   const int rb = blockIdx.x % row_blocks;
   const int split = blockIdx.x / row_blocks;
   const int k0 = split * KS;
+  const int row = rb * ROWS + wave * kWave + lane;
+  const bool active = rb * ROWS + wave * kWave < a.Npad;  // whole wavefronts
 
-  // ---- prologue: x slice -> (FWHT) -> 16-entry tables in LDS -------------
-  for (int c2 = wave; c2 < KS / kRotChunk; c2 += kWavesPerGroup) {
-    float x0, x1, x2, x3;
-    load_x4(a.x, k0 + c2 * kRotChunk, a.cols, lane, a.rotate, x0, x1, x2, x3);
+  // ---- loads: this wave's activations first, then the lane's plane and
+  // scale words, so the table build below only waits for x while the weight
+  // stream is still in flight (vector loads retire in issue order).  Loads
+  // are unconditional (indices clamped in bounds) so no branch splits them.
+  constexpr int XJ = (C2 + WAVES - 1) / WAVES;
+  float xv[XJ][4];
+#pragma unroll
+  for (int j = 0; j < XJ; ++j) {
+    const int c2 = min(wave + j * WAVES, C2 - 1);
+    load_x4(a.x, k0 + c2 * kRotChunk, a.cols, lane, xv[j][0], xv[j][1], xv[j][2], xv[j][3]);
+  }
+  __builtin_amdgcn_sched_barrier(0);  // keep the x loads ahead of the weight stream
+  u32x4 w[CHUNKS][P];
+  float sc[CHUNKS][S];
+  {
+    const u32x4 *__restrict__ pl = reinterpret_cast<const u32x4 *>(a.planes);
+    const size_t Npad = size_t(a.Npad);
+    const int c0 = k0 / kChunk;
+    const int lr = min(row, a.Npad - 1);
+#pragma unroll
+    for (int c = 0; c < CHUNKS; ++c) {
+#pragma unroll
+      for (int p = 0; p < P; ++p)
+        w[c][p] = __builtin_nontemporal_load(pl + (size_t(c0 + c) * P + p) * Npad + lr);
+      const int g = (c0 + c) / a.group_chunks;
+#pragma unroll
+      for (int s = 0; s < S; ++s) sc[c][s] = a.scales[(size_t(s) * a.n_groups + g) * Npad + lr];
+    }
+  }
+
+  // ---- prologue: (FWHT-256) -> 16-entry group tables in LDS --------------
+  // Lane l of the wave owning a 256-chunk holds activations 4l..4l+3 = group
+  // l of the chunk and writes that group's table.
+#pragma unroll
+  for (int j = 0; j < XJ; ++j) {
+    const int c2 = wave + j * WAVES;
+    if (c2 >= C2) break;   // wave-uniform
+    float x0 = xv[j][0], x1 = xv[j][1], x2 = xv[j][2], x3 = xv[j][3];
+    if (a.rotate == LMX_ROTATE_FWHT256) fwht256_regs(x0, x1, x2, x3, lane);
     float t[16];
     group_table(x0, x1, x2, x3, t);
     float4 *dst = reinterpret_cast<float4 *>(tables + (c2 * 64 + lane) * 16);
@@ -177,25 +214,13 @@ __global__ __launch_bounds__(kRowsPerGroup) void lut_gemv_kernel(GemvArgs a, int
   }
   __syncthreads();
 
-  // ---- main loop: one row per lane --------------------------------------
-  const int row = rb * kRowsPerGroup + wave * kWave + lane;
-  const bool active = rb * kRowsPerGroup + wave * kWave < a.Npad;
+  // ---- lookups: one row per lane ------------------------------------------
+  // All 64 lanes read the same 16-entry table at a time: 16 consecutive
+  // dwords, no bank conflicts.  v_perm turns a byte of the pre-shifted plane
+  // word into the table offset 4*nibble; the group's table offset is an
+  // immediate of the ds_read.
   float acc = 0.0f;
   if (active) {
-    const u32x4 *__restrict__ pl = reinterpret_cast<const u32x4 *>(a.planes);
-    const size_t Npad = size_t(a.Npad);
-    const int c0 = k0 / kChunk;
-    u32x4 w[CHUNKS][P];
-    float sc[CHUNKS][S];
-#pragma unroll
-    for (int c = 0; c < CHUNKS; ++c) {
-#pragma unroll
-      for (int p = 0; p < P; ++p)
-        w[c][p] = __builtin_nontemporal_load(pl + (size_t(c0 + c) * P + p) * Npad + row);
-      const int g = (c0 + c) / a.group_chunks;
-#pragma unroll
-      for (int s = 0; s < S; ++s) sc[c][s] = a.scales[(size_t(s) * a.n_groups + g) * Npad + row];
-    }
     const uint32_t tbase = lds_addr(tables);
 #pragma unroll
     for (int c = 0; c < CHUNKS; ++c) {
@@ -207,8 +232,7 @@ __global__ __launch_bounds__(kRowsPerGroup) void lut_gemv_kernel(GemvArgs a, int
       for (int i = 0; i < 4; ++i) {
         uint32_t wi[P], v[NA];
 #pragma unroll
-        for (int p = 0; p < P; ++p)
-          wi[p] = w[c][p][i];
+        for (int p = 0; p < P; ++p) wi[p] = w[c][p][i];
         lookup_words<FMT>(wi, v);
 #pragma unroll
         for (int q = 0; q < NA; ++q) {
@@ -217,6 +241,7 @@ __global__ __launch_bounds__(kRowsPerGroup) void lut_gemv_kernel(GemvArgs a, int
           float t[8];
 #pragma unroll
           for (int b = 0; b < 4; ++b) {
+            // v_perm: address = table base (bytes 1,2) | 4*nibble (byte 0)
             const uint32_t ah = __builtin_amdgcn_perm(cbase, hi, 0x0C060500u | b);
             const uint32_t al = __builtin_amdgcn_perm(cbase, lo, 0x0C060500u | b);
             t[2 * b] = lds_load(ah + (8 * i + 2 * b) * 64);
@@ -236,39 +261,100 @@ __global__ __launch_bounds__(kRowsPerGroup) void lut_gemv_kernel(GemvArgs a, int
     if (active && row < a.rows) a.y[row] = a.bias ? acc + a.bias[row] : acc;
     return;
   }
-  if (active) a.partials[size_t(split) * a.Npad + row] = acc;
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) ticket = atomicAdd(a.counters + rb, 1u);
-  __syncthreads();
-  if (ticket != unsigned(splits - 1)) return;
-  __threadfence();
-  const int r = rb * kRowsPerGroup + threadIdx.x;
+  float *part = a.partials + size_t(split) * a.Npad;
+  if (a.reduce == kReduceTwoPass) {
+    if (active) part[row] = acc;
+    return;
+  }
+  if (a.reduce == kReduceFenceAll) {
+    if (active) part[row] = acc;
+    __threadfence();
+    __syncthreads();
+    if (threadIdx.x == 0) ticket = atomicAdd(a.counters + rb, 1u);
+    __syncthreads();
+    if (ticket != unsigned(splits - 1)) return;
+    __threadfence();
+  } else {
+    // Partials travel as agent-scope (device-coherent) relaxed atomic stores
+    // and loads, which bypass the non-coherent per-XCD L2 state, so no L2
+    // writeback or invalidate is needed.  Each thread waits for its store to
+    // complete before the barrier; the ticket is taken after the barrier, so
+    // the workgroup that draws the last ticket sees every partial.
+    if (active) __hip_atomic_store(part + row, acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0)
+      ticket = __hip_atomic_fetch_add(a.counters + rb, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (ticket != unsigned(splits - 1)) return;
+  }
+  const int r = rb * ROWS + threadIdx.x;
   if (r < a.rows) {
+    // Sum the partials in split order; loads go out 8 at a time so their
+    // latencies overlap.
     float s = 0.0f;
-    for (int k = 0; k < splits; ++k) s += __builtin_nontemporal_load(a.partials + size_t(k) * a.Npad + r);
+    const float *pr = a.partials + r;
+    for (int k0s = 0; k0s < splits; k0s += 8) {
+      float v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        v[j] = k0s + j < splits
+                   ? __hip_atomic_load(pr + size_t(k0s + j) * a.Npad, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                   : 0.0f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) s += v[j];
+    }
     a.y[r] = a.bias ? s + a.bias[r] : s;
   }
-  if (threadIdx.x == 0) a.counters[rb] = 0u;
+  if (threadIdx.x == 0) __hip_atomic_store(a.counters + rb, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Second pass of the two-pass split-K reduction: y[r] = sum_s partials[s][r]
+// (+ bias).  A workgroup covers 64 rows; its 4 wavefronts each sum a quarter
+// of the splits with independent loads, then wave 0 adds the four quarters
+// in a fixed order.
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restrict__ partials, int splits, int Npad,
+                                                            int rows, const float *__restrict__ bias,
+                                                            float *__restrict__ y) {
+  __shared__ float q[4][kWave];
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  const int r = blockIdx.x * kWave + lane;
+  float s = 0.0f;
+  if (r < Npad)
+    for (int k = wave; k < splits; k += 4) s += partials[size_t(k) * Npad + r];
+  q[wave][lane] = s;
+  __syncthreads();
+  if (wave == 0 && r < rows) {
+    const float t = (q[0][lane] + q[1][lane]) + (q[2][lane] + q[3][lane]);
+    y[r] = bias ? t + bias[r] : t;
+  }
+}
+
+template <int FMT, int WAVES>
+static void launch_waves(const GemvArgs &a, hipStream_t st) {
+  const int row_blocks = (a.Npad + WAVES * kWave - 1) / (WAVES * kWave);
+  const int splits = a.Kp / a.kslice;
+  dim3 grid(row_blocks * splits), block(WAVES * kWave);
+  if (a.kslice == 512)
+    lut_gemv_kernel<FMT, 4, WAVES><<<grid, block, 0, st>>>(a, row_blocks, splits);
+  else
+    lut_gemv_kernel<FMT, 2, WAVES><<<grid, block, 0, st>>>(a, row_blocks, splits);
 }
 
 template <int FMT>
 static int launch_fmt(const GemvArgs &a, hipStream_t st) {
-  const int row_blocks = (a.Npad + kRowsPerGroup - 1) / kRowsPerGroup;
-  const int splits = a.Kp / a.kslice;
-  dim3 grid(row_blocks * splits), block(kRowsPerGroup);
-  switch (a.kslice) {
-  case 256: lut_gemv_kernel<FMT, 2><<<grid, block, 0, st>>>(a, row_blocks, splits); break;
-  case 512: lut_gemv_kernel<FMT, 4><<<grid, block, 0, st>>>(a, row_blocks, splits); break;
-  case 1024:
-    if constexpr (Fmt<FMT>::P <= 4) {
-      lut_gemv_kernel<FMT, 8><<<grid, block, 0, st>>>(a, row_blocks, splits);
-      break;
-    }
-    return fail(LMX_ERR_INVALID_ARGUMENT, "k-slice 1024 not built for format %d", FMT);
-  default:
+  if (a.kslice != 256 && a.kslice != 512)
     return fail(LMX_ERR_INVALID_ARGUMENT, "unsupported k-slice %d", a.kslice);
+  switch (a.waves) {
+  case 1: launch_waves<FMT, 1>(a, st); break;
+  case 2: launch_waves<FMT, 2>(a, st); break;
+  case 4: launch_waves<FMT, 4>(a, st); break;
+  default: return fail(LMX_ERR_INVALID_ARGUMENT, "unsupported waves per workgroup %d", a.waves);
   }
+  const int splits = a.Kp / a.kslice;
+  if (splits > 1 && a.reduce == kReduceTwoPass)
+    splitk_reduce_kernel<<<dim3((a.rows + kWave - 1) / kWave), dim3(256), 0, st>>>(a.partials, splits, a.Npad,
+                                                                                  a.rows, a.bias, a.y);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(LMX_ERR_LAUNCH_FAILED, "lut_gemv launch: %s", hipGetErrorString(e));
   return LMX_OK;
@@ -286,6 +372,22 @@ int launch_gemv(int fmt, const GemvArgs &a, void *stream) {
   case LMX_FMT_INT8: return launch_fmt<LMX_FMT_INT8>(a, st);
   }
   return fail(LMX_ERR_UNSUPPORTED_FORMAT, "unknown format %d", fmt);
+}
+
+// ---------------------------------------------------------------------------
+// Copies x[n] into an aligned buffer zero-padded to n_pad (used when the
+// caller's x is not 16-byte aligned or n % 4 != 0).
+__global__ __launch_bounds__(256) void stage_x_kernel(const float *__restrict__ x, size_t n, float *__restrict__ out,
+                                                      size_t n_pad) {
+  const size_t i = size_t(blockIdx.x) * 256 + threadIdx.x;
+  if (i < n_pad) out[i] = i < n ? x[i] : 0.0f;
+}
+
+int launch_stage_x(const float *x, size_t n, float *out, size_t n_pad, void *stream) {
+  stage_x_kernel<<<dim3((n_pad + 255) / 256), dim3(256), 0, static_cast<hipStream_t>(stream)>>>(x, n, out, n_pad);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(LMX_ERR_LAUNCH_FAILED, "stage_x launch: %s", hipGetErrorString(e));
+  return LMX_OK;
 }
 
 // ---------------------------------------------------------------------------
@@ -343,13 +445,13 @@ __global__ __launch_bounds__(256) void luts_kernel(const float *x, size_t n, uns
   if (c * kRotChunk >= n) return;
   float x0, x1, x2, x3;
   const size_t k = c * kRotChunk + 4 * lane;
-  if (rotate == LMX_ROTATE_FWHT256) {
-    load_x4(x, int(c * kRotChunk), int(n), lane, rotate, x0, x1, x2, x3);
+  if (rotate == LMX_ROTATE_FWHT256) {  // n % 256 == 0 and x aligned (checked by the host)
+    load_x4(x, int(c * kRotChunk), int(n), lane, x0, x1, x2, x3);
+    fwht256_regs(x0, x1, x2, x3, lane);
   } else {
     if (k + 3 >= n) return;  // whole groups only, as precompute_luts
     x0 = x[k]; x1 = x[k + 1]; x2 = x[k + 2]; x3 = x[k + 3];
   }
-  if (k + 3 >= n) return;
   float t[16];
   group_table(x0, x1, x2, x3, t);
   float *dst = luts + (k / 4) * 16;
