@@ -34,6 +34,9 @@ EXPORTS = [
     "lmx_weight_create", "lmx_weight_from_blocks", "lmx_weight_destroy", "lmx_weight_info",
     "lmx_weight_read_tiles", "lmx_gemv", "lmx_linear", "lmx_fwht256",
     "lmx_precompute_luts", "lmx_extract_indices",
+    # include/lutmac_hip_compat.h
+    "lmx_host_gemv", "lmx_host_lut_linear", "lmx_host_apply_hadamard_rotation",
+    "lmx_host_precompute_luts",
 ]
 
 
@@ -72,6 +75,10 @@ _SIGS = {
     "lmx_fwht256": ([_p, _sz, _p], _i),
     "lmx_precompute_luts": ([_p, _sz, _u, _p, _p], _i),
     "lmx_extract_indices": ([_p, _p, _sz, _p, _p, _p], _i),
+    "lmx_host_gemv": ([_i, _p, _sz, _p, _p, _sz, _sz], _i),
+    "lmx_host_lut_linear": ([_i, _p, _sz, _p, _p, _p, _sz, _sz, _sz], _i),
+    "lmx_host_apply_hadamard_rotation": ([_p, _sz], _i),
+    "lmx_host_precompute_luts": ([_p, _sz, _p], _i),
 }
 
 _LIB = None
@@ -256,3 +263,39 @@ def extract_indices(sign_plane, zero_plane, n_groups, stream=None):
     check(lib().lmx_extract_indices(_dev_ptr(sign_plane), _dev_ptr(zero_plane), n_groups,
                                     _dev_ptr(pos), _dev_ptr(neg), _stream_ptr(stream)))
     return pos, neg
+
+
+# ---- host-pointer drop-ins (include/lutmac_hip_compat.h) ---------------------
+
+def host_gemv(fmt, blocks, x_padded, M, K):
+    """Raw per-format GEMV on host arrays (reference X_gemv semantics)."""
+    blocks = np.ascontiguousarray(blocks, np.uint8)
+    x = np.ascontiguousarray(x_padded, np.float32)
+    y = np.zeros(M, np.float32)
+    nb = M * ((K + 255) // 256)
+    check(lib().lmx_host_gemv(fmt, _np_ptr(blocks), nb, _np_ptr(x), _np_ptr(y), M, K))
+    return y
+
+
+def host_lut_linear(fmt, blocks, x, M, K, bias=None, batch=1):
+    """lut_linear on host arrays (reference semantics)."""
+    blocks = np.ascontiguousarray(blocks, np.uint8)
+    x = np.ascontiguousarray(x, np.float32)
+    b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+    y = np.zeros(M * batch, np.float32)
+    nb = M * ((K + 255) // 256)
+    check(lib().lmx_host_lut_linear(fmt, _np_ptr(blocks), nb, _np_ptr(b), _np_ptr(x), _np_ptr(y), M, K, batch))
+    return y
+
+
+def host_apply_hadamard_rotation(x):
+    x = np.ascontiguousarray(x, np.float32).copy()
+    check(lib().lmx_host_apply_hadamard_rotation(_np_ptr(x), x.size))
+    return x
+
+
+def host_precompute_luts(x):
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.zeros((x.size // 4) * 16, np.float32)
+    check(lib().lmx_host_precompute_luts(_np_ptr(x), x.size, _np_ptr(out)))
+    return out

@@ -51,6 +51,11 @@ def build(verbose=True):
     tmp = LIB + ".tmp"
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp] + objs, verbose)
     os.replace(tmp, LIB)
+    # C++ drop-in check program (run by tests/test_gpu_compat.py)
+    smoke = os.path.join(ROOT, "tests", "cpp", "compat_smoke")
+    _run([HIPCC, "-O2", "-std=c++17", "-I", os.path.join(ROOT, "include"),
+          os.path.join(ROOT, "tests", "cpp", "compat_smoke.cpp"), "-L", HERE, "-llutmac_hip",
+          "-Wl,-rpath,$ORIGIN/../../lutmac_amd", "-o", smoke], verbose)
     return LIB
 
 

@@ -17,9 +17,18 @@ FORMAT_FILES = {1: "ternary", 2: "binary", 3: "int2", 5: "int3", 6: "int4", 7: "
 
 
 def _declared_symbols():
-    hdr = open(os.path.join(ROOT, "include", "lutmac_hip.h")).read()
-    hdr = re.sub(r"/\*.*?\*/", "", hdr, flags=re.S)
-    return sorted(set(re.findall(r"\b(lmx_[a-z0-9_]+)\s*\(", hdr)))
+    """extern "C" entry points declared by every header under include/."""
+    names = set()
+    inc = os.path.join(ROOT, "include")
+    for h in sorted(os.listdir(inc)):
+        if not h.endswith(".h"):
+            continue
+        hdr = open(os.path.join(inc, h)).read()
+        hdr = re.sub(r"/\*.*?\*/", "", hdr, flags=re.S)
+        if '#ifdef __cplusplus\n}' in hdr:          # drop the C++-only wrapper section
+            hdr = hdr.split('#ifdef __cplusplus\n}')[0]
+        names |= set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(lmx_[a-z0-9_]+)\s*\(", hdr, flags=re.M))
+    return sorted(names)
 
 
 def test_library_exports_every_declared_symbol():
