@@ -67,6 +67,36 @@ int choose_kslice(size_t Npad, size_t Kp, int waves) {
   return 256;
 }
 
+// Full-K configuration for a shape, or kFullK_None for the split-K kernel.
+// A configuration must cover all Kc chunks with its k-slices, fit the LDS,
+// and give at least 128 workgroups; among those, prefer >= 256 workgroups,
+// then fewer idle slices, then more rows per workgroup (fewer table builds).
+// LMX_FULLK: 0 forces split-K, 1..6 forces a configuration.
+int choose_fullk(int fmt, size_t Npad, size_t Kp) {
+  static const int env = env_int("LMX_FULLK", -1);
+  const size_t Kc = Kp / kChunk;
+  FormatInfo fi;
+  format_info(fmt, &fi);
+  auto fits = [&](int cfg) {
+    const FullKShape f = fullk_shape(cfg);
+    if (f.cps * fi.planes > 8) return false;  // keeps the weight words in registers (no spills)
+    return size_t(f.waves * f.h * f.cps) >= Kc && fullk_lds_bytes(f.waves, f.h, f.cps, Kc) <= kMaxLdsBytes;
+  };
+  if (env >= 0) return (env == 0 || !fits(env)) ? kFullK_None : env;
+  int best = kFullK_None;
+  double best_score = -1.0;
+  for (int cfg = kFullK_16x2x2; cfg <= kFullK_4x4x1; ++cfg) {
+    if (!fits(cfg)) continue;
+    const FullKShape f = fullk_shape(cfg);
+    const size_t groups = Npad / size_t(kWave / f.h);
+    if (groups < 128) continue;
+    const double idle = 1.0 - double(Kc) / double(f.waves * f.h * f.cps);
+    const double score = (groups >= 256 ? 4.0 : 0.0) + (1.0 - idle) * 2.0 + (kWave / f.h) / 64.0;
+    if (score > best_score) best_score = score, best = cfg;
+  }
+  return best;
+}
+
 int choose_reduce() {
   static const int env = env_int("LMX_REDUCE", kReduceTwoPass);
   return (env == kReduceTicket || env == kReduceFenceAll) ? env : kReduceTwoPass;
@@ -106,6 +136,7 @@ int upload(int fmt, size_t rows, size_t cols, size_t group, const uint8_t *plane
   w->waves = choose_waves();
   w->kslice = choose_kslice(w->Npad, w->Kp, w->waves);
   w->reduce = choose_reduce();
+  w->fullk = choose_fullk(fmt, w->Npad, w->Kp);
 
   std::vector<uint8_t> tiles;
   std::vector<float> sc;
@@ -362,6 +393,7 @@ int lmx_gemv(const lmx_weight *w, const float *x, float *y, size_t batch, unsign
   a.kslice = w->kslice;
   a.reduce = w->reduce;
   a.waves = w->waves;
+  a.fullk = w->fullk;
   for (size_t b = 0; b < batch; ++b) {
     a.x = x + b * w->cols;
     a.y = y + b * w->rows;
@@ -402,6 +434,7 @@ int lmx_linear(const lmx_weight *w, const float *bias, const float *x, float *y,
   a.kslice = w->kslice;
   a.reduce = w->reduce;
   a.waves = w->waves;
+  a.fullk = w->fullk;
   a.rotate = rotate ? LMX_ROTATE_FWHT256 : LMX_ROTATE_NONE;
   for (size_t b = 0; b < batch; ++b) {
     a.x = x + b * w->cols;

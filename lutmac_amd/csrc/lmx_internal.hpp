@@ -57,7 +57,43 @@ struct GemvArgs {
   unsigned rotate;         // LMX_ROTATE_NONE / LMX_ROTATE_FWHT256
   int reduce;              // split-K reduction strategy (kReduce*)
   int waves;               // wavefronts (64-row slabs) per workgroup: 1, 2 or 4
+  int fullk;               // 0: split-K kernel; else a kFullK_* configuration
 };
+
+// Full-K kernel configurations (waves x k-slices per wave x chunks per slice):
+// the workgroup holds the tables of the whole K and reduces in LDS.
+enum {
+  kFullK_None = 0,
+  kFullK_16x2x2 = 1,  // 32 rows, 32 slices of 256: K <= 8192
+  kFullK_16x2x3 = 2,  // 32 rows, 32 slices of 384: K <= 12288 (LDS-bound ~9472)
+  kFullK_8x2x1 = 3,   // 32 rows, 16 slices of 128: K <= 2048
+  kFullK_16x1x1 = 4,  // 64 rows, 16 slices of 128: K <= 2048
+  kFullK_16x4x1 = 5,  // 16 rows, 64 slices of 128: K <= 8192
+  kFullK_4x4x1 = 6    // 16 rows, 16 slices of 128: K <= 2048
+};
+
+constexpr size_t kMaxLdsBytes = 160 * 1024;  // LDS per workgroup on gfx950
+
+// LDS of a full-K launch: x sums + slice partials (rounded to 256 B), then
+// one table region of cps*2048 + 256 B per slice that holds chunks.
+inline size_t fullk_lds_bytes(int waves, int h, int cps, size_t Kc) {
+  const size_t prefix = (size_t(waves * h * cps + waves * kWave) * 4 + 255) / 256 * 256;
+  const size_t used = (Kc + cps - 1) / cps;
+  return prefix + used * (size_t(cps) * 2048 + 256);
+}
+
+struct FullKShape { int waves, h, cps; };
+inline FullKShape fullk_shape(int cfg) {
+  switch (cfg) {
+  case kFullK_16x2x2: return {16, 2, 2};
+  case kFullK_16x2x3: return {16, 2, 3};
+  case kFullK_8x2x1: return {8, 2, 1};
+  case kFullK_16x1x1: return {16, 1, 1};
+  case kFullK_16x4x1: return {16, 4, 1};
+  case kFullK_4x4x1: return {4, 4, 1};
+  }
+  return {0, 0, 0};
+}
 
 // Split-K reduction strategies.
 constexpr int kReduceTicket = 0;    // last workgroup of a row block sums (one release per group)
@@ -88,6 +124,7 @@ struct lmx_weight {
   int kslice = 0;          // chosen k-slice per workgroup
   int reduce = 0;          // split-K reduction strategy
   int waves = 4;           // wavefronts per workgroup
+  int fullk = 0;           // full-K kernel configuration (kFullK_*), 0 = split-K
   void *d_planes = nullptr;
   float *d_scales = nullptr;
   float *d_partials = nullptr;

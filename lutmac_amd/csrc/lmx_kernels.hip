@@ -92,6 +92,36 @@ __device__ __forceinline__ float finish_chunk(const float *A, float xs, const fl
   }
 }
 
+
+// Table lookups of one 128-k chunk for one lane: NA accumulators over the
+// 32 groups of the chunk.  Addresses come from v_perm (table base bytes 1-2,
+// 4*nibble in byte 0, plus an optional bank shift in bits 6-7); the group's
+// table offset is the ds_read immediate.  All 64 lanes read the same 16-entry
+// table at a time: 16 consecutive dwords, no bank conflicts.
+template <int FMT>
+__device__ __forceinline__ void chunk_lookups(const u32x4 *wc, uint32_t cbase, uint32_t shift, float *A) {
+  constexpr int P = Fmt<FMT>::P, NA = Fmt<FMT>::NA;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    uint32_t wi[P], v[NA];
+#pragma unroll
+    for (int p = 0; p < P; ++p) wi[p] = wc[p][i];
+    lookup_words<FMT>(wi, v);
+#pragma unroll
+    for (int q = 0; q < NA; ++q) {
+      const uint32_t hi = ((v[q] >> 2) & 0x3C3C3C3Cu) | shift;  // byte b: 4*nibble of group 8i+2b
+      const uint32_t lo = ((v[q] << 2) & 0x3C3C3C3Cu) | shift;  // byte b: 4*nibble of group 8i+2b+1
+      float t[8];
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        t[2 * b] = lds_load(__builtin_amdgcn_perm(cbase, hi, 0x0C060500u | b) + (8 * i + 2 * b) * 64);
+        t[2 * b + 1] = lds_load(__builtin_amdgcn_perm(cbase, lo, 0x0C060500u | b) + (8 * i + 2 * b + 1) * 64);
+      }
+      A[q] += ((t[0] + t[1]) + (t[2] + t[3])) + ((t[4] + t[5]) + (t[6] + t[7]));
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Register FWHT-256: lane l holds x[4l..4l+3] of one 256-chunk.  Strides 1
 // and 2 are in-lane, strides 4..128 pair lane l with lane l^(h/4).  Every
@@ -227,29 +257,7 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_kernel(GemvArgs a, int
       float A[NA];
 #pragma unroll
       for (int i = 0; i < NA; ++i) A[i] = 0.0f;
-      const uint32_t cbase = tbase + c * (32 * 64);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        uint32_t wi[P], v[NA];
-#pragma unroll
-        for (int p = 0; p < P; ++p) wi[p] = w[c][p][i];
-        lookup_words<FMT>(wi, v);
-#pragma unroll
-        for (int q = 0; q < NA; ++q) {
-          const uint32_t hi = (v[q] >> 2) & 0x3C3C3C3Cu;  // byte b: 4*nibble of group 8i+2b
-          const uint32_t lo = (v[q] << 2) & 0x3C3C3C3Cu;  // byte b: 4*nibble of group 8i+2b+1
-          float t[8];
-#pragma unroll
-          for (int b = 0; b < 4; ++b) {
-            // v_perm: address = table base (bytes 1,2) | 4*nibble (byte 0)
-            const uint32_t ah = __builtin_amdgcn_perm(cbase, hi, 0x0C060500u | b);
-            const uint32_t al = __builtin_amdgcn_perm(cbase, lo, 0x0C060500u | b);
-            t[2 * b] = lds_load(ah + (8 * i + 2 * b) * 64);
-            t[2 * b + 1] = lds_load(al + (8 * i + 2 * b + 1) * 64);
-          }
-          A[q] += ((t[0] + t[1]) + (t[2] + t[3])) + ((t[4] + t[5]) + (t[6] + t[7]));
-        }
-      }
+      chunk_lookups<FMT>(w[c], tbase + c * (32 * 64), 0u, A);
       float xs = 0.0f;
       if constexpr (Fmt<FMT>::XS) xs = xsum[c];
       acc = finish_chunk<FMT>(A, xs, sc[c], acc);
@@ -330,6 +338,146 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restr
   }
 }
 
+// ---------------------------------------------------------------------------
+// Full-K variant: a workgroup owns RW = 64/H output rows and the whole
+// padded K, so no partial sums leave the workgroup.  The WAVES*H k-slices of
+// CPS chunks each are spread over the lanes: lane l of wave w serves row
+// l % RW of the workgroup and k-slice w*H + l/RW.  The tables of the whole K
+// sit in LDS (16 B per activation); each 256-chunk is rotated by one wave.
+// Slice s keeps its tables at s*(CPS*2048 + 256) bytes; with H = 4, two
+// quarter-wave slices share an LDS pass, so odd slices are shifted by 64 B
+// into other banks (the shift rides in bits 6-7 of the nibble byte).  At the
+// end the NS = WAVES*H slice partials of each row are summed in slice order.
+template <int WAVES, int H, int CPS>
+constexpr uint32_t fullk_prefix_bytes() {
+  return (uint32_t(WAVES * H * CPS + WAVES * kWave) * 4 + 255) / 256 * 256;
+}
+
+template <int H>
+__device__ __forceinline__ uint32_t slice_shift(int s) {
+  return (H == 4 && (s & 1)) ? 64u : 0u;
+}
+
+template <int FMT, int WAVES, int H, int CPS>
+__global__ __launch_bounds__(WAVES * kWave) void lut_gemv_fullk_kernel(GemvArgs a) {
+  constexpr int P = Fmt<FMT>::P, NA = Fmt<FMT>::NA, S = Fmt<FMT>::S;
+  constexpr int RW = kWave / H;
+  constexpr int NS = WAVES * H;
+  constexpr uint32_t SSTRIDE = CPS * 32 * 64 + 256;
+  constexpr int XJ = (NS * CPS / 2 + WAVES - 1) / WAVES;   // 256-chunks per wave (upper bound)
+  constexpr uint32_t PREFIX = fullk_prefix_bytes<WAVES, H, CPS>();
+  extern __shared__ __attribute__((aligned(256))) float lds[];
+  const int Kc = a.Kp / kChunk;
+  const int used = (Kc + CPS - 1) / CPS;                      // slices holding chunks
+  float *xsum = lds;                                          // [NS*CPS]
+  float *red = lds + NS * CPS;                                // [NS][RW]
+  char *tables = reinterpret_cast<char *>(lds) + PREFIX;      // slice s at s*SSTRIDE
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int sub = lane / RW;
+  const int s = wave * H + sub;
+  const int rl = lane % RW;
+  const int row = blockIdx.x * RW + rl;
+  const int lr = min(row, a.Npad - 1);
+
+  // ---- loads: activations for this wave's 256-chunks, then the weights ----
+  const int C2n = a.Kp / kRotChunk;
+  float xv[XJ][4];
+#pragma unroll
+  for (int j = 0; j < XJ; ++j) {
+    const int c2 = min(wave + j * WAVES, C2n - 1);
+    load_x4(a.x, c2 * kRotChunk, a.cols, lane, xv[j][0], xv[j][1], xv[j][2], xv[j][3]);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  u32x4 w[CPS][P];
+  float sc[CPS][S];
+  {
+    const u32x4 *__restrict__ pl = reinterpret_cast<const u32x4 *>(a.planes);
+    const size_t Npad = size_t(a.Npad);
+#pragma unroll
+    for (int c = 0; c < CPS; ++c) {
+      const int ch = min(s * CPS + c, Kc - 1);                 // clamped; masked below
+#pragma unroll
+      for (int p = 0; p < P; ++p) w[c][p] = __builtin_nontemporal_load(pl + (size_t(ch) * P + p) * Npad + lr);
+      const int g = ch / a.group_chunks;
+#pragma unroll
+      for (int t = 0; t < S; ++t) sc[c][t] = a.scales[(size_t(t) * a.n_groups + g) * Npad + lr];
+    }
+  }
+
+  // ---- prologue: (FWHT-256) -> 16-entry group tables of the whole K -------
+#pragma unroll
+  for (int j = 0; j < XJ; ++j) {
+    const int c2 = wave + j * WAVES;
+    if (c2 >= C2n) break;   // wave-uniform
+    float x0 = xv[j][0], x1 = xv[j][1], x2 = xv[j][2], x3 = xv[j][3];
+    if (a.rotate == LMX_ROTATE_FWHT256) fwht256_regs(x0, x1, x2, x3, lane);
+    float t[16];
+    group_table(x0, x1, x2, x3, t);
+    const int ch = c2 * 2 + (lane >> 5);                      // 128-chunk of this group
+    const int ts = ch / CPS;                                  // its k-slice
+    float4 *dst = reinterpret_cast<float4 *>(tables + ts * SSTRIDE + slice_shift<H>(ts) + (ch % CPS) * 2048 +
+                                             (lane & 31) * 64);
+    dst[0] = make_float4(t[0], t[1], t[2], t[3]);
+    dst[1] = make_float4(t[4], t[5], t[6], t[7]);
+    dst[2] = make_float4(t[8], t[9], t[10], t[11]);
+    dst[3] = make_float4(t[12], t[13], t[14], t[15]);
+    if constexpr (Fmt<FMT>::XS) {
+      float xs = t[15];
+#pragma unroll
+      for (int d = 16; d >= 1; d >>= 1) xs += __shfl_xor(xs, d, 64);
+      if ((lane & 31) == 0) xsum[ch] = xs;
+    }
+  }
+  __syncthreads();
+
+  // ---- lookups over this lane's k-slice -----------------------------------
+  float acc = 0.0f;
+  {
+    // Lanes whose slice lies past K read slice used-1 (in bounds) and discard it.
+    const uint32_t tbase = lds_addr(lds) + PREFIX + min(s, used - 1) * SSTRIDE;   // 256-byte aligned
+    const uint32_t shift = slice_shift<H>(s) * 0x01010101u;   // bits 6-7 of each byte
+#pragma unroll
+    for (int c = 0; c < CPS; ++c) {
+      float A[NA];
+#pragma unroll
+      for (int i = 0; i < NA; ++i) A[i] = 0.0f;
+      chunk_lookups<FMT>(w[c], tbase + c * 2048, shift, A);
+      const int ch = s * CPS + c;
+      float xs = 0.0f;
+      if constexpr (Fmt<FMT>::XS) xs = xsum[min(ch, Kc - 1)];
+      const float nacc = finish_chunk<FMT>(A, xs, sc[c], acc);
+      acc = ch < Kc ? nacc : acc;
+    }
+  }
+
+  // ---- in-workgroup reduction over the k-slices, fixed order --------------
+  red[s * RW + rl] = acc;
+  __syncthreads();
+  if (threadIdx.x < RW) {
+    const int r = blockIdx.x * RW + threadIdx.x;
+    float t = 0.0f;
+#pragma unroll 8
+    for (int k = 0; k < NS; ++k) t += red[k * RW + threadIdx.x];
+    if (r < a.rows) a.y[r] = a.bias ? t + a.bias[r] : t;
+  }
+}
+
+template <int FMT, int WAVES, int H, int CPS>
+static int launch_fullk_cfg(const GemvArgs &a, hipStream_t st) {
+  const size_t lds = fullk_lds_bytes(WAVES, H, CPS, a.Kp / kChunk);
+  static const hipError_t attr = hipFuncSetAttribute(
+      reinterpret_cast<const void *>(&lut_gemv_fullk_kernel<FMT, WAVES, H, CPS>),
+      hipFuncAttributeMaxDynamicSharedMemorySize, int(kMaxLdsBytes));
+  if (attr != hipSuccess) return fail(LMX_ERR_LAUNCH_FAILED, "hipFuncSetAttribute: %s", hipGetErrorString(attr));
+  if (lds > kMaxLdsBytes) return fail(LMX_ERR_INVALID_ARGUMENT, "full-K tables need %zu B of LDS", lds);
+  constexpr int RW = kWave / H;
+  lut_gemv_fullk_kernel<FMT, WAVES, H, CPS>
+      <<<dim3((a.Npad + RW - 1) / RW), dim3(WAVES * kWave), lds, st>>>(a);
+  return LMX_OK;
+}
+
 template <int FMT, int WAVES>
 static void launch_waves(const GemvArgs &a, hipStream_t st) {
   const int row_blocks = (a.Npad + WAVES * kWave - 1) / (WAVES * kWave);
@@ -342,7 +490,27 @@ static void launch_waves(const GemvArgs &a, hipStream_t st) {
 }
 
 template <int FMT>
+static int launch_fullk(const GemvArgs &a, hipStream_t st) {
+  switch (a.fullk) {
+  case kFullK_16x2x2: return launch_fullk_cfg<FMT, 16, 2, 2>(a, st);
+  case kFullK_16x2x3: return launch_fullk_cfg<FMT, 16, 2, 3>(a, st);
+  case kFullK_8x2x1: return launch_fullk_cfg<FMT, 8, 2, 1>(a, st);
+  case kFullK_16x1x1: return launch_fullk_cfg<FMT, 16, 1, 1>(a, st);
+  case kFullK_16x4x1: return launch_fullk_cfg<FMT, 16, 4, 1>(a, st);
+  case kFullK_4x4x1: return launch_fullk_cfg<FMT, 4, 4, 1>(a, st);
+  }
+  return fail(LMX_ERR_INVALID_ARGUMENT, "unknown full-K configuration %d", a.fullk);
+}
+
+template <int FMT>
 static int launch_fmt(const GemvArgs &a, hipStream_t st) {
+  if (a.fullk) {
+    int r = launch_fullk<FMT>(a, st);
+    if (r) return r;
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(LMX_ERR_LAUNCH_FAILED, "lut_gemv_fullk launch: %s", hipGetErrorString(e));
+    return LMX_OK;
+  }
   if (a.kslice != 256 && a.kslice != 512)
     return fail(LMX_ERR_INVALID_ARGUMENT, "unsupported k-slice %d", a.kslice);
   switch (a.waves) {
