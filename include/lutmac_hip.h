@@ -128,6 +128,14 @@ int lmx_weight_destroy(lmx_weight *w);
 /* Format, shape and device bytes (planes + scales) of a handle. */
 int lmx_weight_info(const lmx_weight *w, int *format, size_t *rows,
                     size_t *cols, size_t *device_bytes);
+/* Kernel plan chosen for a handle at creation: full-K configuration
+ * (0 = split-K kernel, 1..6 = LMX_FULLK values), split-K k-slice, and
+ * whether the full-K kernel stages its weight loads.  Diagnostic only; the
+ * environment variables LMX_FULLK, LMX_KSLICE, LMX_WAVES, LMX_STAGED and
+ * LMX_REDUCE, read when a handle is created, override the plan.  No
+ * reference counterpart (the reference has one CPU kernel per format). */
+int lmx_weight_kernel_config(const lmx_weight *w, int *fullk, int *kslice,
+                             int *staged);
 /* Copy the device tile layout back to the host (bit-exact repack check). */
 int lmx_weight_read_tiles(const lmx_weight *w, uint8_t *tiles, size_t bytes);
 

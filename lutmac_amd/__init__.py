@@ -32,7 +32,7 @@ EXPORTS = [
     "lmx_format_info", "lmx_block_bytes", "lmx_blocks_to_planes", "lmx_planes_to_blocks",
     "lmx_tile_bytes", "lmx_tile_planes", "lmx_untile_planes",
     "lmx_weight_create", "lmx_weight_from_blocks", "lmx_weight_destroy", "lmx_weight_info",
-    "lmx_weight_read_tiles", "lmx_gemv", "lmx_linear", "lmx_fwht256",
+    "lmx_weight_kernel_config", "lmx_weight_read_tiles", "lmx_gemv", "lmx_linear", "lmx_fwht256",
     "lmx_precompute_luts", "lmx_extract_indices",
     # include/lutmac_hip_compat.h
     "lmx_host_gemv", "lmx_host_lut_linear", "lmx_host_apply_hadamard_rotation",
@@ -69,6 +69,7 @@ _SIGS = {
     "lmx_weight_destroy": ([_p], _i),
     "lmx_weight_info": ([_p, ctypes.POINTER(_i), ctypes.POINTER(_sz), ctypes.POINTER(_sz),
                          ctypes.POINTER(_sz)], _i),
+    "lmx_weight_kernel_config": ([_p, ctypes.POINTER(_i), ctypes.POINTER(_i), ctypes.POINTER(_i)], _i),
     "lmx_weight_read_tiles": ([_p, _p, _sz], _i),
     "lmx_gemv": ([_p, _p, _p, _sz, _u, _p], _i),
     "lmx_linear": ([_p, _p, _p, _p, _sz, _p], _i),
@@ -206,6 +207,12 @@ class Weight:
     @property
     def handle(self):
         return self._h
+
+    def kernel_config(self):
+        """(full-K configuration or 0 for split-K, split-K k-slice, staged loads)."""
+        f, k, st = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+        check(lib().lmx_weight_kernel_config(self._h, ctypes.byref(f), ctypes.byref(k), ctypes.byref(st)))
+        return f.value, k.value, st.value
 
     def read_tiles(self):
         out = np.zeros(tile_bytes(self.format, self.rows, self.cols), np.uint8)

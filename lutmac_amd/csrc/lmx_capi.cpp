@@ -53,14 +53,14 @@ int env_int(const char *name, int dflt) {
 }
 
 int choose_waves() {
-  static const int env = env_int("LMX_WAVES", 4);
+  const int env = env_int("LMX_WAVES", 4);
   return (env == 1 || env == 2 || env == 4) ? env : 4;
 }
 
 // k-slice per workgroup: 512 when the padded K allows it and the grid still
 // has at least 4 workgroups per CU, else 256.  LMX_KSLICE overrides.
 int choose_kslice(size_t Npad, size_t Kp, int waves) {
-  static const int env = env_int("LMX_KSLICE", 0);
+  const int env = env_int("LMX_KSLICE", 0);
   if ((env == 256 || env == 512) && Kp % size_t(env) == 0) return env;
   const size_t row_blocks = (Npad + kWave * waves - 1) / (kWave * waves);
   if (Kp % 512 == 0 && row_blocks * (Kp / 512) >= 1024) return 512;
@@ -68,12 +68,11 @@ int choose_kslice(size_t Npad, size_t Kp, int waves) {
 }
 
 // Full-K configuration for a shape, or kFullK_None for the split-K kernel.
-// A configuration must cover all Kc chunks with its k-slices, fit the LDS,
-// and give at least 128 workgroups; among those, prefer >= 256 workgroups,
-// then fewer idle slices, then more rows per workgroup (fewer table builds).
-// LMX_FULLK: 0 forces split-K, 1..6 forces a configuration.
+// A configuration must cover all Kc chunks with its k-slices, fit the LDS
+// and keep its weight words in registers.  LMX_FULLK: 0 forces split-K,
+// 1..6 forces a configuration (when it fits).
 int choose_fullk(int fmt, size_t Npad, size_t Kp) {
-  static const int env = env_int("LMX_FULLK", -1);
+  const int env = env_int("LMX_FULLK", -1);
   const size_t Kc = Kp / kChunk;
   FormatInfo fi;
   format_info(fmt, &fi);
@@ -83,22 +82,39 @@ int choose_fullk(int fmt, size_t Npad, size_t Kp) {
     return size_t(f.waves * f.h * f.cps) >= Kc && fullk_lds_bytes(f.waves, f.h, f.cps, Kc) <= kMaxLdsBytes;
   };
   if (env >= 0) return (env == 0 || !fits(env)) ? kFullK_None : env;
+  auto workgroups = [&](int cfg) { return Npad / size_t(kWave / fullk_shape(cfg).h); };
+  // Measured on MI355X (4-bit, decode shapes):
+  //  * K <= 2048: 4 waves x 16 rows per workgroup wins from N = 256 up to
+  //    ~16k rows (latency-bound small GEMVs want many small workgroups); up
+  //    to ~32k rows 8 waves x 32 rows; beyond that (LM heads) every
+  //    workgroup rebuilding the tables costs more than the split-K handoff.
+  //  * larger K: the configuration with the most workgroups that still
+  //    leaves at most one per CU (each holds up to 160 KB of tables);
+  //    split-K when none does.
+  if (Kc <= 16) {
+    if (fits(kFullK_4x4x1) && workgroups(kFullK_4x4x1) <= 1024) return kFullK_4x4x1;
+    if (fits(kFullK_8x2x1) && workgroups(kFullK_8x2x1) <= 1024) return kFullK_8x2x1;
+    return kFullK_None;
+  }
   int best = kFullK_None;
-  double best_score = -1.0;
+  size_t best_wg = 0, best_slots = 0;
   for (int cfg = kFullK_16x2x2; cfg <= kFullK_4x4x1; ++cfg) {
     if (!fits(cfg)) continue;
     const FullKShape f = fullk_shape(cfg);
-    const size_t groups = Npad / size_t(kWave / f.h);
-    if (groups < 128) continue;
-    const double idle = 1.0 - double(Kc) / double(f.waves * f.h * f.cps);
-    const double score = (groups >= 256 ? 4.0 : 0.0) + (1.0 - idle) * 2.0 + (kWave / f.h) / 64.0;
-    if (score > best_score) best_score = score, best = cfg;
+    const size_t wg = workgroups(cfg), slots = size_t(f.waves * f.h * f.cps);
+    if (wg > 256) continue;
+    if (wg > best_wg || (wg == best_wg && slots < best_slots)) best = cfg, best_wg = wg, best_slots = slots;
   }
   return best;
 }
 
+int choose_staged() {
+  const int env = env_int("LMX_STAGED", 1);
+  return env;
+}
+
 int choose_reduce() {
-  static const int env = env_int("LMX_REDUCE", kReduceTwoPass);
+  const int env = env_int("LMX_REDUCE", kReduceTwoPass);
   return (env == kReduceTicket || env == kReduceFenceAll) ? env : kReduceTwoPass;
 }
 
@@ -137,6 +153,7 @@ int upload(int fmt, size_t rows, size_t cols, size_t group, const uint8_t *plane
   w->kslice = choose_kslice(w->Npad, w->Kp, w->waves);
   w->reduce = choose_reduce();
   w->fullk = choose_fullk(fmt, w->Npad, w->Kp);
+  w->staged = choose_staged();
 
   std::vector<uint8_t> tiles;
   std::vector<float> sc;
@@ -356,6 +373,14 @@ int lmx_weight_info(const lmx_weight *w, int *format, size_t *rows, size_t *cols
   return LMX_OK;
 }
 
+int lmx_weight_kernel_config(const lmx_weight *w, int *fullk, int *kslice, int *staged) {
+  if (!w) return fail(LMX_ERR_INVALID_ARGUMENT, "weight handle is NULL");
+  if (fullk) *fullk = w->fullk;
+  if (kslice) *kslice = w->kslice;
+  if (staged) *staged = w->staged;
+  return LMX_OK;
+}
+
 int lmx_weight_read_tiles(const lmx_weight *w, uint8_t *tiles, size_t bytes) {
   int st = check_weight(w);
   if (st) return st;
@@ -394,6 +419,7 @@ int lmx_gemv(const lmx_weight *w, const float *x, float *y, size_t batch, unsign
   a.reduce = w->reduce;
   a.waves = w->waves;
   a.fullk = w->fullk;
+  a.staged = w->staged;
   for (size_t b = 0; b < batch; ++b) {
     a.x = x + b * w->cols;
     a.y = y + b * w->rows;
@@ -435,6 +461,7 @@ int lmx_linear(const lmx_weight *w, const float *bias, const float *x, float *y,
   a.reduce = w->reduce;
   a.waves = w->waves;
   a.fullk = w->fullk;
+  a.staged = w->staged;
   a.rotate = rotate ? LMX_ROTATE_FWHT256 : LMX_ROTATE_NONE;
   for (size_t b = 0; b < batch; ++b) {
     a.x = x + b * w->cols;

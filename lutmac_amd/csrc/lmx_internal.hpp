@@ -58,6 +58,7 @@ struct GemvArgs {
   int reduce;              // split-K reduction strategy (kReduce*)
   int waves;               // wavefronts (64-row slabs) per workgroup: 1, 2 or 4
   int fullk;               // 0: split-K kernel; else a kFullK_* configuration
+  int staged;              // full-K: issue part of the weight loads after the table prologue
 };
 
 // Full-K kernel configurations (waves x k-slices per wave x chunks per slice):
@@ -125,6 +126,7 @@ struct lmx_weight {
   int reduce = 0;          // split-K reduction strategy
   int waves = 4;           // wavefronts per workgroup
   int fullk = 0;           // full-K kernel configuration (kFullK_*), 0 = split-K
+  int staged = 1;          // full-K: later chunks' weight loads after the prologue
   void *d_planes = nullptr;
   float *d_scales = nullptr;
   float *d_partials = nullptr;

@@ -93,31 +93,53 @@ __device__ __forceinline__ float finish_chunk(const float *A, float xs, const fl
 }
 
 
+// The 8 lookups of one 32-bit lookup word (word i of a 128-k chunk = groups
+// 8i..8i+7), summed as a balanced tree.  Addresses come from v_perm (table
+// base bytes 1-2, 4*nibble in byte 0, plus an optional bank shift in bits
+// 6-7); the group's table offset is the ds_read immediate.  All 64 lanes
+// read the same 16-entry table at a time: 16 consecutive dwords, no bank
+// conflicts.
+__device__ __forceinline__ float word_lookups(uint32_t v, int i, uint32_t cbase, uint32_t shift) {
+  const uint32_t hi = ((v >> 2) & 0x3C3C3C3Cu) | shift;  // byte b: 4*nibble of group 8i+2b
+  const uint32_t lo = ((v << 2) & 0x3C3C3C3Cu) | shift;  // byte b: 4*nibble of group 8i+2b+1
+  float t[8];
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    t[2 * b] = lds_load(__builtin_amdgcn_perm(cbase, hi, 0x0C060500u | b) + (8 * i + 2 * b) * 64);
+    t[2 * b + 1] = lds_load(__builtin_amdgcn_perm(cbase, lo, 0x0C060500u | b) + (8 * i + 2 * b + 1) * 64);
+  }
+  return ((t[0] + t[1]) + (t[2] + t[3])) + ((t[4] + t[5]) + (t[6] + t[7]));
+}
+
 // Table lookups of one 128-k chunk for one lane: NA accumulators over the
-// 32 groups of the chunk.  Addresses come from v_perm (table base bytes 1-2,
-// 4*nibble in byte 0, plus an optional bank shift in bits 6-7); the group's
-// table offset is the ds_read immediate.  All 64 lanes read the same 16-entry
-// table at a time: 16 consecutive dwords, no bank conflicts.
+// 32 groups of the chunk.
 template <int FMT>
 __device__ __forceinline__ void chunk_lookups(const u32x4 *wc, uint32_t cbase, uint32_t shift, float *A) {
   constexpr int P = Fmt<FMT>::P, NA = Fmt<FMT>::NA;
+  if constexpr (FMT == LMX_FMT_TERNARY) {
+    // Both accumulators need both planes: word-outer.
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    uint32_t wi[P], v[NA];
+    for (int i = 0; i < 4; ++i) {
+      uint32_t wi[P], v[NA];
 #pragma unroll
-    for (int p = 0; p < P; ++p) wi[p] = wc[p][i];
-    lookup_words<FMT>(wi, v);
+      for (int p = 0; p < P; ++p) wi[p] = wc[p][i];
+      lookup_words<FMT>(wi, v);
+#pragma unroll
+      for (int q = 0; q < NA; ++q) A[q] += word_lookups(v[q], i, cbase, shift);
+    }
+  } else {
+    // Accumulator q reads plane q only: plane-outer, so the lookups of a
+    // plane can start as soon as its load has landed.
 #pragma unroll
     for (int q = 0; q < NA; ++q) {
-      const uint32_t hi = ((v[q] >> 2) & 0x3C3C3C3Cu) | shift;  // byte b: 4*nibble of group 8i+2b
-      const uint32_t lo = ((v[q] << 2) & 0x3C3C3C3Cu) | shift;  // byte b: 4*nibble of group 8i+2b+1
-      float t[8];
 #pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        t[2 * b] = lds_load(__builtin_amdgcn_perm(cbase, hi, 0x0C060500u | b) + (8 * i + 2 * b) * 64);
-        t[2 * b + 1] = lds_load(__builtin_amdgcn_perm(cbase, lo, 0x0C060500u | b) + (8 * i + 2 * b + 1) * 64);
+      for (int i = 0; i < 4; ++i) {
+        uint32_t wi[P], v[NA];
+#pragma unroll
+        for (int p = 0; p < P; ++p) wi[p] = wc[p][i];
+        lookup_words<FMT>(wi, v);
+        A[q] += word_lookups(v[q], i, cbase, shift);
       }
-      A[q] += ((t[0] + t[1]) + (t[2] + t[3])) + ((t[4] + t[5]) + (t[6] + t[7]));
     }
   }
 }
@@ -358,7 +380,7 @@ __device__ __forceinline__ uint32_t slice_shift(int s) {
   return (H == 4 && (s & 1)) ? 64u : 0u;
 }
 
-template <int FMT, int WAVES, int H, int CPS>
+template <int FMT, int WAVES, int H, int CPS, bool STAGED>
 __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_fullk_kernel(GemvArgs a) {
   constexpr int P = Fmt<FMT>::P, NA = Fmt<FMT>::NA, S = Fmt<FMT>::S;
   constexpr int RW = kWave / H;
@@ -390,21 +412,27 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_fullk_kernel(GemvArgs 
     load_x4(a.x, c2 * kRotChunk, a.cols, lane, xv[j][0], xv[j][1], xv[j][2], xv[j][3]);
   }
   __builtin_amdgcn_sched_barrier(0);
+  // Weight loads.  STAGED (CPS > 1 only) issues chunk 0 before the table
+  // prologue and the later chunks after it, so that HBM serves chunk 0 of
+  // every wave first and chunk 1 streams in while chunk 0 is looked up.
   u32x4 w[CPS][P];
   float sc[CPS][S];
-  {
-    const u32x4 *__restrict__ pl = reinterpret_cast<const u32x4 *>(a.planes);
-    const size_t Npad = size_t(a.Npad);
+  const u32x4 *__restrict__ pl = reinterpret_cast<const u32x4 *>(a.planes);
+  const size_t Npad = size_t(a.Npad);
+  auto load_planes = [&](int c) {
+    const int ch = min(s * CPS + c, Kc - 1);                   // clamped; masked below
 #pragma unroll
-    for (int c = 0; c < CPS; ++c) {
-      const int ch = min(s * CPS + c, Kc - 1);                 // clamped; masked below
+    for (int p = 0; p < P; ++p) w[c][p] = __builtin_nontemporal_load(pl + (size_t(ch) * P + p) * Npad + lr);
+  };
 #pragma unroll
-      for (int p = 0; p < P; ++p) w[c][p] = __builtin_nontemporal_load(pl + (size_t(ch) * P + p) * Npad + lr);
-      const int g = ch / a.group_chunks;
+  for (int c = 0; c < CPS; ++c) {
+    const int ch = min(s * CPS + c, Kc - 1);
+    const int g = ch / a.group_chunks;
+    if (!STAGED || c == 0) load_planes(c);
 #pragma unroll
-      for (int t = 0; t < S; ++t) sc[c][t] = a.scales[(size_t(t) * a.n_groups + g) * Npad + lr];
-    }
+    for (int t = 0; t < S; ++t) sc[c][t] = a.scales[(size_t(t) * a.n_groups + g) * Npad + lr];
   }
+  if constexpr (STAGED) __builtin_amdgcn_sched_barrier(0);
 
   // ---- prologue: (FWHT-256) -> 16-entry group tables of the whole K -------
 #pragma unroll
@@ -429,6 +457,11 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_fullk_kernel(GemvArgs 
       for (int d = 16; d >= 1; d >>= 1) xs += __shfl_xor(xs, d, 64);
       if ((lane & 31) == 0) xsum[ch] = xs;
     }
+  }
+  if constexpr (STAGED) {
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int c = 1; c < CPS; ++c) load_planes(c);
   }
   __syncthreads();
 
@@ -464,18 +497,25 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_fullk_kernel(GemvArgs 
   }
 }
 
-template <int FMT, int WAVES, int H, int CPS>
-static int launch_fullk_cfg(const GemvArgs &a, hipStream_t st) {
+template <int FMT, int WAVES, int H, int CPS, bool STAGED>
+static int launch_fullk_kernel(const GemvArgs &a, hipStream_t st) {
   const size_t lds = fullk_lds_bytes(WAVES, H, CPS, a.Kp / kChunk);
   static const hipError_t attr = hipFuncSetAttribute(
-      reinterpret_cast<const void *>(&lut_gemv_fullk_kernel<FMT, WAVES, H, CPS>),
+      reinterpret_cast<const void *>(&lut_gemv_fullk_kernel<FMT, WAVES, H, CPS, STAGED>),
       hipFuncAttributeMaxDynamicSharedMemorySize, int(kMaxLdsBytes));
   if (attr != hipSuccess) return fail(LMX_ERR_LAUNCH_FAILED, "hipFuncSetAttribute: %s", hipGetErrorString(attr));
   if (lds > kMaxLdsBytes) return fail(LMX_ERR_INVALID_ARGUMENT, "full-K tables need %zu B of LDS", lds);
   constexpr int RW = kWave / H;
-  lut_gemv_fullk_kernel<FMT, WAVES, H, CPS>
+  lut_gemv_fullk_kernel<FMT, WAVES, H, CPS, STAGED>
       <<<dim3((a.Npad + RW - 1) / RW), dim3(WAVES * kWave), lds, st>>>(a);
   return LMX_OK;
+}
+
+template <int FMT, int WAVES, int H, int CPS>
+static int launch_fullk_cfg(const GemvArgs &a, hipStream_t st) {
+  if constexpr (CPS > 1)
+    if (a.staged) return launch_fullk_kernel<FMT, WAVES, H, CPS, true>(a, st);
+  return launch_fullk_kernel<FMT, WAVES, H, CPS, false>(a, st);
 }
 
 template <int FMT, int WAVES>

@@ -201,3 +201,34 @@ def test_gemv_rejects_bad_arguments(cuda):
     w2 = L.Weight.from_planes(L.FMT_INT4, *synth.make_weights(L.FMT_INT4, 8, 768, seed=4)[:2], 8, 768, 128)
     with pytest.raises(L.LmxError):
         w2.gemv(torch.zeros(768, device="cuda"), flags=L.ROTATE_FWHT_FULL)   # 768 not a power of 2
+
+
+# ---- every kernel plan, forced ---------------------------------------------
+# (full-K configuration, rows, cols): shapes each configuration covers.
+PLAN_SHAPES = {
+    0: (300, 2560),   # split-K kernel
+    1: (96, 8192),    # 16 waves x 2 slices x 2 chunks
+    2: (96, 9216),    # 16 x 2 x 3 (planes <= 2 only)
+    3: (70, 2048),    # 8 x 2 x 1
+    4: (130, 1536),   # 16 x 1 x 1
+    5: (40, 8192),    # 16 x 4 x 1
+    6: (33, 2048),    # 4 x 4 x 1
+}
+
+
+@pytest.mark.parametrize("fmt", [1, 2, 3, 4, 5, 6, 7])
+@pytest.mark.parametrize("cfg", sorted(PLAN_SHAPES))
+@pytest.mark.parametrize("staged", [0, 1])
+def test_forced_kernel_plans(cuda, monkeypatch, fmt, cfg, staged):
+    rows, cols = PLAN_SHAPES[cfg]
+    monkeypatch.setenv("LMX_FULLK", str(cfg))
+    monkeypatch.setenv("LMX_STAGED", str(staged))
+    planes, scales, g = synth.make_weights(fmt, rows, cols, seed=cfg * 10 + fmt, group=128)
+    x = synth.make_activations(cols, seed=cfg + 40, outliers=True)
+    w = L.Weight.from_planes(fmt, planes, scales, rows, cols, g)
+    used, _, st = w.kernel_config()
+    fits = cfg == 0 or L.PLANES[fmt] * {1: 2, 2: 3}.get(cfg, 1) <= 8
+    assert used == (cfg if fits else 0) and st == staged
+    y = w.gemv(dev(x), flags=L.ROTATE_FWHT256).cpu().numpy()
+    ref = oracle_planes_gemv(fmt, planes, scales, rows, cols, g, x, L.ROTATE_FWHT256)
+    assert rel_max_err(y, ref) < TOL
