@@ -8,6 +8,9 @@ rotate over >= 512 MiB of distinct device copies so neither the 256 MB MALL
 nor the L2 holds them between launches.  The timed region is bracketed by
 torch.cuda.synchronize() and HIP events recorded on the stream the kernels
 are launched on; value = algorithmic bytes per GEMV / average time per GEMV.
+The K timed GEMVs are captured in one HIP graph and replayed (the launch
+path of a captured decode step); the per-launch stream time is reported
+beside it (--no-graph times only that).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--formats int4,ternary,...]
 """
@@ -29,7 +32,7 @@ ROTATE_BYTES = 512 * 2**20
 FORMATS = {"int4": 6, "ternary": 1, "binary": 2, "rrq2": 3, "rrq3": 4, "int8": 7}
 
 
-def gemv_bench(L, synth, torch, fmt, n, steps, warmup):
+def gemv_bench(L, synth, torch, fmt, n, steps, warmup, graph=True):
     """Time `steps` GEMVs of an n x n weight of format fmt; returns a dict."""
     group = 0 if fmt == L.FMT_TERNARY else 128
     planes, scales, g = synth.make_weights(fmt, n, n, seed=1000 + fmt, group=group)
@@ -45,15 +48,39 @@ def gemv_bench(L, synth, torch, fmt, n, steps, warmup):
         ws[i % copies].gemv(x, y, flags=flags, stream=stream)
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    # (a) one launch per GEMV on the stream
     start.record(stream)
     for i in range(steps):
         ws[i % copies].gemv(x, y, flags=flags, stream=stream)
     end.record(stream)
     torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / steps
+    ms_stream = start.elapsed_time(end) / steps
+    ms_graph = None
+    if graph:
+        # (b) the same `steps` launches captured once in a HIP graph and
+        # replayed: what a decode loop captured per token sees.
+        cg = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream()
+        side.wait_stream(stream)
+        with torch.cuda.graph(cg, stream=side):
+            for i in range(steps):
+                ws[i % copies].gemv(x, y, flags=flags)
+        stream.wait_stream(side)
+        cg.replay()                     # untimed: uploads the graph
+        torch.cuda.synchronize()
+        start.record(stream)
+        cg.replay()
+        end.record(stream)
+        torch.cuda.synchronize()
+        ms_graph = start.elapsed_time(end) / steps
+        del cg
+    ms = ms_graph if ms_graph is not None else ms_stream
     gbps = B / (ms * 1e-3) / 1e9
     out = {"format": L.FORMAT_NAMES[fmt], "rows": n, "cols": n, "group": g, "rotation": flags,
+           "kernel_plan": dict(zip(("fullk", "kslice", "staged"), ws[0].kernel_config())),
            "algorithmic_bytes": B, "us_per_gemv": round(ms * 1e3, 3), "GB_per_s": round(gbps, 1),
+           "launch": "hip_graph" if ms_graph is not None else "stream",
+           "us_per_gemv_stream_launch": round(ms_stream * 1e3, 3),
            "frac_of_peak": round(gbps / HBM_PEAK_GBPS, 4), "weight_copies": copies,
            "rotated_MiB": round(copies * B / 2**20, 1)}
     for w in ws:
@@ -126,6 +153,8 @@ def main():
     ap.add_argument("--formats", default="int4,ternary,binary,rrq2,rrq3,int8")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="time one stream launch per GEMV only (no HIP-graph replay)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain device copy of 35717120 bytes (counter calibration)")
     args = ap.parse_args()
@@ -145,7 +174,8 @@ def main():
     names = [f for f in args.formats.split(",") if f]
     sweep = {}
     for name in names:
-        r = gemv_bench(L, synth, torch, FORMATS[name], args.size, args.steps, args.warmup)
+        r = gemv_bench(L, synth, torch, FORMATS[name], args.size, args.steps, args.warmup,
+                       graph=not args.no_graph)
         sweep[name] = r
         print(f"# {name}: {r['us_per_gemv']} us/GEMV, {r['GB_per_s']} GB/s "
               f"({100 * r['frac_of_peak']:.1f}% of peak)", file=sys.stderr, flush=True)
