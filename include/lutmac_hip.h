@@ -14,7 +14,7 @@
  *
  * Activation/output pointers passed to lmx_gemv/lmx_linear and the debug
  * kernels are DEVICE pointers; the host-pointer wrappers with the
- * reference's exact signatures live in lutmac_amd/csrc/lut_gemm_compat.hpp.
+ * reference's exact signatures live in lutmac_hip_compat.h.
  */
 #ifndef LUTMAC_HIP_H
 #define LUTMAC_HIP_H

@@ -1,21 +1,22 @@
 // lmx_kernels.hip -- gfx950 kernels of the bit-serial LUT-GEMV path.
 //
-// One GEMV = one launch of lut_gemv_kernel<FMT, CHUNKS>:
-//   * a workgroup owns 256 output rows (4 wavefronts, one row per lane) and a
-//     k-slice of CHUNKS*128 activations;
-//   * prologue (fused): each wavefront takes one 256-chunk of x, rotates it
-//     with an in-register FWHT-256 (butterflies across lanes via shuffles)
+// One GEMV is one launch of lut_gemv_fullk_kernel where its tables fit, or
+// lut_gemv_kernel (split-K) + splitk_reduce_kernel elsewhere.  Both share:
+//   * a fused prologue: each wavefront takes 256-chunks of x, rotates them
+//     with an in-register FWHT-256 (cross-lane butterflies via shuffles)
 //     when asked, and writes the 16-entry partial-sum table of every group
-//     of 4 activations straight into LDS (lane l owns group l of the chunk);
-//   * main loop: every lane streams its row's bit-planes (one 16-byte load
-//     per plane per 128-k chunk, 1 KiB contiguous per wavefront), turns each
-//     plane nibble into an LDS address with one v_perm and accumulates the
-//     looked-up partial sums in fp32.  All 64 lanes read the same 16-entry
-//     table at a time, so a lookup touches 16 consecutive dwords: no bank
-//     conflicts, broadcast for equal indices;
-//   * split-K: each workgroup writes one partial per row; the last workgroup
-//     of a row block (atomic ticket) sums the partials in split order, adds
-//     the bias and writes y, so results do not depend on scheduling.
+//     of 4 activations straight into LDS (lane l owns group l of a chunk);
+//   * the lookup loop: every lane streams one row's bit-planes (one 16-byte
+//     non-temporal load per plane per 128-k chunk, 1 KiB contiguous per
+//     wavefront), turns each plane nibble into an LDS address with one
+//     v_perm and accumulates the looked-up partial sums in fp32.  All 64
+//     lanes read the same 16-entry table at a time, so a lookup touches 16
+//     consecutive dwords: no bank conflicts;
+//   * deterministic reductions (fixed slice order, no float atomics).
+// Full-K: a workgroup owns 64/H rows and the whole K (tables of the whole K
+// in LDS), k-slices spread over its lanes, slice partials summed in LDS.
+// Split-K: a workgroup owns 64*WAVES rows x one k-slice and writes one
+// partial per row; a second kernel (or the last workgroup) sums them.
 //
 // Per-format identities (T = group table, m_p = plane-p nibble, ~ = 4-bit
 // complement, xs = sum of the chunk's activations):

@@ -11,7 +11,7 @@
 //
 // The reference functions return void and have no error channel; these
 // entry points return an lmx_status, and the C++ wrappers in
-// lut_gemm_compat.hpp abort with the message on failure (never a silent CPU
+// include/lutmac_hip_compat.h abort with the message on failure (never a silent CPU
 // fallback).
 #include <hip/hip_runtime.h>
 
