@@ -37,7 +37,22 @@ EXPORTS = [
     # include/lutmac_hip_compat.h
     "lmx_host_gemv", "lmx_host_lut_linear", "lmx_host_apply_hadamard_rotation",
     "lmx_host_precompute_luts",
+    # include/lutmac_decode.h
+    "lmx_decoder_create", "lmx_decoder_destroy", "lmx_decoder_set_layer", "lmx_decoder_set_head",
+    "lmx_decoder_reset", "lmx_decoder_step", "lmx_decoder_tokens", "lmx_decoder_generate",
+    # include/lutmac_synth.h
+    "lmx_quantize_int4", "lmx_synth_int4_normal", "lmx_synth_normal",
 ]
+
+
+class DecoderConfigC(ctypes.Structure):
+    """lmx_decoder_config (include/lutmac_decode.h)."""
+    _fields_ = [("hidden", ctypes.c_size_t), ("n_layers", ctypes.c_size_t), ("n_heads", ctypes.c_size_t),
+                ("n_kv_heads", ctypes.c_size_t), ("head_dim", ctypes.c_size_t), ("ffn", ctypes.c_size_t),
+                ("vocab", ctypes.c_size_t), ("max_seq", ctypes.c_size_t), ("rms_eps", ctypes.c_float),
+                ("rope_theta", ctypes.c_float), ("rope_mode", ctypes.c_int), ("rope_factor", ctypes.c_float),
+                ("rope_low_freq_factor", ctypes.c_float), ("rope_high_freq_factor", ctypes.c_float),
+                ("rope_orig_max_pos", ctypes.c_size_t)]
 
 
 class LmxError(RuntimeError):
@@ -79,6 +94,18 @@ _SIGS = {
     "lmx_host_gemv": ([_i, _p, _sz, _p, _p, _sz, _sz], _i),
     "lmx_host_lut_linear": ([_i, _p, _sz, _p, _p, _p, _sz, _sz, _sz], _i),
     "lmx_host_apply_hadamard_rotation": ([_p, _sz], _i),
+    "lmx_quantize_int4": ([_p, _sz, _sz, _sz, _p, _p], _i),
+    "lmx_synth_int4_normal": ([ctypes.c_uint64, ctypes.c_uint64, _sz, _sz, ctypes.c_float, _sz, _p, _p], _i),
+    "lmx_synth_normal": ([ctypes.c_uint64, ctypes.c_uint64, _sz, _sz, ctypes.c_float, _p], _i),
+    "lmx_decoder_create": ([ctypes.POINTER(DecoderConfigC), ctypes.POINTER(_p)], _i),
+    "lmx_decoder_destroy": ([_p], _i),
+    "lmx_decoder_set_layer": ([_p, _sz, _p, _p, _p, _p, _p, _p, _p], _i),
+    "lmx_decoder_set_head": ([_p, _p, _p], _i),
+    "lmx_decoder_reset": ([_p, _p, _sz], _i),
+    "lmx_decoder_step": ([_p, _p, _p], _i),
+    "lmx_decoder_tokens": ([_p, _p, _sz, _p], _i),
+    "lmx_decoder_generate": ([_p, _p, _sz, _sz, _p, ctypes.POINTER(ctypes.c_float),
+                              ctypes.POINTER(ctypes.c_float), _p], _i),
     "lmx_host_precompute_luts": ([_p, _sz, _p], _i),
 }
 
@@ -167,6 +194,31 @@ def untile_planes(fmt, tiles, rows, cols):
     tiles = np.ascontiguousarray(tiles, np.uint8)
     check(lib().lmx_untile_planes(fmt, _np_ptr(tiles), rows, cols, _np_ptr(out)))
     return out
+
+
+def quantize_int4(w, group):
+    """fp32 [rows, cols] -> (planes [4, rows, cols/8], scales [1, rows, cols/group]) with the
+    reference's 4-bit rule per group (lmx_quantize_int4)."""
+    w = np.ascontiguousarray(w, np.float32)
+    rows, cols = w.shape
+    planes = np.zeros((4, rows, cols // 8), np.uint8)
+    scales = np.zeros((1, rows, cols // group), np.float32)
+    check(lib().lmx_quantize_int4(_np_ptr(w), rows, cols, group, _np_ptr(planes), _np_ptr(scales)))
+    return planes, scales
+
+
+def synth_int4_normal(seed, stream, rows, cols, std, group):
+    """Seeded N(0, std^2) weights quantized to 4-bit planes (lmx_synth_int4_normal)."""
+    planes = np.zeros((4, rows, cols // 8), np.uint8)
+    scales = np.zeros((1, rows, cols // group), np.float32)
+    check(lib().lmx_synth_int4_normal(seed, stream, rows, cols, std, group, _np_ptr(planes), _np_ptr(scales)))
+    return planes, scales
+
+
+def synth_normal(seed, stream, rows, cols, std):
+    w = np.zeros((rows, cols), np.float32)
+    check(lib().lmx_synth_normal(seed, stream, rows, cols, std, _np_ptr(w)))
+    return w
 
 
 def device_count():

@@ -25,9 +25,11 @@ DEVICE = ["-x", "hip", f"--offload-arch={ARCH}",
 
 SOURCES = [
     ("lmx_kernels.hip", True),
+    ("lmx_decode.hip", True),
     ("lmx_capi.cpp", False),
     ("lmx_repack.cpp", False),
     ("lut_gemm_compat.cpp", False),
+    ("lmx_synth.cpp", False),
 ]
 
 

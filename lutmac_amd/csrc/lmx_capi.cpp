@@ -217,6 +217,28 @@ int stage_if_needed(const lmx_weight *w, GemvArgs &a, void *stream) {
 }
 
 }  // namespace
+
+GemvArgs weight_args(const lmx_weight *w) {
+  GemvArgs a{};
+  a.planes = w->d_planes;
+  a.scales = w->d_scales;
+  a.partials = w->d_partials;
+  a.counters = w->d_counters;
+  a.rows = int(w->rows);
+  a.Npad = int(w->Npad);
+  a.cols = int(w->cols);
+  a.Kp = int(w->Kp);
+  a.group_chunks = int(w->group / kChunk);
+  a.n_groups = int(w->n_groups);
+  a.kslice = w->kslice;
+  a.reduce = w->reduce;
+  a.waves = w->waves;
+  a.fullk = w->fullk;
+  a.staged = w->staged;
+  a.xmode = kXModeNone;
+  return a;
+}
+
 }  // namespace lmx
 
 using namespace lmx;
@@ -403,23 +425,7 @@ int lmx_gemv(const lmx_weight *w, const float *x, float *y, size_t batch, unsign
   if (flags == LMX_ROTATE_FWHT_FULL && (!is_pow2(w->cols) || w->cols < 256 || w->cols > 16384))
     return fail(LMX_ERR_INVALID_ARGUMENT, "length-K FWHT needs cols a power of two in [256, 16384], got %zu",
                 w->cols);
-  GemvArgs a{};
-  a.planes = w->d_planes;
-  a.scales = w->d_scales;
-  a.bias = nullptr;
-  a.partials = w->d_partials;
-  a.counters = w->d_counters;
-  a.rows = int(w->rows);
-  a.Npad = int(w->Npad);
-  a.cols = int(w->cols);
-  a.Kp = int(w->Kp);
-  a.group_chunks = int(w->group / kChunk);
-  a.n_groups = int(w->n_groups);
-  a.kslice = w->kslice;
-  a.reduce = w->reduce;
-  a.waves = w->waves;
-  a.fullk = w->fullk;
-  a.staged = w->staged;
+  GemvArgs a = weight_args(w);
   for (size_t b = 0; b < batch; ++b) {
     a.x = x + b * w->cols;
     a.y = y + b * w->rows;
@@ -445,23 +451,8 @@ int lmx_linear(const lmx_weight *w, const float *bias, const float *x, float *y,
   if (batch == 0) return LMX_OK;
   const bool rotate = w->format == LMX_FMT_TERNARY || w->format == LMX_FMT_BINARY ||
                       w->format == LMX_FMT_RRQ2 || w->format == LMX_FMT_RRQ3;
-  GemvArgs a{};
-  a.planes = w->d_planes;
-  a.scales = w->d_scales;
+  GemvArgs a = weight_args(w);
   a.bias = bias;
-  a.partials = w->d_partials;
-  a.counters = w->d_counters;
-  a.rows = int(w->rows);
-  a.Npad = int(w->Npad);
-  a.cols = int(w->cols);
-  a.Kp = int(w->Kp);
-  a.group_chunks = int(w->group / kChunk);
-  a.n_groups = int(w->n_groups);
-  a.kslice = w->kslice;
-  a.reduce = w->reduce;
-  a.waves = w->waves;
-  a.fullk = w->fullk;
-  a.staged = w->staged;
   a.rotate = rotate ? LMX_ROTATE_FWHT256 : LMX_ROTATE_NONE;
   for (size_t b = 0; b < batch; ++b) {
     a.x = x + b * w->cols;

@@ -1,0 +1,615 @@
+// lmx_decode.hip -- device-resident batch-1 decoder forward (lutmac_decode.h).
+//
+// A token step is Model::forward(token, pos) + greedy Model::sample
+// (src/model.cpp:47-453, 455-490) with every op on the GPU:
+//   embed_kernel           row `token` of the tied table, dequantized from the
+//                          tile layout (model.cpp:58-85)
+//   per layer:
+//     GEMV qkv             RMSNorm(input_norm) fused into the table prologue,
+//                          q|k|v rows in one weight, + bias (model.cpp:296-323)
+//     attention_kernel     RoPE of q and k, KV-cache append, scores, softmax,
+//                          weighted V sum for the query heads of one KV head
+//                          (model.cpp:326-372, embedding.cpp:36-75,
+//                          attention.cpp:23-42)
+//     GEMV o               + residual: the hidden state is the bias and the
+//                          output (model.cpp:376-388)
+//     GEMV gate|up         RMSNorm(post_norm) fused (model.cpp:390-403)
+//     GEMV down            SiLU(gate)*up fused into the prologue, + residual
+//                          (model.cpp:410-426)
+//   GEMV head              RMSNorm(final_norm) fused, tied table (model.cpp:433-447)
+//   argmax_kernel          first maximum (model.cpp:480-490); writes the next
+//                          token and advances the device position
+// The position and the token sequence live in device memory, so the same
+// captured step replays for every position.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstring>
+#include <vector>
+
+#include "lmx_internal.hpp"
+#include "lutmac_decode.h"
+
+namespace lmx {
+namespace {
+
+template <int FMT> struct EmbFmt;
+template <> struct EmbFmt<LMX_FMT_TERNARY> { static constexpr int P = 2, S = 1; };
+template <> struct EmbFmt<LMX_FMT_BINARY> { static constexpr int P = 1, S = 1; };
+template <> struct EmbFmt<LMX_FMT_RRQ2> { static constexpr int P = 2, S = 2; };
+template <> struct EmbFmt<LMX_FMT_RRQ3> { static constexpr int P = 3, S = 3; };
+template <> struct EmbFmt<LMX_FMT_INT3> { static constexpr int P = 3, S = 1; };
+template <> struct EmbFmt<LMX_FMT_INT4> { static constexpr int P = 4, S = 1; };
+template <> struct EmbFmt<LMX_FMT_INT8> { static constexpr int P = 8, S = 1; };
+
+// Weight value from its plane bits and scales (the block accessors of
+// types.hpp: BitPlaneBlock 140-160, BinaryBlock::get 404-411, Int2Block::get
+// 217-234 generalised to k stages, Int3Block 270-285, Int4Block::get 186-190,
+// Int8Block::get 448-460).
+template <int FMT>
+__device__ __forceinline__ float weight_value(const int *b, const float *s) {
+  if constexpr (FMT == LMX_FMT_TERNARY) {
+    return b[1] ? 0.0f : (b[0] ? -1.0f : 1.0f) * s[0];
+  } else if constexpr (FMT == LMX_FMT_BINARY) {
+    return b[0] ? s[0] : -s[0];
+  } else if constexpr (FMT == LMX_FMT_RRQ2 || FMT == LMX_FMT_RRQ3) {
+    float v = 0.0f;
+#pragma unroll
+    for (int i = 0; i < EmbFmt<FMT>::S; ++i) v += b[i] ? s[i] : -s[i];
+    return v;
+  } else {
+    int q = 0;
+#pragma unroll
+    for (int p = 0; p < EmbFmt<FMT>::P; ++p) q |= b[p] << p;
+    if constexpr (FMT == LMX_FMT_INT3) return float(q - 4) * s[0];
+    if constexpr (FMT == LMX_FMT_INT4) return float(q - 8) * s[0];
+    return float(int(int8_t(uint8_t(q)))) * s[0];
+  }
+}
+
+// hidden[k] = W[token][k] from the tile layout [Kp/128][P][Npad][16 B] and
+// scales [S][n_groups][Npad]; one weight per thread.
+template <int FMT>
+__global__ __launch_bounds__(256) void embed_kernel(const uint8_t *__restrict__ planes, const float *__restrict__ scales,
+                                                    int Npad, int rows, int n_groups, int group_chunks, int cols,
+                                                    const int *__restrict__ tokens, const int *__restrict__ pos,
+                                                    float *__restrict__ out) {
+  constexpr int P = EmbFmt<FMT>::P, S = EmbFmt<FMT>::S;
+  const int k = blockIdx.x * 256 + threadIdx.x;
+  if (k >= cols) return;
+  const int t = min(max(tokens[*pos], 0), rows - 1);
+  const int c = k / kChunk, byte = (k % kChunk) / 8, bit = 7 - k % 8;
+  int b[P];
+#pragma unroll
+  for (int p = 0; p < P; ++p) b[p] = (planes[((size_t(c) * P + p) * Npad + t) * 16 + byte] >> bit) & 1;
+  const int g = c / group_chunks;
+  float s[S];
+#pragma unroll
+  for (int i = 0; i < S; ++i) s[i] = scales[(size_t(i) * n_groups + g) * Npad + t];
+  out[k] = weight_value<FMT>(b, s);
+}
+
+// RoPE + KV append + attention for the `group` query heads of KV head
+// blockIdx.x; wave w < group serves query head blockIdx.x * group + w.
+// LDS: probabilities [group][max_seq], rotated queries [group][HD].
+template <int HD>
+__global__ __launch_bounds__(1024) void attention_kernel(const float *__restrict__ qkv, float *__restrict__ kc,
+                                                         float *__restrict__ vc, const int *__restrict__ pos_p,
+                                                         const float *__restrict__ freq, float pos_div, int n_heads,
+                                                         int n_kv, int group, int max_seq, float scale,
+                                                         float *__restrict__ out) {
+  extern __shared__ float lds[];
+  constexpr int HALF = HD / 2;
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  const int kvh = blockIdx.x;
+  const int pos = min(*pos_p, max_seq - 1);
+  const int seq = pos + 1;
+  const float pf = float(pos) / pos_div;
+  const size_t row = size_t(n_kv) * HD;   // floats per cache position
+  float *p = lds + wave * max_seq;
+  float *qs = lds + group * max_seq + wave * HD;
+
+  // (a) rotate k of this KV head and append k, v at `pos`
+  if (wave == 0) {
+    const float *kin = qkv + size_t(n_heads) * HD + kvh * HD;
+    const float *vin = kin + row;
+    float *kd = kc + size_t(pos) * row + kvh * HD;
+    float *vd = vc + size_t(pos) * row + kvh * HD;
+    for (int d = lane; d < HALF; d += kWave) {
+      float sn, cs;
+      sincosf(pf * freq[d], &sn, &cs);
+      const float k0 = kin[d], k1 = kin[d + HALF];
+      kd[d] = k0 * cs - k1 * sn;
+      kd[d + HALF] = k0 * sn + k1 * cs;
+    }
+    for (int d = lane; d < HD; d += kWave) vd[d] = vin[d];
+  }
+  // (b) rotate this wave's query head into LDS
+  if (wave < group) {
+    const float *qin = qkv + size_t(kvh * group + wave) * HD;
+    for (int d = lane; d < HALF; d += kWave) {
+      float sn, cs;
+      sincosf(pf * freq[d], &sn, &cs);
+      const float q0 = qin[d], q1 = qin[d + HALF];
+      qs[d] = q0 * cs - q1 * sn;
+      qs[d + HALF] = q0 * sn + q1 * cs;
+    }
+  }
+  __syncthreads();
+
+  // (c) scores q.k_t * scale, lanes over positions; running max
+  float mx = -INFINITY;
+  if (wave < group) {
+    for (int t = lane; t < seq; t += kWave) {
+      const float4 *kr = reinterpret_cast<const float4 *>(kc + size_t(t) * row + kvh * HD);
+      float sc = 0.0f;
+#pragma unroll 4
+      for (int d4 = 0; d4 < HD / 4; ++d4) {
+        const float4 kv = kr[d4];
+        sc += qs[4 * d4] * kv.x;
+        sc += qs[4 * d4 + 1] * kv.y;
+        sc += qs[4 * d4 + 2] * kv.z;
+        sc += qs[4 * d4 + 3] * kv.w;
+      }
+      sc *= scale;
+      p[t] = sc;
+      mx = fmaxf(mx, sc);
+    }
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) mx = fmaxf(mx, __shfl_xor(mx, d, 64));
+  }
+  __syncthreads();
+  // (d) softmax (attention.cpp:23-42): exp(x - max), sum, x * (1/sum)
+  float sum = 0.0f;
+  if (wave < group) {
+    for (int t = lane; t < seq; t += kWave) {
+      const float e = expf(p[t] - mx);
+      p[t] = e;
+      sum += e;
+    }
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) sum += __shfl_xor(sum, d, 64);
+    const float inv = 1.0f / sum;
+    for (int t = lane; t < seq; t += kWave) p[t] *= inv;
+  }
+  __syncthreads();
+  // (e) out[d] = sum_t p_t * v_t[d], lanes over d
+  if (wave < group) {
+    float *o = out + size_t(kvh * group + wave) * HD;
+    const float *vb = vc + kvh * HD;
+#pragma unroll
+    for (int d0 = 0; d0 < HD; d0 += kWave) {
+      float acc = 0.0f;
+      const float *vd = vb + d0 + lane;
+      for (int t = 0; t < seq; ++t) acc += p[t] * vd[size_t(t) * row];
+      o[d0 + lane] = acc;
+    }
+  }
+}
+
+// First maximum of logits[0..V) (strict >, so the lowest index wins ties).
+// Thread 0 writes it to tokens[pos + 1] unless that position is forced and
+// advances the device position.
+__global__ __launch_bounds__(1024) void argmax_kernel(const float *__restrict__ logits, int V, int *__restrict__ tokens,
+                                                      int *__restrict__ pos_p, int n_forced, int max_pos) {
+  __shared__ float bv[16];
+  __shared__ int bi[16];
+  float best = -INFINITY;
+  int idx = 0x7fffffff;
+  for (int i = threadIdx.x; i < V; i += 1024) {
+    const float v = logits[i];
+    if (v > best) best = v, idx = i;
+  }
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) {
+    const float ob = __shfl_xor(best, d, 64);
+    const int oi = __shfl_xor(idx, d, 64);
+    if (ob > best || (ob == best && oi < idx)) best = ob, idx = oi;
+  }
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  if (lane == 0) bv[wave] = best, bi[wave] = idx;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < 16; ++w)
+      if (bv[w] > best || (bv[w] == best && bi[w] < idx)) best = bv[w], idx = bi[w];
+    if (idx == 0x7fffffff) idx = 0;   // no finite maximum: the reference's initial best
+    const int pos = *pos_p;
+    if (pos + 1 >= n_forced && pos + 1 <= max_pos) tokens[pos + 1] = idx;
+    *pos_p = pos + 1;
+  }
+}
+
+int hip_err(hipError_t e, const char *what) {
+  if (e == hipErrorOutOfMemory) return fail(LMX_ERR_OUT_OF_MEMORY, "%s: %s", what, hipGetErrorString(e));
+  return fail(LMX_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+int launch_err(const char *what) {
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? LMX_OK : fail(LMX_ERR_LAUNCH_FAILED, "%s launch: %s", what, hipGetErrorString(e));
+}
+
+bool rotates(int fmt) {   // lut_gemm_scalar.cpp:88-96: ternary and 1/2-bit inputs are rotated
+  return fmt == LMX_FMT_TERNARY || fmt == LMX_FMT_BINARY || fmt == LMX_FMT_RRQ2 || fmt == LMX_FMT_RRQ3;
+}
+
+// Frequencies theta^(-2d/hd) for d < hd/2, Llama-3 scaled when asked.
+std::vector<float> rope_freqs(const lmx_decoder_config &c) {
+  const int hd = int(c.head_dim);
+  std::vector<float> f(hd / 2);
+  for (int d = 0; d < hd / 2; ++d) {
+    if (c.rope_mode == LMX_ROPE_REFERENCE) {
+      f[d] = 1.0f / std::pow(c.rope_theta, (2.0f * float(d)) / float(hd));   // embedding.cpp:46
+      continue;
+    }
+    const double inv = 1.0 / std::pow(double(c.rope_theta), 2.0 * d / hd);
+    const double lo_wl = double(c.rope_orig_max_pos) / c.rope_low_freq_factor;
+    const double hi_wl = double(c.rope_orig_max_pos) / c.rope_high_freq_factor;
+    const double wl = 2.0 * 3.14159265358979323846 / inv;
+    double v;
+    if (wl < hi_wl) {
+      v = inv;
+    } else if (wl > lo_wl) {
+      v = inv / c.rope_factor;
+    } else {
+      const double sm = (double(c.rope_orig_max_pos) / wl - c.rope_low_freq_factor) /
+                        (c.rope_high_freq_factor - c.rope_low_freq_factor);
+      v = (1.0 - sm) * inv / c.rope_factor + sm * inv;
+    }
+    f[d] = float(v);
+  }
+  return f;
+}
+
+size_t attn_lds_bytes(const lmx_decoder_config &c) {
+  const size_t group = c.n_heads / c.n_kv_heads;
+  return group * (c.max_seq + c.head_dim) * sizeof(float);
+}
+
+}  // namespace
+}  // namespace lmx
+
+using namespace lmx;
+
+struct lmx_decoder {
+  lmx_decoder_config cfg{};
+  int device = 0;
+  struct Layer {
+    const lmx_weight *qkv = nullptr, *o = nullptr, *gate_up = nullptr, *down = nullptr;
+    float *in_norm = nullptr, *post_norm = nullptr, *qkv_bias = nullptr;
+  };
+  std::vector<Layer> layers;
+  const lmx_weight *head = nullptr;
+  float *final_norm = nullptr;
+  float *hidden = nullptr, *qkv = nullptr, *attn = nullptr, *gate_up = nullptr, *logits = nullptr;
+  float *kcache = nullptr, *vcache = nullptr, *freq = nullptr;
+  int *tokens = nullptr, *pos = nullptr;
+  int n_forced = 0;
+  size_t host_pos = 0;
+  float pos_div = 1.0f;
+  std::vector<void *> allocs;
+  hipStream_t stream = nullptr;   // capture/replay stream of lmx_decoder_generate
+
+  int alloc(void **p, size_t bytes) {
+    hipError_t e = hipMalloc(p, bytes);
+    if (e != hipSuccess) return hip_err(e, "hipMalloc (decoder)");
+    allocs.push_back(*p);
+    e = hipMemset(*p, 0, bytes);
+    return e == hipSuccess ? LMX_OK : hip_err(e, "hipMemset (decoder)");
+  }
+  ~lmx_decoder() {
+    if (stream) (void)hipStreamDestroy(stream);
+    for (void *p : allocs) (void)hipFree(p);
+  }
+};
+
+namespace {
+
+int gemv(const lmx_weight *w, const float *x, float *y, const float *bias, int xmode, const float *xw, float eps,
+         hipStream_t st) {
+  GemvArgs a = weight_args(w);
+  a.x = x;
+  a.y = y;
+  a.bias = bias;
+  a.rotate = rotates(w->format) ? LMX_ROTATE_FWHT256 : LMX_ROTATE_NONE;
+  a.xmode = xmode;
+  a.xw = xw;
+  a.eps = eps;
+  return launch_gemv(w->format, a, st);
+}
+
+template <int FMT>
+void launch_embed(const lmx_weight *w, const int *tokens, const int *pos, float *out, hipStream_t st) {
+  embed_kernel<FMT><<<dim3(unsigned((w->cols + 255) / 256)), dim3(256), 0, st>>>(
+      static_cast<const uint8_t *>(w->d_planes), w->d_scales, int(w->Npad), int(w->rows), int(w->n_groups),
+      int(w->group / kChunk), int(w->cols), tokens, pos, out);
+}
+
+int embed(const lmx_weight *w, const int *tokens, const int *pos, float *out, hipStream_t st) {
+  switch (w->format) {
+  case LMX_FMT_TERNARY: launch_embed<LMX_FMT_TERNARY>(w, tokens, pos, out, st); break;
+  case LMX_FMT_BINARY: launch_embed<LMX_FMT_BINARY>(w, tokens, pos, out, st); break;
+  case LMX_FMT_RRQ2: launch_embed<LMX_FMT_RRQ2>(w, tokens, pos, out, st); break;
+  case LMX_FMT_RRQ3: launch_embed<LMX_FMT_RRQ3>(w, tokens, pos, out, st); break;
+  case LMX_FMT_INT3: launch_embed<LMX_FMT_INT3>(w, tokens, pos, out, st); break;
+  case LMX_FMT_INT4: launch_embed<LMX_FMT_INT4>(w, tokens, pos, out, st); break;
+  case LMX_FMT_INT8: launch_embed<LMX_FMT_INT8>(w, tokens, pos, out, st); break;
+  default: return fail(LMX_ERR_UNSUPPORTED_FORMAT, "embedding format %d", w->format);
+  }
+  return launch_err("embed");
+}
+
+int attention(lmx_decoder *d, size_t layer, hipStream_t st) {
+  const lmx_decoder_config &c = d->cfg;
+  const int group = int(c.n_heads / c.n_kv_heads);
+  const size_t lds = attn_lds_bytes(c);
+  const size_t per_layer = c.max_seq * c.n_kv_heads * c.head_dim;
+  float *kc = d->kcache + layer * per_layer, *vc = d->vcache + layer * per_layer;
+  const float scale = 1.0f / std::sqrt(float(c.head_dim));   // model.cpp:337
+  if (c.head_dim == 64)
+    attention_kernel<64><<<dim3(unsigned(c.n_kv_heads)), dim3(unsigned(group * kWave)), lds, st>>>(
+        d->qkv, kc, vc, d->pos, d->freq, d->pos_div, int(c.n_heads), int(c.n_kv_heads), group, int(c.max_seq), scale,
+        d->attn);
+  else
+    attention_kernel<128><<<dim3(unsigned(c.n_kv_heads)), dim3(unsigned(group * kWave)), lds, st>>>(
+        d->qkv, kc, vc, d->pos, d->freq, d->pos_div, int(c.n_heads), int(c.n_kv_heads), group, int(c.max_seq), scale,
+        d->attn);
+  return launch_err("attention");
+}
+
+int check_shape(const lmx_weight *w, size_t rows, size_t cols, const char *what) {
+  if (!w) return fail(LMX_ERR_INVALID_ARGUMENT, "%s weight is NULL", what);
+  if (w->rows != rows || w->cols != cols)
+    return fail(LMX_ERR_INVALID_ARGUMENT, "%s weight is %zu x %zu, expected %zu x %zu", what, w->rows, w->cols, rows,
+                cols);
+  return LMX_OK;
+}
+
+int upload(lmx_decoder *d, float **dst, const float *src, size_t n) {
+  int st = d->alloc(reinterpret_cast<void **>(dst), n * sizeof(float));
+  if (st) return st;
+  hipError_t e = hipMemcpy(*dst, src, n * sizeof(float), hipMemcpyHostToDevice);
+  return e == hipSuccess ? LMX_OK : hip_err(e, "hipMemcpy (decoder weights)");
+}
+
+int step(lmx_decoder *d, float *logits_out, hipStream_t st) {
+  const lmx_decoder_config &c = d->cfg;
+  int r = embed(d->head, d->tokens, d->pos, d->hidden, st);
+  if (r) return r;
+  for (size_t l = 0; l < c.n_layers; ++l) {
+    const lmx_decoder::Layer &L = d->layers[l];
+    if ((r = gemv(L.qkv, d->hidden, d->qkv, L.qkv_bias, kXModeRmsNorm, L.in_norm, c.rms_eps, st)) ||
+        (r = attention(d, l, st)) ||
+        (r = gemv(L.o, d->attn, d->hidden, d->hidden, kXModeNone, nullptr, 0.0f, st)) ||
+        (r = gemv(L.gate_up, d->hidden, d->gate_up, nullptr, kXModeRmsNorm, L.post_norm, c.rms_eps, st)) ||
+        (r = gemv(L.down, d->gate_up, d->hidden, d->hidden, kXModeSiluMul, nullptr, 0.0f, st)))
+      return r;
+  }
+  float *lg = logits_out ? logits_out : d->logits;
+  if ((r = gemv(d->head, d->hidden, lg, nullptr, kXModeRmsNorm, d->final_norm, c.rms_eps, st))) return r;
+  argmax_kernel<<<dim3(1), dim3(1024), 0, st>>>(lg, int(c.vocab), d->tokens, d->pos, d->n_forced, int(c.max_seq));
+  return launch_err("argmax");
+}
+
+int ready(const lmx_decoder *d) {
+  if (!d) return fail(LMX_ERR_INVALID_ARGUMENT, "decoder is NULL");
+  if (!d->head) return fail(LMX_ERR_INVALID_ARGUMENT, "decoder head not set");
+  for (size_t l = 0; l < d->layers.size(); ++l)
+    if (!d->layers[l].qkv) return fail(LMX_ERR_INVALID_ARGUMENT, "decoder layer %zu not set", l);
+  return LMX_OK;
+}
+
+int set_position(lmx_decoder *d, const int32_t *tokens, size_t n, hipStream_t st) {
+  if (n == 0 || n > d->cfg.max_seq) return fail(LMX_ERR_INVALID_ARGUMENT, "%zu tokens for max_seq %zu", n, d->cfg.max_seq);
+  for (size_t i = 0; i < n; ++i)
+    if (tokens[i] < 0 || size_t(tokens[i]) >= d->cfg.vocab)
+      return fail(LMX_ERR_INVALID_ARGUMENT, "token %d at %zu outside the vocabulary", tokens[i], i);
+  const int zero = 0;
+  hipError_t e = hipMemcpyAsync(d->tokens, tokens, n * sizeof(int32_t), hipMemcpyHostToDevice, st);
+  if (e == hipSuccess) e = hipMemcpyAsync(d->pos, &zero, sizeof(int), hipMemcpyHostToDevice, st);
+  if (e == hipSuccess) e = hipStreamSynchronize(st);
+  if (e != hipSuccess) return hip_err(e, "decoder reset");
+  d->n_forced = int(n);
+  d->host_pos = 0;
+  return LMX_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int lmx_decoder_create(const lmx_decoder_config *cfg, lmx_decoder **out) {
+  if (!cfg || !out) return fail(LMX_ERR_INVALID_ARGUMENT, "NULL argument");
+  *out = nullptr;
+  const lmx_decoder_config &c = *cfg;
+  if (!c.hidden || !c.n_layers || !c.n_heads || !c.n_kv_heads || !c.ffn || !c.vocab || !c.max_seq)
+    return fail(LMX_ERR_INVALID_ARGUMENT, "decoder sizes must be non-zero");
+  if (c.head_dim != 64 && c.head_dim != 128) return fail(LMX_ERR_INVALID_ARGUMENT, "head_dim must be 64 or 128");
+  if (c.n_heads % c.n_kv_heads || c.n_heads / c.n_kv_heads > 16)
+    return fail(LMX_ERR_INVALID_ARGUMENT, "n_heads must be a multiple of n_kv_heads, at most 16 per KV head");
+  if (c.hidden % 4 || c.ffn % 4 || (c.n_heads * c.head_dim) % 4)
+    return fail(LMX_ERR_INVALID_ARGUMENT, "hidden, ffn and n_heads*head_dim must be multiples of 4");
+  if (c.max_seq > (1u << 24)) return fail(LMX_ERR_INVALID_ARGUMENT, "max_seq too large");
+  if (attn_lds_bytes(c) > kMaxLdsBytes)
+    return fail(LMX_ERR_INVALID_ARGUMENT, "max_seq %zu needs %zu B of LDS for attention (max %zu)", c.max_seq,
+                attn_lds_bytes(c), size_t(kMaxLdsBytes));
+  if (c.rope_mode != LMX_ROPE_REFERENCE && c.rope_mode != LMX_ROPE_LLAMA3)
+    return fail(LMX_ERR_INVALID_ARGUMENT, "unknown rope mode %d", c.rope_mode);
+  if (c.rope_mode == LMX_ROPE_REFERENCE && !(c.rope_factor > 0.0f))
+    return fail(LMX_ERR_INVALID_ARGUMENT, "rope factor must be positive");
+  if (c.rope_mode == LMX_ROPE_LLAMA3 &&
+      !(c.rope_factor > 0.0f && c.rope_high_freq_factor > c.rope_low_freq_factor && c.rope_orig_max_pos > 0))
+    return fail(LMX_ERR_INVALID_ARGUMENT, "invalid llama3 rope scaling parameters");
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(LMX_ERR_NO_DEVICE, "hipGetDevice: %s", hipGetErrorString(e));
+  lmx_decoder *d = new (std::nothrow) lmx_decoder();
+  if (!d) return fail(LMX_ERR_OUT_OF_MEMORY, "decoder allocation");
+  d->cfg = c;
+  d->device = dev;
+  d->layers.resize(c.n_layers);
+  d->pos_div = c.rope_mode == LMX_ROPE_REFERENCE ? c.rope_factor : 1.0f;
+  const size_t qkv_rows = (c.n_heads + 2 * c.n_kv_heads) * c.head_dim;
+  const size_t kv = c.n_layers * c.max_seq * c.n_kv_heads * c.head_dim;
+  const std::vector<float> fr = rope_freqs(c);
+  int st;
+  if ((st = d->alloc(reinterpret_cast<void **>(&d->hidden), c.hidden * 4)) ||
+      (st = d->alloc(reinterpret_cast<void **>(&d->qkv), qkv_rows * 4)) ||
+      (st = d->alloc(reinterpret_cast<void **>(&d->attn), c.n_heads * c.head_dim * 4)) ||
+      (st = d->alloc(reinterpret_cast<void **>(&d->gate_up), 2 * c.ffn * 4)) ||
+      (st = d->alloc(reinterpret_cast<void **>(&d->logits), c.vocab * 4)) ||
+      (st = d->alloc(reinterpret_cast<void **>(&d->kcache), kv * 4)) ||
+      (st = d->alloc(reinterpret_cast<void **>(&d->vcache), kv * 4)) ||
+      (st = d->alloc(reinterpret_cast<void **>(&d->tokens), (c.max_seq + 1) * 4)) ||
+      (st = d->alloc(reinterpret_cast<void **>(&d->pos), 4)) || (st = upload(d, &d->freq, fr.data(), fr.size()))) {
+    delete d;
+    return st;
+  }
+  e = hipStreamCreateWithFlags(&d->stream, hipStreamNonBlocking);
+  if (e != hipSuccess) {
+    delete d;
+    return hip_err(e, "hipStreamCreate (decoder)");
+  }
+  for (const void *k : {reinterpret_cast<const void *>(&attention_kernel<64>),
+                        reinterpret_cast<const void *>(&attention_kernel<128>)}) {
+    e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, int(kMaxLdsBytes));
+    if (e != hipSuccess) {
+      delete d;
+      return fail(LMX_ERR_LAUNCH_FAILED, "hipFuncSetAttribute (attention): %s", hipGetErrorString(e));
+    }
+  }
+  *out = d;
+  return LMX_OK;
+}
+
+int lmx_decoder_destroy(lmx_decoder *d) {
+  delete d;
+  return LMX_OK;
+}
+
+int lmx_decoder_set_layer(lmx_decoder *d, size_t layer, const lmx_weight *qkv, const lmx_weight *o,
+                          const lmx_weight *gate_up, const lmx_weight *down, const float *input_norm,
+                          const float *post_norm, const float *qkv_bias) {
+  if (!d) return fail(LMX_ERR_INVALID_ARGUMENT, "decoder is NULL");
+  const lmx_decoder_config &c = d->cfg;
+  if (layer >= c.n_layers) return fail(LMX_ERR_INVALID_ARGUMENT, "layer %zu >= %zu", layer, c.n_layers);
+  if (!input_norm || !post_norm) return fail(LMX_ERR_INVALID_ARGUMENT, "norm weights are NULL");
+  const size_t qd = c.n_heads * c.head_dim, kvd = c.n_kv_heads * c.head_dim;
+  int st;
+  if ((st = check_shape(qkv, qd + 2 * kvd, c.hidden, "qkv")) || (st = check_shape(o, c.hidden, qd, "o")) ||
+      (st = check_shape(gate_up, 2 * c.ffn, c.hidden, "gate_up")) || (st = check_shape(down, c.hidden, c.ffn, "down")))
+    return st;
+  for (const lmx_weight *w : {qkv, o, gate_up, down})
+    if (w->device != d->device) return fail(LMX_ERR_INVALID_ARGUMENT, "weight on another device");
+  lmx_decoder::Layer &L = d->layers[layer];
+  if ((st = upload(d, &L.in_norm, input_norm, c.hidden)) || (st = upload(d, &L.post_norm, post_norm, c.hidden)))
+    return st;
+  L.qkv_bias = nullptr;
+  if (qkv_bias && (st = upload(d, &L.qkv_bias, qkv_bias, qd + 2 * kvd))) return st;
+  L.qkv = qkv, L.o = o, L.gate_up = gate_up, L.down = down;
+  return LMX_OK;
+}
+
+int lmx_decoder_set_head(lmx_decoder *d, const lmx_weight *embed_head, const float *final_norm) {
+  if (!d) return fail(LMX_ERR_INVALID_ARGUMENT, "decoder is NULL");
+  if (!final_norm) return fail(LMX_ERR_INVALID_ARGUMENT, "final norm is NULL");
+  int st = check_shape(embed_head, d->cfg.vocab, d->cfg.hidden, "embedding/head");
+  if (st) return st;
+  if (embed_head->device != d->device) return fail(LMX_ERR_INVALID_ARGUMENT, "weight on another device");
+  if ((st = upload(d, &d->final_norm, final_norm, d->cfg.hidden))) return st;
+  d->head = embed_head;
+  return LMX_OK;
+}
+
+int lmx_decoder_reset(lmx_decoder *d, const int32_t *tokens, size_t n) {
+  int st = ready(d);
+  if (st) return st;
+  if (!tokens) return fail(LMX_ERR_INVALID_ARGUMENT, "tokens is NULL");
+  return set_position(d, tokens, n, nullptr);
+}
+
+int lmx_decoder_step(lmx_decoder *d, float *d_logits, void *stream) {
+  int st = ready(d);
+  if (st) return st;
+  if (d->host_pos >= d->cfg.max_seq)
+    return fail(LMX_ERR_INVALID_ARGUMENT, "position %zu reached max_seq", d->host_pos);
+  st = step(d, d_logits, static_cast<hipStream_t>(stream));
+  if (st) return st;
+  ++d->host_pos;
+  return LMX_OK;
+}
+
+int lmx_decoder_tokens(lmx_decoder *d, int32_t *out, size_t n, void *stream) {
+  if (!d || !out) return fail(LMX_ERR_INVALID_ARGUMENT, "NULL argument");
+  if (n > d->cfg.max_seq + 1) return fail(LMX_ERR_INVALID_ARGUMENT, "n %zu > max_seq + 1", n);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  hipError_t e = hipMemcpyAsync(out, d->tokens, n * sizeof(int32_t), hipMemcpyDeviceToHost, st);
+  if (e == hipSuccess) e = hipStreamSynchronize(st);
+  return e == hipSuccess ? LMX_OK : hip_err(e, "decoder tokens");
+}
+
+int lmx_decoder_generate(lmx_decoder *d, const int32_t *prompt, size_t n_prompt, size_t n_new, int32_t *out_tokens,
+                         float *prefill_ms, float *decode_ms, void *stream) {
+  int st = ready(d);
+  if (st) return st;
+  if (!prompt || !out_tokens || n_prompt == 0 || n_new == 0)
+    return fail(LMX_ERR_INVALID_ARGUMENT, "need a prompt, an output buffer and n_new > 0");
+  if (n_prompt + n_new > d->cfg.max_seq + 1)
+    return fail(LMX_ERR_INVALID_ARGUMENT, "n_prompt + n_new = %zu exceeds max_seq + 1", n_prompt + n_new);
+  // The caller's stream may be the legacy default stream, which cannot be
+  // captured: work runs on the decoder's own stream, ordered after the
+  // caller's pending work, and this call returns when it is done.
+  hipStream_t s = d->stream;
+  {
+    hipEvent_t dep = nullptr;
+    hipError_t e0 = hipEventCreateWithFlags(&dep, hipEventDisableTiming);
+    if (e0 == hipSuccess) e0 = hipEventRecord(dep, static_cast<hipStream_t>(stream));
+    if (e0 == hipSuccess) e0 = hipStreamWaitEvent(s, dep, 0);
+    if (dep) (void)hipEventDestroy(dep);
+    if (e0 != hipSuccess) return hip_err(e0, "decoder stream ordering");
+  }
+  // One eager step (first-launch set-up of every kernel), then capture.
+  if ((st = set_position(d, prompt, n_prompt, s)) || (st = step(d, nullptr, s))) return st;
+  hipError_t e = hipStreamSynchronize(s);
+  if (e != hipSuccess) return hip_err(e, "decoder warm-up step");
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  e = hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal);
+  if (e != hipSuccess) return hip_err(e, "hipStreamBeginCapture");
+  st = step(d, nullptr, s);
+  e = hipStreamEndCapture(s, &graph);
+  if (st) {
+    if (graph) (void)hipGraphDestroy(graph);
+    return st;
+  }
+  if (e != hipSuccess) return hip_err(e, "hipStreamEndCapture");
+  e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(graph);
+  if (e != hipSuccess) return hip_err(e, "hipGraphInstantiate");
+  hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
+  for (auto &x : ev)
+    if (e == hipSuccess) e = hipEventCreate(&x);
+  if (e == hipSuccess && (st = set_position(d, prompt, n_prompt, s)) != LMX_OK) e = hipErrorUnknown;
+  if (e == hipSuccess) e = hipEventRecord(ev[0], s);
+  for (size_t i = 0; i < n_prompt && e == hipSuccess; ++i) e = hipGraphLaunch(exec, s);
+  if (e == hipSuccess) e = hipEventRecord(ev[1], s);
+  for (size_t i = 1; i < n_new && e == hipSuccess; ++i) e = hipGraphLaunch(exec, s);
+  if (e == hipSuccess) e = hipEventRecord(ev[2], s);
+  if (e == hipSuccess) e = hipEventSynchronize(ev[2]);
+  float t0 = 0.0f, t1 = 0.0f;
+  if (e == hipSuccess) e = hipEventElapsedTime(&t0, ev[0], ev[1]);
+  if (e == hipSuccess) e = hipEventElapsedTime(&t1, ev[1], ev[2]);
+  if (e == hipSuccess)
+    e = hipMemcpy(out_tokens, d->tokens, (n_prompt + n_new) * sizeof(int32_t), hipMemcpyDeviceToHost);
+  for (auto &x : ev)
+    if (x) (void)hipEventDestroy(x);
+  (void)hipGraphExecDestroy(exec);
+  if (st) return st;
+  if (e != hipSuccess) return hip_err(e, "decoder generate");
+  d->host_pos = n_prompt + n_new - 1;
+  if (prefill_ms) *prefill_ms = t0;
+  if (decode_ms) *decode_ms = t1;
+  return LMX_OK;
+}
+
+}  // extern "C"

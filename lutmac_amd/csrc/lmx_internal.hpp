@@ -59,7 +59,19 @@ struct GemvArgs {
   int waves;               // wavefronts (64-row slabs) per workgroup: 1, 2 or 4
   int fullk;               // 0: split-K kernel; else a kFullK_* configuration
   int staged;              // full-K: issue part of the weight loads after the table prologue
+  int xmode;               // activation transform fused into the table prologue (kXMode*)
+  const float *xw;         // kXModeRmsNorm: norm weight [cols]
+  float eps;               // kXModeRmsNorm: epsilon
 };
+
+// Activation transforms applied while the tables are built:
+//   kXModeRmsNorm:  x'[k] = x[k] * inv_rms * xw[k], inv_rms = 1/sqrt(sum x^2 / cols + eps)
+//                   (norm.cpp:18-34), the sum taken over x[0..cols) by every workgroup
+//   kXModeSiluMul:  x'[k] = silu(x[k]) * x[cols + k]  (model.cpp:36,413-416: gate and
+//                   up halves of one fused gate|up output)
+constexpr int kXModeNone = 0;
+constexpr int kXModeRmsNorm = 1;
+constexpr int kXModeSiluMul = 2;
 
 // Full-K kernel configurations (waves x k-slices per wave x chunks per slice):
 // the workgroup holds the tables of the whole K and reduces in LDS.
@@ -133,3 +145,8 @@ struct lmx_weight {
   unsigned *d_counters = nullptr;
   float *d_xrot = nullptr;  // staging for LMX_ROTATE_FWHT_FULL (cols floats)
 };
+
+namespace lmx {
+// Kernel arguments of a handle (x, y, bias, rotation and transform unset).
+GemvArgs weight_args(const lmx_weight *w);
+}  // namespace lmx

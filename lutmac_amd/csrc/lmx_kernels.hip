@@ -193,6 +193,55 @@ __device__ __forceinline__ void load_x4(const float *__restrict__ x, int k0, int
   x3 = in ? v.w : 0.0f;
 }
 
+// Second operand of the fused activation transform for the lane's 4
+// activations at k0 + 4*lane: the norm weights (kXModeRmsNorm) or the up
+// half of a gate|up vector (kXModeSiluMul).  Clamped in bounds like load_x4.
+__device__ __forceinline__ void load_aux4(const GemvArgs &a, int k0, int lane, float *aux) {
+  const float *p = a.xmode == kXModeRmsNorm ? a.xw : a.x + a.cols;
+  const float4 v = *reinterpret_cast<const float4 *>(p + min(k0 + 4 * lane, a.cols - 4));
+  aux[0] = v.x; aux[1] = v.y; aux[2] = v.z; aux[3] = v.w;
+}
+
+__device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }   // model.cpp:36
+
+__device__ __forceinline__ void xform4(int mode, float inv_rms, const float *aux, float &x0, float &x1, float &x2,
+                                       float &x3) {
+  if (mode == kXModeRmsNorm) {   // input * inv_rms * weight, in that order (norm.cpp:31)
+    x0 = x0 * inv_rms * aux[0]; x1 = x1 * inv_rms * aux[1];
+    x2 = x2 * inv_rms * aux[2]; x3 = x3 * inv_rms * aux[3];
+  } else if (mode == kXModeSiluMul) {
+    x0 = silu(x0) * aux[0]; x1 = silu(x1) * aux[1];
+    x2 = silu(x2) * aux[2]; x3 = silu(x3) * aux[3];
+  }
+}
+
+// 1/sqrt(sum(x[0..cols)^2)/cols + eps) (norm.cpp:20-28) from per-thread
+// partial sums.  Every workgroup sums in the same fixed order, so every
+// workgroup gets the same bits.  red: NT/64 floats of LDS.
+template <int NT>
+__device__ float wg_inv_rms_from(float s, int cols, float eps, float *red) {
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) s += __shfl_xor(s, d, 64);
+  if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = s;
+  __syncthreads();
+  float t = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NT / kWave; ++i) t += red[i];
+  __syncthreads();
+  return 1.0f / sqrtf(t / float(cols) + eps);
+}
+
+// The same over all of x read from memory (workgroups that hold a k-slice).
+template <int NT>
+__device__ float wg_inv_rms(const float *__restrict__ x, int cols, float eps, float *red) {
+  float s = 0.0f;
+  for (int k = 4 * int(threadIdx.x); k < cols; k += 4 * NT) {
+    const float4 v = *reinterpret_cast<const float4 *>(x + k);
+    s += (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
+  }
+  return wg_inv_rms_from<NT>(s, cols, eps, red);
+}
+
 // ---------------------------------------------------------------------------
 template <int FMT, int CHUNKS, int WAVES>
 __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_kernel(GemvArgs a, int row_blocks, int splits) {
@@ -202,6 +251,7 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_kernel(GemvArgs a, int
   constexpr int C2 = KS / kRotChunk;  // 256-chunks of the slice
   __shared__ __attribute__((aligned(16))) float tables[KS / 4 * 16];
   __shared__ float xsum[CHUNKS];
+  __shared__ float xred[WAVES];
   __shared__ unsigned ticket;
 
   const int lane = threadIdx.x & (kWave - 1);
@@ -217,11 +267,15 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_kernel(GemvArgs a, int
   // stream is still in flight (vector loads retire in issue order).  Loads
   // are unconditional (indices clamped in bounds) so no branch splits them.
   constexpr int XJ = (C2 + WAVES - 1) / WAVES;
-  float xv[XJ][4];
+  float xv[XJ][4], aux[XJ][4];
 #pragma unroll
   for (int j = 0; j < XJ; ++j) {
     const int c2 = min(wave + j * WAVES, C2 - 1);
     load_x4(a.x, k0 + c2 * kRotChunk, a.cols, lane, xv[j][0], xv[j][1], xv[j][2], xv[j][3]);
+  }
+  if (a.xmode != kXModeNone) {
+#pragma unroll
+    for (int j = 0; j < XJ; ++j) load_aux4(a, k0 + min(wave + j * WAVES, C2 - 1) * kRotChunk, lane, aux[j]);
   }
   __builtin_amdgcn_sched_barrier(0);  // keep the x loads ahead of the weight stream
   u32x4 w[CHUNKS][P];
@@ -242,14 +296,16 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_kernel(GemvArgs a, int
     }
   }
 
-  // ---- prologue: (FWHT-256) -> 16-entry group tables in LDS --------------
+  // ---- prologue: (transform) -> (FWHT-256) -> 16-entry group tables ------
   // Lane l of the wave owning a 256-chunk holds activations 4l..4l+3 = group
   // l of the chunk and writes that group's table.
+  const float inv_rms = a.xmode == kXModeRmsNorm ? wg_inv_rms<ROWS>(a.x, a.cols, a.eps, xred) : 1.0f;
 #pragma unroll
   for (int j = 0; j < XJ; ++j) {
     const int c2 = wave + j * WAVES;
     if (c2 >= C2) break;   // wave-uniform
     float x0 = xv[j][0], x1 = xv[j][1], x2 = xv[j][2], x3 = xv[j][3];
+    xform4(a.xmode, inv_rms, aux[j], x0, x1, x2, x3);
     if (a.rotate == LMX_ROTATE_FWHT256) fwht256_regs(x0, x1, x2, x3, lane);
     float t[16];
     group_table(x0, x1, x2, x3, t);
@@ -406,11 +462,15 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_fullk_kernel(GemvArgs 
 
   // ---- loads: activations for this wave's 256-chunks, then the weights ----
   const int C2n = a.Kp / kRotChunk;
-  float xv[XJ][4];
+  float xv[XJ][4], aux[XJ][4];
 #pragma unroll
   for (int j = 0; j < XJ; ++j) {
     const int c2 = min(wave + j * WAVES, C2n - 1);
     load_x4(a.x, c2 * kRotChunk, a.cols, lane, xv[j][0], xv[j][1], xv[j][2], xv[j][3]);
+  }
+  if (a.xmode != kXModeNone) {
+#pragma unroll
+    for (int j = 0; j < XJ; ++j) load_aux4(a, min(wave + j * WAVES, C2n - 1) * kRotChunk, lane, aux[j]);
   }
   __builtin_amdgcn_sched_barrier(0);
   // Weight loads.  STAGED (CPS > 1 only) issues chunk 0 before the table
@@ -435,12 +495,24 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_fullk_kernel(GemvArgs 
   }
   if constexpr (STAGED) __builtin_amdgcn_sched_barrier(0);
 
-  // ---- prologue: (FWHT-256) -> 16-entry group tables of the whole K -------
+  // ---- prologue: (transform) -> (FWHT-256) -> group tables of the whole K -
+  // The waves' x registers cover all of x once (chunks past C2n are clamped
+  // duplicates and skipped), so the norm needs no second read of x.
+  float inv_rms = 1.0f;
+  if (a.xmode == kXModeRmsNorm) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < XJ; ++j)
+      if (wave + j * WAVES < C2n)
+        ss += (xv[j][0] * xv[j][0] + xv[j][1] * xv[j][1]) + (xv[j][2] * xv[j][2] + xv[j][3] * xv[j][3]);
+    inv_rms = wg_inv_rms_from<WAVES * kWave>(ss, a.cols, a.eps, red);
+  }
 #pragma unroll
   for (int j = 0; j < XJ; ++j) {
     const int c2 = wave + j * WAVES;
     if (c2 >= C2n) break;   // wave-uniform
     float x0 = xv[j][0], x1 = xv[j][1], x2 = xv[j][2], x3 = xv[j][3];
+    xform4(a.xmode, inv_rms, aux[j], x0, x1, x2, x3);
     if (a.rotate == LMX_ROTATE_FWHT256) fwht256_regs(x0, x1, x2, x3, lane);
     float t[16];
     group_table(x0, x1, x2, x3, t);

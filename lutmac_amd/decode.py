@@ -1,0 +1,200 @@
+"""Host side of the device-resident decoder (include/lutmac_decode.h).
+
+Mirrors the reference engine's model path (src/model.cpp:47-490): a
+Llama/Qwen-style config, a seeded random-init model whose linears are
+quantized to 4-bit with the reference's rule (quantize.hpp:444-461: scale =
+absmax/7 per group, q = round(w/scale) clamped to [-7, 7], stored q + 8),
+and a ``Decoder`` that uploads it as LUT-GEMV weight handles and runs token
+steps or whole greedy generations on the GPU.
+
+Weights are kept in the canonical plane form (planes[p][row][cols/8],
+scales[1][row][cols/group]) with the fused layouts the device decoder takes:
+q|k|v rows in one matrix and gate|up rows in one matrix.
+"""
+import ctypes
+from dataclasses import dataclass, replace
+
+import numpy as np
+
+from . import (FMT_INT4, DecoderConfigC, Weight, _np_ptr, _stream_ptr, check, lib, synth_int4_normal)
+
+ROPE_REFERENCE = 0
+ROPE_LLAMA3 = 1
+
+
+@dataclass(frozen=True)
+class DecoderConfig:
+    hidden: int
+    n_layers: int
+    n_heads: int
+    n_kv_heads: int
+    head_dim: int
+    ffn: int
+    vocab: int
+    max_seq: int
+    rms_eps: float = 1e-5
+    rope_theta: float = 500000.0
+    rope_mode: int = ROPE_LLAMA3
+    rope_factor: float = 32.0
+    rope_low_freq_factor: float = 1.0
+    rope_high_freq_factor: float = 4.0
+    rope_orig_max_pos: int = 8192
+    qkv_bias: bool = False
+
+    @property
+    def q_dim(self):
+        return self.n_heads * self.head_dim
+
+    @property
+    def kv_dim(self):
+        return self.n_kv_heads * self.head_dim
+
+    def c_struct(self):
+        return DecoderConfigC(self.hidden, self.n_layers, self.n_heads, self.n_kv_heads, self.head_dim,
+                              self.ffn, self.vocab, self.max_seq, self.rms_eps, self.rope_theta,
+                              self.rope_mode, self.rope_factor, self.rope_low_freq_factor,
+                              self.rope_high_freq_factor, self.rope_orig_max_pos)
+
+
+# Llama-3.2-1B architecture, 64 prompt + 256 new tokens.
+LLAMA_3_2_1B = DecoderConfig(hidden=2048, n_layers=16, n_heads=32, n_kv_heads=8, head_dim=64, ffn=8192,
+                             vocab=128256, max_seq=320)
+# Qwen-2.5-1.5B architecture (QKV bias, theta 1e6, no scaling).
+QWEN_2_5_1_5B = DecoderConfig(hidden=1536, n_layers=28, n_heads=12, n_kv_heads=2, head_dim=128, ffn=8960,
+                              vocab=151936, max_seq=2048, rms_eps=1e-6, rope_theta=1000000.0,
+                              rope_mode=ROPE_REFERENCE, rope_factor=1.0, qkv_bias=True)
+
+
+def round_half_away(v):
+    """std::round on float32 values (halves away from zero)."""
+    r = np.round(v)
+    frac = np.abs(v - np.trunc(v))
+    half = frac == np.float32(0.5)
+    if half.any():
+        r[half] = np.trunc(v[half]) + np.sign(v[half])
+    return r
+
+
+def quantize_int4_np(w, group):
+    """numpy restatement of lmx_quantize_int4 (checks the C++ producer): fp32 [rows, cols]
+    -> (planes [4, rows, cols/8], scales [1, rows, cols/group]) with the reference's
+    4-bit rule (quantize.hpp:437-461) applied per `group` weights, in the arithmetic
+    of its -ffast-math build (scale = absmax * (1/7), q = round(w / scale))."""
+    rows, cols = w.shape
+    g = w.reshape(rows, cols // group, group)
+    scale = (np.abs(g).max(axis=2) * np.float32(1.0 / 7.0)).astype(np.float32)
+    live = scale > np.float32(1e-10)
+    safe = np.where(live, scale, np.float32(1.0))
+    q = round_half_away((g / safe[:, :, None]).astype(np.float32)) * live[:, :, None]
+    q = (np.clip(q, -7, 7).astype(np.int16) + 8).astype(np.uint8).reshape(rows, cols)
+    planes = np.stack([np.packbits((q >> p) & 1, axis=1, bitorder="big") for p in range(4)])
+    return planes, scale[None]
+
+
+class SyntheticModel:
+    """Seeded random-init decoder: linears N(0, 0.02) quantized to 4-bit per `group`;
+    norm weights 1 (or 1 + 0.1 N(0,1) with ``random_norms``); tied embedding/head."""
+
+    def __init__(self, cfg, seed=0, group=128, random_norms=False):
+        self.cfg, self.group = cfg, group
+        rng = np.random.default_rng(seed)
+        stream = iter(range(1 << 30))
+
+        def lin(rows, cols):   # matrix i of the model draws from generator stream i
+            return synth_int4_normal(seed, next(stream), rows, cols, 0.02, group)
+
+        def norm():
+            if random_norms:
+                return (1.0 + 0.1 * rng.standard_normal(cfg.hidden)).astype(np.float32)
+            return np.ones(cfg.hidden, np.float32)
+
+        h = cfg.hidden
+        self.layers = []
+        for _ in range(cfg.n_layers):
+            L = {"qkv": lin(cfg.q_dim + 2 * cfg.kv_dim, h), "o": lin(h, cfg.q_dim),
+                 "gate_up": lin(2 * cfg.ffn, h), "down": lin(h, cfg.ffn),
+                 "in_norm": norm(), "post_norm": norm(), "qkv_bias": None}
+            if cfg.qkv_bias:
+                L["qkv_bias"] = (0.02 * rng.standard_normal(cfg.q_dim + 2 * cfg.kv_dim)).astype(np.float32)
+            self.layers.append(L)
+        self.head = lin(cfg.vocab, h)
+        self.final_norm = norm()
+
+    def shapes(self):
+        c = self.cfg
+        return {"qkv": (c.q_dim + 2 * c.kv_dim, c.hidden), "o": (c.hidden, c.q_dim),
+                "gate_up": (2 * c.ffn, c.hidden), "down": (c.hidden, c.ffn)}
+
+
+class Decoder:
+    """Device decoder over LUT-GEMV weight handles (lutmac_decode.h)."""
+
+    def __init__(self, model):
+        self.model, self.cfg = model, model.cfg
+        self._h = None
+        self.weights = []
+        shapes = model.shapes()
+        c = self.cfg
+        h = ctypes.c_void_p()
+        cs = c.c_struct()
+        check(lib().lmx_decoder_create(ctypes.byref(cs), ctypes.byref(h)))
+        self._h = h
+        for i, L in enumerate(model.layers):
+            ws = [Weight.from_planes(FMT_INT4, L[n][0], L[n][1], *shapes[n], model.group)
+                  for n in ("qkv", "o", "gate_up", "down")]
+            self.weights += ws
+            bias = None if L["qkv_bias"] is None else L["qkv_bias"]
+            check(lib().lmx_decoder_set_layer(self._h, i, *[w.handle for w in ws], _np_ptr(L["in_norm"]),
+                                              _np_ptr(L["post_norm"]),
+                                              None if bias is None else _np_ptr(bias)))
+        self.head = Weight.from_planes(FMT_INT4, model.head[0], model.head[1], c.vocab, c.hidden, model.group)
+        check(lib().lmx_decoder_set_head(self._h, self.head.handle, _np_ptr(model.final_norm)))
+
+    def reset(self, tokens):
+        t = np.ascontiguousarray(tokens, np.int32)
+        check(lib().lmx_decoder_reset(self._h, _np_ptr(t), t.size))
+
+    def step(self, logits=None, stream=None):
+        """One forward step at the current position; logits (device float32 tensor of
+        vocab entries) receives the step's logits when given."""
+        from . import _dev_ptr
+        check(lib().lmx_decoder_step(self._h, _dev_ptr(logits), _stream_ptr(stream)))
+        return logits
+
+    def tokens(self, n, stream=None):
+        out = np.zeros(n, np.int32)
+        check(lib().lmx_decoder_tokens(self._h, _np_ptr(out), n, _stream_ptr(stream)))
+        return out
+
+    def generate(self, prompt, n_new, stream=None):
+        """Greedy generation; returns (tokens[n_prompt + n_new], prefill_ms, decode_ms)."""
+        p = np.ascontiguousarray(prompt, np.int32)
+        out = np.zeros(p.size + n_new, np.int32)
+        t0, t1 = ctypes.c_float(), ctypes.c_float()
+        check(lib().lmx_decoder_generate(self._h, _np_ptr(p), p.size, n_new, _np_ptr(out),
+                                         ctypes.byref(t0), ctypes.byref(t1), _stream_ptr(stream)))
+        return out, t0.value, t1.value
+
+    def close(self):
+        if self._h:
+            lib().lmx_decoder_destroy(self._h)
+            self._h = None
+        for w in self.weights:
+            w.close()
+        self.weights = []
+        if getattr(self, "head", None) is not None:
+            self.head.close()
+            self.head = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def small_config(**kw):
+    """A small model of the same architecture for parity tests (cols multiples of 256)."""
+    base = DecoderConfig(hidden=256, n_layers=2, n_heads=8, n_kv_heads=2, head_dim=64, ffn=512, vocab=1000,
+                         max_seq=64)
+    return replace(base, **kw)

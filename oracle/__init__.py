@@ -153,3 +153,142 @@ def planes_gemv(fmt, planes, scales, M, Kp, G, x):
     y = np.zeros(M, np.float32)
     lib().orc_planes_gemv(fmt, _ptr(planes), _ptr(scales), M, Kp, G, _ptr(x), _ptr(y))
     return y
+
+
+# ---- decoder forward (oracle restatement and the reference's Model) -------
+
+class OrcMatrix(ctypes.Structure):
+    _fields_ = [("fmt", ctypes.c_int), ("planes", _p), ("scales", _p), ("rows", _sz), ("cols", _sz),
+                ("group", _sz)]
+
+
+class OrcModel(ctypes.Structure):
+    _fields_ = [("hidden", _sz), ("n_layers", _sz), ("n_heads", _sz), ("n_kv_heads", _sz),
+                ("head_dim", _sz), ("ffn", _sz), ("vocab", _sz), ("max_seq", _sz),
+                ("rms_eps", ctypes.c_float), ("rope_theta", ctypes.c_float), ("rope_mode", ctypes.c_int),
+                ("rope_factor", ctypes.c_float), ("rope_low_freq_factor", ctypes.c_float),
+                ("rope_high_freq_factor", ctypes.c_float), ("rope_orig_max_pos", _sz),
+                ("qkv", ctypes.POINTER(OrcMatrix)), ("o", ctypes.POINTER(OrcMatrix)),
+                ("gate_up", ctypes.POINTER(OrcMatrix)), ("down", ctypes.POINTER(OrcMatrix)),
+                ("in_norm", _p), ("post_norm", _p), ("qkv_bias", _p), ("head", OrcMatrix),
+                ("final_norm", _p), ("kcache", _p), ("vcache", _p)]
+
+
+class OracleDecoder:
+    """orc_decode_step over a model in canonical planes (4-bit, fused q|k|v and
+    gate|up rows): teacher-forced logits for the parity tests."""
+
+    def __init__(self, model):
+        L = lib()
+        L.orc_decode_step.argtypes = [ctypes.POINTER(OrcModel), ctypes.c_int, _sz, _p]
+        L.orc_decode_step.restype = ctypes.c_int
+        c = model.cfg
+        self.cfg, self._keep = c, []
+
+        def mat(pl_sc, rows, cols):
+            pl, sc = np.ascontiguousarray(pl_sc[0], np.uint8), f32(pl_sc[1])
+            self._keep += [pl, sc]
+            return OrcMatrix(FMT_INT4, _ptr(pl), _ptr(sc), rows, cols, model.group)
+
+        shapes = model.shapes()
+        arrs = {}
+        for n in ("qkv", "o", "gate_up", "down"):
+            arrs[n] = (OrcMatrix * c.n_layers)(*[mat(Ly[n], *shapes[n]) for Ly in model.layers])
+        self._keep.append(arrs)
+        in_norm = f32(np.concatenate([Ly["in_norm"] for Ly in model.layers]))
+        post_norm = f32(np.concatenate([Ly["post_norm"] for Ly in model.layers]))
+        bias = None
+        if model.layers[0]["qkv_bias"] is not None:
+            bias = f32(np.concatenate([Ly["qkv_bias"] for Ly in model.layers]))
+        self.kc = np.zeros(c.n_layers * c.max_seq * c.kv_dim, np.float32)
+        self.vc = np.zeros_like(self.kc)
+        fn = f32(model.final_norm)
+        self._keep += [in_norm, post_norm, bias, fn]
+        self.m = OrcModel(c.hidden, c.n_layers, c.n_heads, c.n_kv_heads, c.head_dim, c.ffn, c.vocab, c.max_seq,
+                          c.rms_eps, c.rope_theta, c.rope_mode, c.rope_factor, c.rope_low_freq_factor,
+                          c.rope_high_freq_factor, c.rope_orig_max_pos, arrs["qkv"], arrs["o"], arrs["gate_up"],
+                          arrs["down"], _ptr(in_norm), _ptr(post_norm), _ptr(bias),
+                          mat(model.head, c.vocab, c.hidden), _ptr(fn), _ptr(self.kc), _ptr(self.vc))
+
+    def step(self, token, pos):
+        logits = np.zeros(self.cfg.vocab, np.float32)
+        rc = lib().orc_decode_step(ctypes.byref(self.m), int(token), pos, _ptr(logits))
+        if rc != 0:
+            raise ValueError(f"orc_decode_step failed ({rc})")
+        return logits
+
+
+def int4_blocks_from_planes(planes, scales):
+    """Canonical 4-bit planes [4, rows, cols/8] + group-256 scales [1, rows, cols/256]
+    -> the reference's Int4Block bytes (types.hpp:174-202: even index in the high nibble)."""
+    rows = planes.shape[1]
+    bits = np.unpackbits(planes, axis=-1, bitorder="big")            # [4, rows, cols]
+    q = (bits[0] | (bits[1] << 1) | (bits[2] << 2) | (bits[3] << 3)).astype(np.uint8)
+    cols = q.shape[1]
+    nb = cols // 256
+    q = q.reshape(rows, nb, 256)
+    out = np.zeros((rows, nb, 132), np.uint8)
+    out[:, :, :128] = (q[:, :, 0::2] << 4) | q[:, :, 1::2]
+    out[:, :, 128:] = f32(scales[0].reshape(rows, nb)).view(np.uint8).reshape(rows, nb, 4)
+    return out.reshape(-1)
+
+
+class RefDecoder:
+    """The reference's own Model::forward (oracle/_ref/libref.so) on a 4-bit model with
+    group-256 scales and the reference's RoPE form: teacher-forced logits."""
+
+    def __init__(self, model, blocks=None):
+        R = ref()
+        if R is None:
+            raise RuntimeError("oracle/_ref/libref.so not built")
+        for name, args, res in [
+            ("ref_model_create", [_sz] * 8 + [ctypes.c_float] * 3, _p),
+            ("ref_model_set_linear", [_p, _sz, ctypes.c_int, _p, _sz, _sz, _sz], None),
+            ("ref_model_set_norms", [_p, _sz, _p, _p], None),
+            ("ref_model_set_embed", [_p, _p, _sz, _p], None),
+            ("ref_model_forward", [_p, ctypes.c_int, _sz, _p], None),
+            ("ref_model_destroy", [_p], None),
+        ]:
+            f = getattr(R, name)
+            f.argtypes, f.restype = args, res
+        c = model.cfg
+        assert model.group == 256 and c.rope_mode == 0, "reference model: group-256 blocks, reference RoPE"
+        self.cfg = c
+        self.h = R.ref_model_create(c.hidden, c.n_layers, c.n_heads, c.n_kv_heads, c.head_dim, c.ffn, c.vocab,
+                                    c.max_seq, c.rms_eps, c.rope_theta, c.rope_factor)
+        qd, kvd = c.q_dim, c.kv_dim
+        for i, Ly in enumerate(model.layers):
+            pl, sc = Ly["qkv"]
+            parts = [(0, 0, qd), (1, qd, qd + kvd), (2, qd + kvd, qd + 2 * kvd)]
+            for which, a, b in parts:
+                self._set(i, which, pl[:, a:b], sc[:, a:b], b - a, c.hidden)
+            pl, sc = Ly["gate_up"]
+            self._set(i, 4, pl[:, :c.ffn], sc[:, :c.ffn], c.ffn, c.hidden)
+            self._set(i, 5, pl[:, c.ffn:], sc[:, c.ffn:], c.ffn, c.hidden)
+            self._set(i, 3, *Ly["o"], c.hidden, qd)
+            self._set(i, 6, *Ly["down"], c.hidden, c.ffn)
+            a, b = f32(Ly["in_norm"]), f32(Ly["post_norm"])
+            R.ref_model_set_norms(self.h, i, _ptr(a), _ptr(b))
+        blk = int4_blocks_from_planes(*model.head)
+        fn = f32(model.final_norm)
+        R.ref_model_set_embed(self.h, _ptr(blk), blk.size // 132, _ptr(fn))
+
+    def _set(self, layer, which, planes, scales, rows, cols):
+        blk = int4_blocks_from_planes(np.ascontiguousarray(planes), np.ascontiguousarray(scales))
+        ref().ref_model_set_linear(self.h, layer, which, _ptr(blk), blk.size // 132, rows, cols)
+
+    def step(self, token, pos):
+        logits = np.zeros(self.cfg.vocab, np.float32)
+        ref().ref_model_forward(self.h, int(token), pos, _ptr(logits))
+        return logits
+
+    def close(self):
+        if self.h:
+            ref().ref_model_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

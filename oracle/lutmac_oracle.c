@@ -419,21 +419,174 @@ int orc_plane_value(int fmt, const uint8_t *planes, size_t M, size_t Kp,
   return 0;
 }
 
+/* Integer values of the 8 weights of byte `byte` of row r (stage st). */
+static void byte_values(int fmt, const uint8_t *planes, size_t M, size_t Kp,
+                        size_t r, size_t byte, int st, int *v) {
+  const size_t rb = Kp / 8;
+  int P = orc_format_planes(fmt);
+  uint8_t b[8];
+  for (int p = 0; p < P; ++p) b[p] = planes[((size_t)p * M + r) * rb + byte];
+  for (int j = 0; j < 8; ++j) {
+    int bit = 7 - j, q = 0;
+    switch (fmt) {
+    case ORC_FMT_TERNARY:
+      v[j] = ((b[1] >> bit) & 1) ? 0 : (((b[0] >> bit) & 1) ? -1 : 1);
+      break;
+    case ORC_FMT_BINARY:
+      v[j] = ((b[0] >> bit) & 1) ? 1 : -1;
+      break;
+    case ORC_FMT_RRQ2:
+    case ORC_FMT_RRQ3:
+      v[j] = ((b[st] >> bit) & 1) ? 1 : -1;
+      break;
+    default:
+      for (int p = 0; p < P; ++p) q |= ((b[p] >> bit) & 1) << p;
+      v[j] = fmt == ORC_FMT_INT3 ? q - 4 : fmt == ORC_FMT_INT4 ? q - 8 : (int)(int8_t)(uint8_t)q;
+    }
+  }
+}
+
 void orc_planes_gemv(int fmt, const uint8_t *planes, const float *scales,
                      size_t M, size_t Kp, size_t G, const float *x, float *y) {
   int S = orc_format_stages(fmt);
   size_t ng = Kp / G;
+  int v[8];
   for (size_t r = 0; r < M; ++r) {
     float acc = 0.0f;
     for (int st = 0; st < S; ++st) {
       const float *sc = scales + ((size_t)st * M + r) * ng;
       for (size_t g = 0; g < ng; ++g) {
         float gs = 0.0f;
-        for (size_t k = g * G; k < (g + 1) * G; ++k)
-          gs += (float)orc_plane_value(fmt, planes, M, Kp, r, k, st) * x[k];
+        for (size_t byte = g * G / 8; byte < (g + 1) * G / 8; ++byte) {
+          byte_values(fmt, planes, M, Kp, r, byte, st, v);
+          for (int j = 0; j < 8; ++j) gs += (float)v[j] * x[byte * 8 + j];
+        }
         acc += gs * sc[g];
       }
     }
     y[r] = acc;
   }
+}
+
+/* ---- decoder forward (src/model.cpp:47-453) ------------------------------ */
+
+/* src/layers/norm.cpp:18-34 */
+static void rms_norm(const float *in, const float *w, float *out, size_t n, float eps) {
+  float ss = 0.0f;
+  for (size_t i = 0; i < n; ++i) ss += in[i] * in[i];
+  float rms = sqrtf(ss / (float)n + eps);
+  float inv = 1.0f / rms;
+  for (size_t i = 0; i < n; ++i) out[i] = in[i] * inv * w[i];
+}
+
+/* Frequencies of the rotary embedding: theta^(-2d/hd) as
+ * src/layers/embedding.cpp:46 computes it, or with the published Llama-3
+ * frequency scaling (computed in double, rounded to float). */
+static float rope_freq(const orc_model *m, size_t d) {
+  size_t hd = m->head_dim;
+  if (m->rope_mode == 0) return 1.0f / powf(m->rope_theta, (2.0f * (float)d) / (float)hd);
+  double inv = 1.0 / pow((double)m->rope_theta, 2.0 * (double)d / (double)hd);
+  double lo_wl = (double)m->rope_orig_max_pos / m->rope_low_freq_factor;
+  double hi_wl = (double)m->rope_orig_max_pos / m->rope_high_freq_factor;
+  double wl = 2.0 * 3.14159265358979323846 / inv;
+  if (wl < hi_wl) return (float)inv;
+  if (wl > lo_wl) return (float)(inv / m->rope_factor);
+  double sm = ((double)m->rope_orig_max_pos / wl - m->rope_low_freq_factor) /
+              (m->rope_high_freq_factor - m->rope_low_freq_factor);
+  return (float)((1.0 - sm) * inv / m->rope_factor + sm * inv);
+}
+
+void orc_rope_freqs(const orc_model *m, float *out) {
+  for (size_t d = 0; d < m->head_dim / 2; ++d) out[d] = rope_freq(m, d);
+}
+
+/* src/layers/embedding.cpp:36-75 (rotate-half pairs d, d + hd/2) */
+static void rope(const orc_model *m, float *v, size_t n_heads, size_t pos) {
+  size_t hd = m->head_dim, half = hd / 2;
+  float pf = m->rope_mode == 0 ? (float)pos / m->rope_factor : (float)pos;
+  for (size_t h = 0; h < n_heads; ++h) {
+    float *x = v + h * hd;
+    for (size_t d = 0; d < half; ++d) {
+      float angle = pf * rope_freq(m, d);
+      float c = cosf(angle), s = sinf(angle);
+      float a = x[d], b = x[d + half];
+      x[d] = a * c - b * s;
+      x[d + half] = a * s + b * c;
+    }
+  }
+}
+
+static void linear(const orc_matrix *w, const float *x, float *y) {
+  orc_planes_gemv(w->fmt, w->planes, w->scales, w->rows, w->cols, w->group, x, y);
+}
+
+static float silu(float x) { return x / (1.0f + expf(-x)); } /* model.cpp:36 */
+
+int orc_decode_step(const orc_model *m, int token, size_t pos, float *logits) {
+  const size_t h = m->hidden, nh = m->n_heads, nkv = m->n_kv_heads, hd = m->head_dim;
+  const size_t qd = nh * hd, kvd = nkv * hd, ffn = m->ffn;
+  if (pos >= m->max_seq || token < 0 || (size_t)token >= m->vocab) return -1;
+  float *hs = malloc(h * 4), *nrm = malloc(h * 4), *qkv = malloc((qd + 2 * kvd) * 4);
+  float *att = malloc(qd * 4), *tmp = malloc(h * 4), *gu = malloc(2 * ffn * 4);
+  float *inter = malloc(ffn * 4), *w = malloc((pos + 1) * 4);
+  if (!hs || !nrm || !qkv || !att || !tmp || !gu || !inter || !w) return -2;
+
+  /* embedding row (model.cpp:58-85, per-group scales of the tied table) */
+  {
+    const orc_matrix *e = &m->head;
+    size_t ng = e->cols / e->group;
+    int v[8];
+    for (size_t byte = 0; byte < h / 8; ++byte) {
+      byte_values(e->fmt, e->planes, e->rows, e->cols, (size_t)token, byte, 0, v);
+      for (int j = 0; j < 8; ++j) {
+        size_t k = byte * 8 + j;
+        hs[k] = (float)v[j] * e->scales[(size_t)token * ng + k / e->group];
+      }
+    }
+  }
+  const float scale = 1.0f / sqrtf((float)hd); /* model.cpp:337 */
+  const size_t group = nh / nkv;
+  for (size_t l = 0; l < m->n_layers; ++l) {
+    float *kc = m->kcache + l * m->max_seq * kvd, *vc = m->vcache + l * m->max_seq * kvd;
+    rms_norm(hs, m->in_norm + l * h, nrm, h, m->rms_eps);
+    linear(&m->qkv[l], nrm, qkv);
+    if (m->qkv_bias)
+      for (size_t j = 0; j < qd + 2 * kvd; ++j) qkv[j] += m->qkv_bias[l * (qd + 2 * kvd) + j];
+    rope(m, qkv, nh, pos);
+    rope(m, qkv + qd, nkv, pos);
+    memcpy(kc + pos * kvd, qkv + qd, kvd * 4);
+    memcpy(vc + pos * kvd, qkv + qd + kvd, kvd * 4);
+    memset(att, 0, qd * 4);
+    for (size_t hh = 0; hh < nh; ++hh) { /* model.cpp:341-372 */
+      size_t kvh = hh / group;
+      const float *q = qkv + hh * hd;
+      for (size_t t = 0; t <= pos; ++t) {
+        const float *k = kc + t * kvd + kvh * hd;
+        float sc = 0.0f;
+        for (size_t d = 0; d < hd; ++d) sc += q[d] * k[d];
+        w[t] = sc * scale;
+      }
+      float mx = w[0], sum = 0.0f; /* attention.cpp:23-42 */
+      for (size_t t = 1; t <= pos; ++t) mx = w[t] > mx ? w[t] : mx;
+      for (size_t t = 0; t <= pos; ++t) { w[t] = expf(w[t] - mx); sum += w[t]; }
+      float inv = 1.0f / sum;
+      for (size_t t = 0; t <= pos; ++t) w[t] *= inv;
+      float *o = att + hh * hd;
+      for (size_t t = 0; t <= pos; ++t) {
+        const float *v = vc + t * kvd + kvh * hd;
+        for (size_t d = 0; d < hd; ++d) o[d] += w[t] * v[d];
+      }
+    }
+    linear(&m->o[l], att, tmp);
+    for (size_t j = 0; j < h; ++j) hs[j] += tmp[j];
+    rms_norm(hs, m->post_norm + l * h, nrm, h, m->rms_eps);
+    linear(&m->gate_up[l], nrm, gu);
+    for (size_t j = 0; j < ffn; ++j) inter[j] = silu(gu[j]) * gu[ffn + j];
+    linear(&m->down[l], inter, tmp);
+    for (size_t j = 0; j < h; ++j) hs[j] += tmp[j];
+  }
+  rms_norm(hs, m->final_norm, nrm, h, m->rms_eps);
+  linear(&m->head, nrm, logits);
+  free(hs); free(nrm); free(qkv); free(att); free(tmp); free(gu); free(inter); free(w);
+  return 0;
 }

@@ -114,6 +114,42 @@ int orc_plane_value(int fmt, const uint8_t *planes, size_t M, size_t Kp,
 void orc_planes_gemv(int fmt, const uint8_t *planes, const float *scales,
                      size_t M, size_t Kp, size_t G, const float *x, float *y);
 
+/* ---- decoder forward ----------------------------------------------------
+ * One token step of src/model.cpp:47-453 for a Llama/Qwen-style model whose
+ * linears are canonical-plane matrices (cols a multiple of 256, group G | cols):
+ * embedding row of the tied table, per layer RMSNorm (norm.cpp:18-34), fused
+ * q|k|v rows (+ bias), RoPE (embedding.cpp:36-75; rope_mode 0 = the
+ * reference's (pos/factor)*theta^(-2d/hd), 1 = Llama-3 frequency scaling),
+ * KV append, attention with softmax (model.cpp:326-372, attention.cpp:23-42),
+ * o + residual, RMSNorm, fused gate|up, SiLU(gate)*up, down + residual;
+ * final RMSNorm and the tied head.  kcache/vcache: [layer][max_seq][kv][hd],
+ * caller-owned.  Returns 0, or < 0 on bad arguments / allocation failure. */
+typedef struct {
+  int fmt;
+  const uint8_t *planes; /* [P][rows][cols/8] */
+  const float *scales;   /* [S][rows][cols/group] */
+  size_t rows, cols, group;
+} orc_matrix;
+
+typedef struct {
+  size_t hidden, n_layers, n_heads, n_kv_heads, head_dim, ffn, vocab, max_seq;
+  float rms_eps, rope_theta;
+  int rope_mode;
+  float rope_factor, rope_low_freq_factor, rope_high_freq_factor;
+  size_t rope_orig_max_pos;
+  const orc_matrix *qkv, *o, *gate_up, *down; /* [n_layers] each */
+  const float *in_norm, *post_norm;           /* [n_layers][hidden] */
+  const float *qkv_bias;                      /* [n_layers][qkv rows] or NULL */
+  orc_matrix head;                            /* tied embedding / LM head */
+  const float *final_norm;
+  float *kcache, *vcache;
+} orc_model;
+
+int orc_decode_step(const orc_model *m, int token, size_t pos, float *logits);
+/* The rotary frequencies the step uses (head_dim/2 floats; reads only the
+ * head_dim and rope_* fields). */
+void orc_rope_freqs(const orc_model *m, float *out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,86 @@
+// ref_model_shim.cpp -- extern "C" access to the reference's own Model::forward
+// (src/model.cpp:47-453), built into oracle/_ref/libref.so with the
+// reference's sources.  TEST INFRASTRUCTURE ONLY: the parity checker and the
+// timed CPU decode baseline; never part of the product path.
+//
+// The model is assembled in memory the way load_model fills it
+// (src/model.cpp:576-701): 4-bit linears as Int4Block vectors, the tied
+// lm_head as a copy of the 4-bit embedding (model.cpp:667-689), norms, and
+// Model::allocate() for the KV cache and buffers.
+#include <cstring>
+#include <memory>
+
+#include "lutmac/model.hpp"
+
+using namespace lutmac;
+
+namespace {
+
+void fill_int4(PackedTensor &t, const uint8_t *blocks, size_t n, size_t rows, size_t cols) {
+  t.shape = {rows, cols};
+  t.is_quantized = true;
+  t.quant_bits = 4;
+  t.int4_blocks.resize(n);
+  for (size_t i = 0; i < n; ++i) {
+    std::memcpy(t.int4_blocks[i].data, blocks + i * 132, 128);
+    std::memcpy(&t.int4_blocks[i].scale, blocks + i * 132 + 128, 4);
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+void *ref_model_create(size_t hidden, size_t n_layers, size_t n_heads, size_t n_kv, size_t head_dim, size_t ffn,
+                       size_t vocab, size_t max_seq, float eps, float theta, float rope_factor) {
+  auto *m = new Model();
+  ModelConfig &c = m->config;
+  c.model_type = "llama";
+  c.vocab_size = vocab;
+  c.hidden_size = hidden;
+  c.intermediate_size = ffn;
+  c.num_hidden_layers = n_layers;
+  c.num_attention_heads = n_heads;
+  c.num_key_value_heads = n_kv;
+  c.head_dim_val = head_dim;
+  c.max_position_embeddings = max_seq;
+  c.rms_norm_eps = eps;
+  c.rope_theta = theta;
+  c.rope_scaling_factor = rope_factor;
+  c.activation = ActivationType::SILU;
+  m->allocate();
+  return m;
+}
+
+// which: 0 q, 1 k, 2 v, 3 o, 4 gate, 5 up, 6 down; blocks are Int4Block bytes.
+void ref_model_set_linear(void *mp, size_t layer, int which, const uint8_t *blocks, size_t n, size_t rows,
+                          size_t cols) {
+  TransformerLayer &L = static_cast<Model *>(mp)->layers[layer];
+  PackedTensor *t[] = {&L.q_proj, &L.k_proj, &L.v_proj, &L.o_proj, &L.gate_proj, &L.up_proj, &L.down_proj};
+  fill_int4(*t[which], blocks, n, rows, cols);
+}
+
+void ref_model_set_norms(void *mp, size_t layer, const float *in_norm, const float *post_norm) {
+  Model *m = static_cast<Model *>(mp);
+  TransformerLayer &L = m->layers[layer];
+  const size_t h = m->config.hidden_size;
+  L.input_layernorm_weight.assign(in_norm, in_norm + h);
+  L.post_attention_layernorm_weight.assign(post_norm, post_norm + h);
+}
+
+void ref_model_set_embed(void *mp, const uint8_t *blocks, size_t n, const float *final_norm) {
+  Model *m = static_cast<Model *>(mp);
+  fill_int4(m->embed_tokens, blocks, n, m->config.vocab_size, m->config.hidden_size);
+  m->lm_head = m->embed_tokens;   // tied (model.cpp:667-689)
+  m->norm_weight.assign(final_norm, final_norm + m->config.hidden_size);
+}
+
+void ref_model_forward(void *mp, int token, size_t pos, float *logits) {
+  Model *m = static_cast<Model *>(mp);
+  m->forward(token, pos);
+  std::memcpy(logits, m->logits.data(), m->config.vocab_size * sizeof(float));
+}
+
+void ref_model_destroy(void *mp) { delete static_cast<Model *>(mp); }
+
+}  // extern "C"

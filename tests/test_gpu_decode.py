@@ -1,0 +1,125 @@
+"""GPU parity of the device-resident decoder (include/lutmac_decode.h).
+
+Teacher-forced logits of every step against the oracle's decode restatement
+(orc_decode_step, itself pinned to the reference's Model::forward by
+tests/test_decode_cpu.py) and, in the reference's own configuration
+(group-256 4-bit blocks, its RoPE form), against the reference's Model::forward
+directly.  Bar: max |logit - ref| <= DECODE_TOL * ||ref||_2 at every step
+(fp32 accumulation-order differences compounded over the layers).
+Greedy generation: the captured-graph replay must reproduce eager steps
+token for token, and every generated token must be the oracle's argmax up
+to the same tolerance.
+"""
+import numpy as np
+import pytest
+import torch
+
+import lutmac_amd as L
+import oracle
+from conftest import rel_max_err
+from lutmac_amd import decode as D
+
+pytestmark = pytest.mark.gpu
+
+DECODE_TOL = 1e-5
+
+
+def device_logits(dec, tokens):
+    dec.reset(tokens)
+    out = []
+    lg = torch.empty(dec.cfg.vocab, dtype=torch.float32, device="cuda")
+    for _ in range(len(tokens)):
+        dec.step(lg)
+        out.append(lg.cpu().numpy().copy())
+    return out
+
+
+def check_against(dec, ref, tokens, tol=DECODE_TOL):
+    got = device_logits(dec, tokens)
+    for pos, t in enumerate(tokens):
+        want = ref.step(t, pos)
+        err = rel_max_err(got[pos], want)
+        assert err < tol, f"step {pos}: rel err {err:.3e}"
+
+
+@pytest.mark.parametrize("rope_mode", [D.ROPE_LLAMA3, D.ROPE_REFERENCE])
+def test_decoder_matches_oracle_small(cuda, rope_mode):
+    cfg = D.small_config(rope_mode=rope_mode, rope_factor=32.0 if rope_mode == D.ROPE_LLAMA3 else 4.0,
+                         rope_orig_max_pos=64, rope_theta=10000.0)
+    m = D.SyntheticModel(cfg, seed=11, group=128, random_norms=True)
+    toks = np.random.default_rng(12).integers(0, cfg.vocab, 24)
+    check_against(D.Decoder(m), oracle.OracleDecoder(m), toks)
+
+
+def test_decoder_matches_oracle_qwen_style(cuda):
+    # head_dim 128, 6 query heads per KV head, QKV bias, theta 1e6
+    cfg = D.small_config(hidden=512, n_heads=12, n_kv_heads=2, head_dim=128, ffn=768, vocab=1500,
+                         rope_mode=D.ROPE_REFERENCE, rope_factor=1.0, rope_theta=1e6, rms_eps=1e-6,
+                         qkv_bias=True)
+    m = D.SyntheticModel(cfg, seed=13, group=128, random_norms=True)
+    toks = np.random.default_rng(14).integers(0, cfg.vocab, 20)
+    check_against(D.Decoder(m), oracle.OracleDecoder(m), toks)
+
+
+@pytest.mark.skipif(oracle.ref() is None, reason="oracle/_ref/libref.so not built")
+def test_decoder_matches_reference_model(cuda):
+    # the reference's own configuration: group-256 blocks, (pos/factor) RoPE
+    cfg = D.small_config(rope_mode=D.ROPE_REFERENCE, rope_factor=1.0, rope_theta=10000.0)
+    m = D.SyntheticModel(cfg, seed=15, group=256, random_norms=True)
+    toks = np.random.default_rng(16).integers(0, cfg.vocab, 16)
+    check_against(D.Decoder(m), oracle.RefDecoder(m), toks)
+
+
+def test_generate_graph_equals_eager_and_oracle(cuda):
+    cfg = D.small_config(max_seq=48)
+    m = D.SyntheticModel(cfg, seed=17, group=128, random_norms=True)
+    dec = D.Decoder(m)
+    prompt = np.random.default_rng(18).integers(0, cfg.vocab, 8)
+    n_new = 24
+    out, t_pre, t_dec = dec.generate(prompt, n_new)
+    assert np.array_equal(out[:8], prompt) and t_pre > 0 and t_dec > 0
+    # eager steps from the same prompt
+    dec.reset(prompt)
+    for _ in range(len(prompt) + n_new - 1):
+        dec.step()
+    assert np.array_equal(dec.tokens(len(prompt) + n_new), out)
+    # every generated token is the oracle's argmax (teacher-forced on the device's sequence)
+    o = oracle.OracleDecoder(m)
+    for pos in range(len(out) - 1):
+        lg = o.step(out[pos], pos)
+        if pos + 1 >= len(prompt):
+            assert lg[out[pos + 1]] >= lg.max() - DECODE_TOL * np.linalg.norm(lg)
+    # a second generation on the same decoder repeats the first
+    out2, _, _ = dec.generate(prompt, n_new)
+    assert np.array_equal(out, out2)
+
+
+def test_llama_1b_architecture_steps(cuda):
+    cfg = D.LLAMA_3_2_1B
+    m = D.SyntheticModel(cfg, seed=19, group=128)
+    toks = np.random.default_rng(20).integers(0, cfg.vocab, 2)
+    check_against(D.Decoder(m), oracle.OracleDecoder(m), toks)
+
+
+def test_decoder_rejects_bad_arguments(cuda):
+    import ctypes
+    bad = D.small_config(head_dim=96)
+    h = ctypes.c_void_p()
+    cs = bad.c_struct()
+    assert L.lib().lmx_decoder_create(ctypes.byref(cs), ctypes.byref(h)) == L.ERR_INVALID_ARGUMENT
+    cfg = D.small_config()
+    cs = cfg.c_struct()
+    assert L.lib().lmx_decoder_create(ctypes.byref(cs), ctypes.byref(h)) == L.OK
+    try:
+        # not ready: no layers or head set
+        assert L.lib().lmx_decoder_step(h, None, None) == L.ERR_INVALID_ARGUMENT
+        # wrong shape for the qkv weight
+        from lutmac_amd import synth
+        planes, scales, g = synth.make_weights(L.FMT_INT4, 64, 256, seed=1)
+        w = L.Weight.from_planes(L.FMT_INT4, planes, scales, 64, 256, g)
+        ones = np.ones(cfg.hidden, np.float32)
+        st = L.lib().lmx_decoder_set_layer(h, 0, w.handle, w.handle, w.handle, w.handle,
+                                           L._np_ptr(ones), L._np_ptr(ones), None)
+        assert st == L.ERR_INVALID_ARGUMENT
+    finally:
+        L.lib().lmx_decoder_destroy(h)
