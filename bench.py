@@ -12,6 +12,9 @@ The K timed GEMVs are captured in one HIP graph and replayed (the launch
 path of a captured decode step); the per-launch stream time is reported
 beside it (--no-graph times only that).
 
+Beside it, the metric's second half: batch-1 greedy decode tokens/s of a
+random-init Llama-3.2-1B architecture in "decode".
+
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--formats int4,ternary,...]
 """
 import argparse
@@ -123,6 +126,78 @@ def cpu_baseline(n, budget_s=10.0):
             "ms_per_gemv": round(t * 1e3, 2)}
 
 
+def decode_weight_bytes(cfg, group):
+    """HBM bytes of the weights one token step reads: every linear and the tied
+    head (4-bit codes + fp32 group scales), plus the norm weights."""
+    rows_cols = [(cfg.q_dim + 2 * cfg.kv_dim, cfg.hidden), (cfg.hidden, cfg.q_dim),
+                 (2 * cfg.ffn, cfg.hidden), (cfg.hidden, cfg.ffn)]
+    per_layer = sum(r * c // 2 + r * (c // group) * 4 for r, c in rows_cols) + 2 * cfg.hidden * 4
+    head = cfg.vocab * cfg.hidden // 2 + cfg.vocab * (cfg.hidden // group) * 4
+    return cfg.n_layers * per_layer + head + cfg.hidden * 4
+
+
+def decode_bench(n_prompt, n_new, seed=2024):
+    """greedy batch-1 decode of a random-init Llama-3.2-1B
+    architecture, all linears and the tied head 4-bit with per-128 scales;
+    64 seeded prompt tokens, then n_new generated tokens (one captured HIP
+    graph per token step, replayed)."""
+    from lutmac_amd import decode as D
+    from dataclasses import replace
+    cfg = replace(D.LLAMA_3_2_1B, max_seq=max(D.LLAMA_3_2_1B.max_seq, n_prompt + n_new))
+    t0 = time.perf_counter()
+    model = D.SyntheticModel(cfg, seed=seed, group=128)
+    dec = D.Decoder(model)
+    setup_s = time.perf_counter() - t0
+    prompt = np.random.default_rng(seed + 1).integers(0, cfg.vocab, n_prompt)
+    dec.generate(prompt, n_new)                         # untimed: first launches, graph set-up
+    out, pre_ms, dec_ms = dec.generate(prompt, n_new)
+    tok_s = (n_new - 1) / (dec_ms / 1e3)
+    B = decode_weight_bytes(cfg, 128)
+    kv_avg = 2 * cfg.n_layers * cfg.kv_dim * 4 * (n_prompt + n_new / 2)   # K and V read per step, mean length
+    dec.close()
+    return {"metric": "1B-arch decode tokens/s bs=1", "tokens_per_s": round(tok_s, 1),
+            "ms_per_token": round(dec_ms / (n_new - 1), 4),
+            "prefill_tokens_per_s": round(n_prompt / (pre_ms / 1e3), 1),
+            "n_prompt": n_prompt, "n_new": n_new,
+            "timing": "HIP events around the graph replays; decode = the n_new-1 steps after the prompt",
+            "config": {"workload": "Llama-3.2-1B architecture, random-init N(0,0.02) weights, 4-bit per-128-group "
+                                   "linears and tied 4-bit embedding/head, greedy (BASELINE config 4)",
+                       "layers": cfg.n_layers, "hidden": cfg.hidden, "heads": cfg.n_heads,
+                       "kv_heads": cfg.n_kv_heads, "ffn": cfg.ffn, "vocab": cfg.vocab,
+                       "rope": "theta 500000, llama3 scaling factor 32"},
+            "weight_bytes_per_token": B, "kv_bytes_per_token_mean": int(kv_avg),
+            "achieved_GB_s": round((B + kv_avg) * tok_s / 1e9, 1),
+            "frac_of_peak": round((B + kv_avg) * tok_s / 1e9 / HBM_PEAK_GBPS, 4),
+            "first_tokens": [int(t) for t in out[n_prompt:n_prompt + 8]],
+            "setup_s": round(setup_s, 1)}
+
+
+def cpu_decode_baseline(budget_s, seed=2024):
+    """The reference's own Model::forward (oracle/_ref/libref.so, 1 thread:
+    lut_linear -> int4_gemv scalar) on the same architecture in its native
+    form (group-256 Int4Blocks, its RoPE), token steps until ~budget_s."""
+    import oracle
+    from lutmac_amd import decode as D
+    from dataclasses import replace
+    if oracle.ref() is None:
+        return None
+    cfg = replace(D.LLAMA_3_2_1B, rope_mode=D.ROPE_REFERENCE, rope_factor=1.0, max_seq=64)
+    ref = oracle.RefDecoder(D.SyntheticModel(cfg, seed=seed, group=256))
+    toks = np.random.default_rng(seed + 1).integers(0, cfg.vocab, 64)
+    n, t0 = 0, time.perf_counter()
+    while True:
+        ref.step(toks[n], n)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or n >= 64:
+            break
+    ref.close()
+    return {"value": round(n / el, 3), "unit": "tokens/s", "cores": 1, "kind": "reference",
+            "sample": f"reference Model::forward (src/model.cpp:47-453) via oracle/_ref, Llama-3.2-1B "
+                      f"architecture in group-256 Int4Blocks, {n} token steps at positions 0..{n - 1} "
+                      f"in {el:.1f} s, 1 thread"}
+
+
 def calibrate_copy(nbytes=35717120, steps=200):
     """Plain device copy of a known size (torch's copy kernel), the yardstick
     that scales rocprofv3's FETCH_SIZE / WRITE_SIZE counters to bytes."""
@@ -153,6 +228,10 @@ def main():
     ap.add_argument("--formats", default="int4,ternary,binary,rrq2,rrq3,int8")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-decode", action="store_true", help="skip the 1B-architecture decode")
+    ap.add_argument("--decode-prompt", type=int, default=64)
+    ap.add_argument("--decode-tokens", type=int, default=256)
+    ap.add_argument("--cpu-decode-seconds", type=float, default=10.0)
     ap.add_argument("--no-graph", action="store_true",
                     help="time one stream launch per GEMV only (no HIP-graph replay)")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -180,7 +259,14 @@ def main():
         print(f"# {name}: {r['us_per_gemv']} us/GEMV, {r['GB_per_s']} GB/s "
               f"({100 * r['frac_of_peak']:.1f}% of peak)", file=sys.stderr, flush=True)
     head = sweep.get("int4") or sweep[names[0]]
+    decode = None
+    if not args.no_decode:
+        decode = decode_bench(args.decode_prompt, args.decode_tokens)
+        print(f"# decode: {decode['tokens_per_s']} tokens/s ({decode['ms_per_token']} ms/token)",
+              file=sys.stderr, flush=True)
     cpu = None if args.no_cpu else cpu_baseline(args.size, args.cpu_seconds)
+    if decode is not None and not args.no_cpu:
+        decode["cpu_baseline"] = cpu_decode_baseline(args.cpu_decode_seconds)
     line = {
         "metric": METRIC,
         "value": head["GB_per_s"],
@@ -203,6 +289,7 @@ def main():
                      "frac": head["frac_of_peak"],
                      "traffic": load_traffic(f"{head['format']}_{args.size}")},
         "cpu_baseline": cpu,
+        "decode": decode,
         "sweep": sweep,
     }
     print(json.dumps(line), flush=True)

@@ -45,7 +45,7 @@ typedef struct {
   size_t hidden;       /* hidden size */
   size_t n_layers;
   size_t n_heads;      /* query heads */
-  size_t n_kv_heads;   /* key/value heads (GQA), divides n_heads */
+  size_t n_kv_heads;   /* key/value heads (GQA), divides n_heads, <= 8 query heads each */
   size_t head_dim;     /* 64 or 128 */
   size_t ffn;          /* intermediate size */
   size_t vocab;

@@ -7,18 +7,20 @@
 //   per layer:
 //     GEMV qkv             RMSNorm(input_norm) fused into the table prologue,
 //                          q|k|v rows in one weight, + bias (model.cpp:296-323)
-//     attention_kernel     RoPE of q and k, KV-cache append, scores, softmax,
-//                          weighted V sum for the query heads of one KV head
+//     attn_chunk_kernel    RoPE of q and k, KV-cache append, scores, partial
+//                          softmax and weighted V sums over 64-position chunks
 //                          (model.cpp:326-372, embedding.cpp:36-75,
 //                          attention.cpp:23-42)
-//     GEMV o               + residual: the hidden state is the bias and the
+//     GEMV o               merges the chunks while loading its activations;
+//                          + residual: the hidden state is the bias and the
 //                          output (model.cpp:376-388)
 //     GEMV gate|up         RMSNorm(post_norm) fused (model.cpp:390-403)
 //     GEMV down            SiLU(gate)*up fused into the prologue, + residual
 //                          (model.cpp:410-426)
-//   GEMV head              RMSNorm(final_norm) fused, tied table (model.cpp:433-447)
-//   argmax_kernel          first maximum (model.cpp:480-490); writes the next
-//                          token and advances the device position
+//   GEMV head              RMSNorm(final_norm) fused, tied table (model.cpp:433-447),
+//                          each wave's first maximum folded into a 64-bit key
+//                          by the GEMV's epilogue (model.cpp:480-490)
+//   argmax_finish_kernel   maximum of the keys -> next token, position + 1
 // The position and the token sequence live in device memory, so the same
 // captured step replays for every position.
 #include <hip/hip_runtime.h>
@@ -89,134 +91,162 @@ __global__ __launch_bounds__(256) void embed_kernel(const uint8_t *__restrict__ 
   out[k] = weight_value<FMT>(b, s);
 }
 
-// RoPE + KV append + attention for the `group` query heads of KV head
-// blockIdx.x; wave w < group serves query head blockIdx.x * group + w.
-// LDS: probabilities [group][max_seq], rotated queries [group][HD].
+// Decode attention split over the sequence in chunks of kAttnChunk = 64
+// positions, so the work spreads over n_kv * chunks workgroups instead of
+// n_kv: workgroup (kv head, chunk); wave w serves query head kvh * group + w
+// over the chunk's positions and writes the chunk's partial softmax (max
+// score m, sum of exp l, sum of exp * v) for that head; chunks past the
+// sequence write an empty partial.  The o-projection GEMV merges the chunks
+// while it loads its activations (kXModeAttnMerge).  The workgroup whose
+// chunk holds `pos` also rotates k and appends k, v at `pos`.
 template <int HD>
-__global__ __launch_bounds__(1024) void attention_kernel(const float *__restrict__ qkv, float *__restrict__ kc,
-                                                         float *__restrict__ vc, const int *__restrict__ pos_p,
-                                                         const float *__restrict__ freq, float pos_div, int n_heads,
-                                                         int n_kv, int group, int max_seq, float scale,
-                                                         float *__restrict__ out) {
-  extern __shared__ float lds[];
+__device__ __forceinline__ void rope_pair(const float *in, float *out, const float *freq, float pf, int lane) {
   constexpr int HALF = HD / 2;
-  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
-  const int kvh = blockIdx.x;
-  const int pos = min(*pos_p, max_seq - 1);
-  const int seq = pos + 1;
-  const float pf = float(pos) / pos_div;
-  const size_t row = size_t(n_kv) * HD;   // floats per cache position
-  float *p = lds + wave * max_seq;
-  float *qs = lds + group * max_seq + wave * HD;
-
-  // (a) rotate k of this KV head and append k, v at `pos`
-  if (wave == 0) {
-    const float *kin = qkv + size_t(n_heads) * HD + kvh * HD;
-    const float *vin = kin + row;
-    float *kd = kc + size_t(pos) * row + kvh * HD;
-    float *vd = vc + size_t(pos) * row + kvh * HD;
-    for (int d = lane; d < HALF; d += kWave) {
-      float sn, cs;
-      sincosf(pf * freq[d], &sn, &cs);
-      const float k0 = kin[d], k1 = kin[d + HALF];
-      kd[d] = k0 * cs - k1 * sn;
-      kd[d + HALF] = k0 * sn + k1 * cs;
-    }
-    for (int d = lane; d < HD; d += kWave) vd[d] = vin[d];
-  }
-  // (b) rotate this wave's query head into LDS
-  if (wave < group) {
-    const float *qin = qkv + size_t(kvh * group + wave) * HD;
-    for (int d = lane; d < HALF; d += kWave) {
-      float sn, cs;
-      sincosf(pf * freq[d], &sn, &cs);
-      const float q0 = qin[d], q1 = qin[d + HALF];
-      qs[d] = q0 * cs - q1 * sn;
-      qs[d + HALF] = q0 * sn + q1 * cs;
-    }
-  }
-  __syncthreads();
-
-  // (c) scores q.k_t * scale, lanes over positions; running max
-  float mx = -INFINITY;
-  if (wave < group) {
-    for (int t = lane; t < seq; t += kWave) {
-      const float4 *kr = reinterpret_cast<const float4 *>(kc + size_t(t) * row + kvh * HD);
-      float sc = 0.0f;
-#pragma unroll 4
-      for (int d4 = 0; d4 < HD / 4; ++d4) {
-        const float4 kv = kr[d4];
-        sc += qs[4 * d4] * kv.x;
-        sc += qs[4 * d4 + 1] * kv.y;
-        sc += qs[4 * d4 + 2] * kv.z;
-        sc += qs[4 * d4 + 3] * kv.w;
-      }
-      sc *= scale;
-      p[t] = sc;
-      mx = fmaxf(mx, sc);
-    }
-#pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) mx = fmaxf(mx, __shfl_xor(mx, d, 64));
-  }
-  __syncthreads();
-  // (d) softmax (attention.cpp:23-42): exp(x - max), sum, x * (1/sum)
-  float sum = 0.0f;
-  if (wave < group) {
-    for (int t = lane; t < seq; t += kWave) {
-      const float e = expf(p[t] - mx);
-      p[t] = e;
-      sum += e;
-    }
-#pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) sum += __shfl_xor(sum, d, 64);
-    const float inv = 1.0f / sum;
-    for (int t = lane; t < seq; t += kWave) p[t] *= inv;
-  }
-  __syncthreads();
-  // (e) out[d] = sum_t p_t * v_t[d], lanes over d
-  if (wave < group) {
-    float *o = out + size_t(kvh * group + wave) * HD;
-    const float *vb = vc + kvh * HD;
-#pragma unroll
-    for (int d0 = 0; d0 < HD; d0 += kWave) {
-      float acc = 0.0f;
-      const float *vd = vb + d0 + lane;
-      for (int t = 0; t < seq; ++t) acc += p[t] * vd[size_t(t) * row];
-      o[d0 + lane] = acc;
-    }
+  for (int d = lane; d < HALF; d += kWave) {
+    float sn, cs;
+    sincosf(pf * freq[d], &sn, &cs);
+    const float a0 = in[d], a1 = in[d + HALF];
+    out[d] = a0 * cs - a1 * sn;
+    out[d + HALF] = a0 * sn + a1 * cs;
   }
 }
 
-// First maximum of logits[0..V) (strict >, so the lowest index wins ties).
-// Thread 0 writes it to tokens[pos + 1] unless that position is forced and
-// advances the device position.
-__global__ __launch_bounds__(1024) void argmax_kernel(const float *__restrict__ logits, int V, int *__restrict__ tokens,
-                                                      int *__restrict__ pos_p, int n_forced, int max_pos) {
-  __shared__ float bv[16];
-  __shared__ int bi[16];
-  float best = -INFINITY;
-  int idx = 0x7fffffff;
-  for (int i = threadIdx.x; i < V; i += 1024) {
-    const float v = logits[i];
-    if (v > best) best = v, idx = i;
+template <int HD>
+__global__ __launch_bounds__(512) void attn_chunk_kernel(const float *__restrict__ qkv, float *__restrict__ kc,
+                                                         float *__restrict__ vc, const int *__restrict__ pos_p,
+                                                         const float *__restrict__ freq, float pos_div, int n_heads,
+                                                         int n_kv, int group, int max_seq, float scale,
+                                                         float *__restrict__ part, int n_chunks) {
+  constexpr int VD = HD / kWave;                  // value columns per lane
+  constexpr bool kPrefetchV = HD == 64;           // 64 value registers per lane
+  __shared__ float qs[8][HD];
+  __shared__ float pw[8][kAttnChunk];
+  __shared__ float knew[HD];
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  const int kvh = blockIdx.x % n_kv, chunk = blockIdx.x / n_kv;
+  const size_t row = size_t(n_kv) * HD;
+  const int head = kvh * group + wave;
+  const int t0 = chunk * kAttnChunk;
+  const float *kin = qkv + size_t(n_heads) * HD + kvh * HD;
+  const float *vin = kin + row;
+  // Loads first, none depending on the position, so the kernel pays about one
+  // memory round trip: the position, this lane's cached key row t0 + lane
+  // and (head_dim 64) the chunk's value column d = lane.  The cache holds
+  // n_chunks * 64 rows, so every row is in bounds; rows at or past the
+  // position are masked below.
+  const int pos = min(*pos_p, max_seq - 1);
+  float4 kr[HD / 4];
+  {
+    const float4 *src = reinterpret_cast<const float4 *>(kc + size_t(t0 + lane) * row + kvh * HD);
+#pragma unroll
+    for (int d4 = 0; d4 < HD / 4; ++d4) kr[d4] = src[d4];
   }
+  float vv[kPrefetchV ? kAttnChunk : 1];
+  if constexpr (kPrefetchV) {
+    const float *vb = vc + size_t(t0) * row + kvh * HD + lane;
+#pragma unroll
+    for (int j = 0; j < kAttnChunk; ++j) vv[j] = vb[size_t(j) * row];
+  }
+  float *dst = part + (size_t(head) * n_chunks + chunk) * (HD + 4);   // m, l, -, -, o[HD]
+  if (t0 > pos) {   // chunk past the sequence: an empty partial (weight 0 in the merge)
+#pragma unroll
+    for (int u = 0; u < VD; ++u) dst[4 + u * kWave + lane] = 0.0f;
+    if (lane == 0) dst[0] = -INFINITY, dst[1] = 0.0f;
+    return;   // uniform over the workgroup
+  }
+  const float pf = float(pos) / pos_div;
+  const int t = t0 + lane;
+  const bool valid = t <= pos;
+  const int n = min(kAttnChunk, pos - t0 + 1);     // positions of the chunk in the sequence
+  const bool own = pos / kAttnChunk == chunk;      // the chunk holds the new position
+  const int jnew = own ? pos - t0 : -1;            // its index in the chunk
+  const int nold = own ? n - 1 : n;                // positions already in the cache
+
+  if (own && wave == 0) rope_pair<HD>(kin, knew, freq, pf, lane);
+  rope_pair<HD>(qkv + size_t(head) * HD, qs[wave], freq, pf, lane);
+  __syncthreads();
+  if (own && wave == 0) {   // append the new position to the cache
+    for (int d = lane; d < HD; d += kWave) {
+      kc[size_t(pos) * row + kvh * HD + d] = knew[d];
+      vc[size_t(pos) * row + kvh * HD + d] = vin[d];
+    }
+  }
+
+  // scores q.k_t * scale of positions t0 + lane (model.cpp:341-351)
+  float sc = -INFINITY;
+  if (valid) {
+    float acc = 0.0f;
+    const bool isnew = lane == jnew;
+#pragma unroll
+    for (int d4 = 0; d4 < HD / 4; ++d4) {
+      const float4 kv = isnew ? make_float4(knew[4 * d4], knew[4 * d4 + 1], knew[4 * d4 + 2], knew[4 * d4 + 3])
+                              : kr[d4];
+      acc += qs[wave][4 * d4] * kv.x;
+      acc += qs[wave][4 * d4 + 1] * kv.y;
+      acc += qs[wave][4 * d4 + 2] * kv.z;
+      acc += qs[wave][4 * d4 + 3] * kv.w;
+    }
+    sc = acc * scale;
+  }
+  float m = sc;
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) m = fmaxf(m, __shfl_xor(m, d, 64));
+  const float e = valid ? expf(sc - m) : 0.0f;
+  float l = e;
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) l += __shfl_xor(l, d, 64);
+  pw[wave][lane] = lane < nold ? e : 0.0f;          // cached positions only
+  const float enew = __shfl(e, jnew < 0 ? 0 : jnew, 64);
+  __syncthreads();
+
+  // o[d] = sum_j e_j v_{t0+j}[d] over the cached positions (8 partial sums),
+  // plus e_new * v_new for the new one (model.cpp:362-371)
+#pragma unroll
+  for (int u = 0; u < VD; ++u) {
+    const int d = u * kWave + lane;
+    float s8[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    if constexpr (kPrefetchV) {
+#pragma unroll
+      for (int j = 0; j < kAttnChunk; ++j) s8[j % 8] += pw[wave][j] * vv[j];
+    } else {
+      const float *vb = vc + size_t(t0) * row + kvh * HD + d;
+      int j = 0;
+      for (; j + 8 <= nold; j += 8) {
+#pragma unroll
+        for (int w8 = 0; w8 < 8; ++w8) s8[w8] += pw[wave][j + w8] * vb[size_t(j + w8) * row];
+      }
+      for (; j < nold; ++j) s8[0] += pw[wave][j] * vb[size_t(j) * row];
+    }
+    float o = ((s8[0] + s8[1]) + (s8[2] + s8[3])) + ((s8[4] + s8[5]) + (s8[6] + s8[7]));
+    if (own) o += enew * vin[d];
+    dst[4 + d] = o;
+  }
+  if (lane == 0) dst[0] = m, dst[1] = l;
+}
+
+// Greedy token of the step: the largest of the head GEMV's per-wave argmax
+// keys (the encoding keeps the first maximum, model.cpp:480-490); written
+// unless the next position is forced; then the position advances.
+__global__ __launch_bounds__(1024) void argmax_finish_kernel(const unsigned long long *__restrict__ slots, int n_slots,
+                                                             int *__restrict__ tokens, int *__restrict__ pos_p,
+                                                             int n_forced, int max_pos) {
+  __shared__ unsigned long long best[16];
+  unsigned long long key = 0;
+  for (int i = threadIdx.x; i < n_slots; i += 1024) key = slots[i] > key ? slots[i] : key;
 #pragma unroll
   for (int d = 32; d >= 1; d >>= 1) {
-    const float ob = __shfl_xor(best, d, 64);
-    const int oi = __shfl_xor(idx, d, 64);
-    if (ob > best || (ob == best && oi < idx)) best = ob, idx = oi;
+    const uint32_t lo = __shfl_xor(uint32_t(key), d, 64), hi = __shfl_xor(uint32_t(key >> 32), d, 64);
+    const unsigned long long o = (static_cast<unsigned long long>(hi) << 32) | lo;
+    key = o > key ? o : key;
   }
-  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
-  if (lane == 0) bv[wave] = best, bi[wave] = idx;
+  if ((threadIdx.x & (kWave - 1)) == 0) best[threadIdx.x / kWave] = key;
   __syncthreads();
-  if (threadIdx.x == 0) {
-    for (int w = 1; w < 16; ++w)
-      if (bv[w] > best || (bv[w] == best && bi[w] < idx)) best = bv[w], idx = bi[w];
-    if (idx == 0x7fffffff) idx = 0;   // no finite maximum: the reference's initial best
-    const int pos = *pos_p;
-    if (pos + 1 >= n_forced && pos + 1 <= max_pos) tokens[pos + 1] = idx;
-    *pos_p = pos + 1;
-  }
+  if (threadIdx.x != 0) return;
+  for (int w = 1; w < 16; ++w) key = best[w] > key ? best[w] : key;
+  const int idx = key ? int(0xFFFFFFFFu - uint32_t(key)) : 0;   // no finite maximum: index 0
+  const int pos = *pos_p;
+  if (pos + 1 >= n_forced && pos + 1 <= max_pos) tokens[pos + 1] = idx;
+  *pos_p = pos + 1;
 }
 
 int hip_err(hipError_t e, const char *what) {
@@ -261,10 +291,7 @@ std::vector<float> rope_freqs(const lmx_decoder_config &c) {
   return f;
 }
 
-size_t attn_lds_bytes(const lmx_decoder_config &c) {
-  const size_t group = c.n_heads / c.n_kv_heads;
-  return group * (c.max_seq + c.head_dim) * sizeof(float);
-}
+size_t attn_chunks(const lmx_decoder_config &c) { return (c.max_seq + kAttnChunk - 1) / kAttnChunk; }
 
 }  // namespace
 }  // namespace lmx
@@ -281,8 +308,11 @@ struct lmx_decoder {
   std::vector<Layer> layers;
   const lmx_weight *head = nullptr;
   float *final_norm = nullptr;
-  float *hidden = nullptr, *qkv = nullptr, *attn = nullptr, *gate_up = nullptr, *logits = nullptr;
+  float *hidden = nullptr, *qkv = nullptr, *gate_up = nullptr, *logits = nullptr;
   float *kcache = nullptr, *vcache = nullptr, *freq = nullptr;
+  float *attn_part = nullptr;            // [n_heads][chunks][m, l, -, -, o[head_dim]]
+  unsigned long long *amax = nullptr;    // per-wave argmax keys of the head GEMV
+  size_t amax_slots = 0;
   int *tokens = nullptr, *pos = nullptr;
   int n_forced = 0;
   size_t host_pos = 0;
@@ -306,8 +336,9 @@ struct lmx_decoder {
 namespace {
 
 int gemv(const lmx_weight *w, const float *x, float *y, const float *bias, int xmode, const float *xw, float eps,
-         hipStream_t st) {
+         hipStream_t st, unsigned long long *amax = nullptr) {
   GemvArgs a = weight_args(w);
+  a.amax = amax;
   a.x = x;
   a.y = y;
   a.bias = bias;
@@ -316,6 +347,20 @@ int gemv(const lmx_weight *w, const float *x, float *y, const float *bias, int x
   a.xw = xw;
   a.eps = eps;
   return launch_gemv(w->format, a, st);
+}
+
+// o-projection with the attention chunks merged in its activation loader;
+// the hidden state is the residual (bias) and the output.
+int gemv_attn_merge(lmx_decoder *d, const lmx_weight *o, hipStream_t st) {
+  GemvArgs a = weight_args(o);
+  a.x = d->attn_part;
+  a.y = d->hidden;
+  a.bias = d->hidden;
+  a.rotate = rotates(o->format) ? LMX_ROTATE_FWHT256 : LMX_ROTATE_NONE;
+  a.xmode = kXModeAttnMerge;
+  a.achunks = int(attn_chunks(d->cfg));
+  a.ahd_shift = d->cfg.head_dim == 64 ? 6 : 7;
+  return launch_gemv(o->format, a, st);
 }
 
 template <int FMT>
@@ -342,18 +387,18 @@ int embed(const lmx_weight *w, const int *tokens, const int *pos, float *out, hi
 int attention(lmx_decoder *d, size_t layer, hipStream_t st) {
   const lmx_decoder_config &c = d->cfg;
   const int group = int(c.n_heads / c.n_kv_heads);
-  const size_t lds = attn_lds_bytes(c);
-  const size_t per_layer = c.max_seq * c.n_kv_heads * c.head_dim;
+  const int nch = int(attn_chunks(c));
+  const size_t per_layer = size_t(nch) * kAttnChunk * c.n_kv_heads * c.head_dim;
   float *kc = d->kcache + layer * per_layer, *vc = d->vcache + layer * per_layer;
   const float scale = 1.0f / std::sqrt(float(c.head_dim));   // model.cpp:337
+  const dim3 grid(unsigned(c.n_kv_heads * nch)), block(unsigned(group * kWave));
   if (c.head_dim == 64)
-    attention_kernel<64><<<dim3(unsigned(c.n_kv_heads)), dim3(unsigned(group * kWave)), lds, st>>>(
-        d->qkv, kc, vc, d->pos, d->freq, d->pos_div, int(c.n_heads), int(c.n_kv_heads), group, int(c.max_seq), scale,
-        d->attn);
+    attn_chunk_kernel<64><<<grid, block, 0, st>>>(d->qkv, kc, vc, d->pos, d->freq, d->pos_div, int(c.n_heads),
+                                                  int(c.n_kv_heads), group, int(c.max_seq), scale, d->attn_part, nch);
   else
-    attention_kernel<128><<<dim3(unsigned(c.n_kv_heads)), dim3(unsigned(group * kWave)), lds, st>>>(
-        d->qkv, kc, vc, d->pos, d->freq, d->pos_div, int(c.n_heads), int(c.n_kv_heads), group, int(c.max_seq), scale,
-        d->attn);
+    attn_chunk_kernel<128><<<grid, block, 0, st>>>(d->qkv, kc, vc, d->pos, d->freq, d->pos_div, int(c.n_heads),
+                                                   int(c.n_kv_heads), group, int(c.max_seq), scale, d->attn_part,
+                                                   nch);
   return launch_err("attention");
 }
 
@@ -380,14 +425,15 @@ int step(lmx_decoder *d, float *logits_out, hipStream_t st) {
     const lmx_decoder::Layer &L = d->layers[l];
     if ((r = gemv(L.qkv, d->hidden, d->qkv, L.qkv_bias, kXModeRmsNorm, L.in_norm, c.rms_eps, st)) ||
         (r = attention(d, l, st)) ||
-        (r = gemv(L.o, d->attn, d->hidden, d->hidden, kXModeNone, nullptr, 0.0f, st)) ||
+        (r = gemv_attn_merge(d, L.o, st)) ||
         (r = gemv(L.gate_up, d->hidden, d->gate_up, nullptr, kXModeRmsNorm, L.post_norm, c.rms_eps, st)) ||
         (r = gemv(L.down, d->gate_up, d->hidden, d->hidden, kXModeSiluMul, nullptr, 0.0f, st)))
       return r;
   }
   float *lg = logits_out ? logits_out : d->logits;
-  if ((r = gemv(d->head, d->hidden, lg, nullptr, kXModeRmsNorm, d->final_norm, c.rms_eps, st))) return r;
-  argmax_kernel<<<dim3(1), dim3(1024), 0, st>>>(lg, int(c.vocab), d->tokens, d->pos, d->n_forced, int(c.max_seq));
+  if ((r = gemv(d->head, d->hidden, lg, nullptr, kXModeRmsNorm, d->final_norm, c.rms_eps, st, d->amax))) return r;
+  argmax_finish_kernel<<<dim3(1), dim3(1024), 0, st>>>(d->amax, int(d->amax_slots), d->tokens, d->pos, d->n_forced,
+                                                       int(c.max_seq));
   return launch_err("argmax");
 }
 
@@ -425,14 +471,11 @@ int lmx_decoder_create(const lmx_decoder_config *cfg, lmx_decoder **out) {
   if (!c.hidden || !c.n_layers || !c.n_heads || !c.n_kv_heads || !c.ffn || !c.vocab || !c.max_seq)
     return fail(LMX_ERR_INVALID_ARGUMENT, "decoder sizes must be non-zero");
   if (c.head_dim != 64 && c.head_dim != 128) return fail(LMX_ERR_INVALID_ARGUMENT, "head_dim must be 64 or 128");
-  if (c.n_heads % c.n_kv_heads || c.n_heads / c.n_kv_heads > 16)
-    return fail(LMX_ERR_INVALID_ARGUMENT, "n_heads must be a multiple of n_kv_heads, at most 16 per KV head");
+  if (c.n_heads % c.n_kv_heads || c.n_heads / c.n_kv_heads > 8)
+    return fail(LMX_ERR_INVALID_ARGUMENT, "n_heads must be a multiple of n_kv_heads, at most 8 per KV head");
   if (c.hidden % 4 || c.ffn % 4 || (c.n_heads * c.head_dim) % 4)
     return fail(LMX_ERR_INVALID_ARGUMENT, "hidden, ffn and n_heads*head_dim must be multiples of 4");
   if (c.max_seq > (1u << 24)) return fail(LMX_ERR_INVALID_ARGUMENT, "max_seq too large");
-  if (attn_lds_bytes(c) > kMaxLdsBytes)
-    return fail(LMX_ERR_INVALID_ARGUMENT, "max_seq %zu needs %zu B of LDS for attention (max %zu)", c.max_seq,
-                attn_lds_bytes(c), size_t(kMaxLdsBytes));
   if (c.rope_mode != LMX_ROPE_REFERENCE && c.rope_mode != LMX_ROPE_LLAMA3)
     return fail(LMX_ERR_INVALID_ARGUMENT, "unknown rope mode %d", c.rope_mode);
   if (c.rope_mode == LMX_ROPE_REFERENCE && !(c.rope_factor > 0.0f))
@@ -450,18 +493,20 @@ int lmx_decoder_create(const lmx_decoder_config *cfg, lmx_decoder **out) {
   d->layers.resize(c.n_layers);
   d->pos_div = c.rope_mode == LMX_ROPE_REFERENCE ? c.rope_factor : 1.0f;
   const size_t qkv_rows = (c.n_heads + 2 * c.n_kv_heads) * c.head_dim;
-  const size_t kv = c.n_layers * c.max_seq * c.n_kv_heads * c.head_dim;
+  const size_t kv = c.n_layers * attn_chunks(c) * kAttnChunk * c.n_kv_heads * c.head_dim;   // whole chunks
   const std::vector<float> fr = rope_freqs(c);
   int st;
   if ((st = d->alloc(reinterpret_cast<void **>(&d->hidden), c.hidden * 4)) ||
       (st = d->alloc(reinterpret_cast<void **>(&d->qkv), qkv_rows * 4)) ||
-      (st = d->alloc(reinterpret_cast<void **>(&d->attn), c.n_heads * c.head_dim * 4)) ||
       (st = d->alloc(reinterpret_cast<void **>(&d->gate_up), 2 * c.ffn * 4)) ||
       (st = d->alloc(reinterpret_cast<void **>(&d->logits), c.vocab * 4)) ||
       (st = d->alloc(reinterpret_cast<void **>(&d->kcache), kv * 4)) ||
       (st = d->alloc(reinterpret_cast<void **>(&d->vcache), kv * 4)) ||
       (st = d->alloc(reinterpret_cast<void **>(&d->tokens), (c.max_seq + 1) * 4)) ||
-      (st = d->alloc(reinterpret_cast<void **>(&d->pos), 4)) || (st = upload(d, &d->freq, fr.data(), fr.size()))) {
+      (st = d->alloc(reinterpret_cast<void **>(&d->pos), 4)) ||
+      (st = d->alloc(reinterpret_cast<void **>(&d->attn_part),
+                     c.n_heads * attn_chunks(c) * (c.head_dim + 4) * sizeof(float))) ||
+      (st = upload(d, &d->freq, fr.data(), fr.size()))) {
     delete d;
     return st;
   }
@@ -469,14 +514,6 @@ int lmx_decoder_create(const lmx_decoder_config *cfg, lmx_decoder **out) {
   if (e != hipSuccess) {
     delete d;
     return hip_err(e, "hipStreamCreate (decoder)");
-  }
-  for (const void *k : {reinterpret_cast<const void *>(&attention_kernel<64>),
-                        reinterpret_cast<const void *>(&attention_kernel<128>)}) {
-    e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, int(kMaxLdsBytes));
-    if (e != hipSuccess) {
-      delete d;
-      return fail(LMX_ERR_LAUNCH_FAILED, "hipFuncSetAttribute (attention): %s", hipGetErrorString(e));
-    }
   }
   *out = d;
   return LMX_OK;
@@ -517,6 +554,9 @@ int lmx_decoder_set_head(lmx_decoder *d, const lmx_weight *embed_head, const flo
   if (st) return st;
   if (embed_head->device != d->device) return fail(LMX_ERR_INVALID_ARGUMENT, "weight on another device");
   if ((st = upload(d, &d->final_norm, final_norm, d->cfg.hidden))) return st;
+  const size_t slots = gemv_argmax_slots(weight_args(embed_head));
+  if ((st = d->alloc(reinterpret_cast<void **>(&d->amax), slots * sizeof(unsigned long long)))) return st;
+  d->amax_slots = slots;
   d->head = embed_head;
   return LMX_OK;
 }

@@ -62,6 +62,10 @@ struct GemvArgs {
   int xmode;               // activation transform fused into the table prologue (kXMode*)
   const float *xw;         // kXModeRmsNorm: norm weight [cols]
   float eps;               // kXModeRmsNorm: epsilon
+  unsigned long long *amax;  // when set: per-wave argmax keys of y (gemv_argmax_slots of them)
+  // kXModeAttnMerge: x is [heads][chunks][m, l, -, -, o[head_dim]] attention partials
+  int achunks;             // chunks per head in the partials
+  int ahd_shift;           // log2(head_dim)
 };
 
 // Activation transforms applied while the tables are built:
@@ -69,9 +73,15 @@ struct GemvArgs {
 //                   (norm.cpp:18-34), the sum taken over x[0..cols) by every workgroup
 //   kXModeSiluMul:  x'[k] = silu(x[k]) * x[cols + k]  (model.cpp:36,413-416: gate and
 //                   up halves of one fused gate|up output)
+// (both applied by xform4 after the load; the merge below replaces the load)
 constexpr int kXModeNone = 0;
 constexpr int kXModeRmsNorm = 1;
 constexpr int kXModeSiluMul = 2;
+//   kXModeAttnMerge: x[h*hd + d] = sum_c e^(m_c - M) o_c[d] / sum_c e^(m_c - M) l_c over
+//                   the attention chunks of head h (partials m, l, o[hd]; empty chunks
+//                   m = -inf, l = 0)
+constexpr int kXModeAttnMerge = 3;
+constexpr int kAttnChunk = 64;
 
 // Full-K kernel configurations (waves x k-slices per wave x chunks per slice):
 // the workgroup holds the tables of the whole K and reduces in LDS.
@@ -114,6 +124,8 @@ constexpr int kReduceFenceAll = 1;  // same, with a device fence in every thread
 constexpr int kReduceTwoPass = 2;   // partials, then a separate reduce kernel
 
 int launch_gemv(int fmt, const GemvArgs &a, void *stream);
+// Number of argmax key slots a launch with these arguments writes.
+size_t gemv_argmax_slots(const GemvArgs &a);
 int launch_fwht256(float *x, size_t n, void *stream);
 int launch_stage_x(const float *x, size_t n, float *out, size_t n_pad, void *stream);
 int launch_fwht_full(const float *x, float *out, size_t n, void *stream);

@@ -193,6 +193,37 @@ __device__ __forceinline__ void load_x4(const float *__restrict__ x, int k0, int
   x3 = in ? v.w : 0.0f;
 }
 
+// kXModeAttnMerge load: the lane's 4 activations x[k..k+3] (one head, four
+// consecutive dims) merged from all attention chunks of the head with an
+// online softmax rescale.  Chunk 0 always holds position 0; chunks past the
+// sequence carry (m = -inf, l = 0, o = 0) and weigh 0.  The loads do not
+// depend on each other or on the position, so they overlap.
+__device__ __forceinline__ void load_x4_attn(const GemvArgs &a, int k0, int lane, float &x0, float &x1, float &x2,
+                                             float &x3) {
+  const int k = k0 + 4 * lane;
+  x0 = x1 = x2 = x3 = 0.0f;
+  if (k >= a.cols) return;
+  const int hd = 1 << a.ahd_shift, stride = hd + 4;   // (m, l, -, -, o[hd]): 16-byte aligned rows
+  const int head = k >> a.ahd_shift, d = k & (hd - 1);
+  const float *ph = a.x + size_t(head) * a.achunks * stride;
+  float M = ph[0], L = ph[1];
+  float4 o = *reinterpret_cast<const float4 *>(ph + 4 + d);
+#pragma unroll 8
+  for (int c = 1; c < a.achunks; ++c) {
+    const float *q = ph + size_t(c) * stride;
+    const float m = q[0], l = q[1];
+    const float4 v = *reinterpret_cast<const float4 *>(q + 4 + d);
+    const float Mn = fmaxf(M, m);
+    const float r = expf(M - Mn), w = m == -INFINITY ? 0.0f : expf(m - Mn);
+    L = L * r + w * l;
+    o.x = o.x * r + w * v.x; o.y = o.y * r + w * v.y;
+    o.z = o.z * r + w * v.z; o.w = o.w * r + w * v.w;
+    M = Mn;
+  }
+  const float inv = 1.0f / L;
+  x0 = o.x * inv; x1 = o.y * inv; x2 = o.z * inv; x3 = o.w * inv;
+}
+
 // Second operand of the fused activation transform for the lane's 4
 // activations at k0 + 4*lane: the norm weights (kXModeRmsNorm) or the up
 // half of a gate|up vector (kXModeSiluMul).  Clamped in bounds like load_x4.
@@ -213,6 +244,34 @@ __device__ __forceinline__ void xform4(int mode, float inv_rms, const float *aux
     x0 = silu(x0) * aux[0]; x1 = silu(x1) * aux[1];
     x2 = silu(x2) * aux[2]; x3 = silu(x3) * aux[3];
   }
+}
+
+// Greedy-sampling fold: the key (orderable value bits << 32 | ~row) of the
+// largest y over the wave's valid lanes.  Larger value wins; equal values
+// keep the lower row, as the reference's first-maximum scan does
+// (model.cpp:480-490).  NaN never wins; -0 counts as +0.  Every lane of the
+// wave must call it; every lane gets the wave's key (0 = no valid row).
+__device__ __forceinline__ unsigned long long wave_argmax_key(float v, int row, bool valid) {
+  unsigned long long key = 0;
+  if (valid && !__builtin_isnan(v)) {
+    uint32_t u = __float_as_uint(v + 0.0f);
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    key = (static_cast<unsigned long long>(u) << 32) | (0xFFFFFFFFu - uint32_t(row));
+  }
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) {
+    const uint32_t lo = __shfl_xor(uint32_t(key), d, 64), hi = __shfl_xor(uint32_t(key >> 32), d, 64);
+    const unsigned long long o = (static_cast<unsigned long long>(hi) << 32) | lo;
+    key = o > key ? o : key;
+  }
+  return key;
+}
+
+// Writes the wave's key into its slot: one slot per wave of the launch
+// (every slot is written on every launch, so the reader sees no stale keys).
+__device__ __forceinline__ void wave_argmax(unsigned long long *slots, int slot, float v, int row, bool valid) {
+  const unsigned long long key = wave_argmax_key(v, row, valid);
+  if ((threadIdx.x & (kWave - 1)) == 0) slots[slot] = key;
 }
 
 // 1/sqrt(sum(x[0..cols)^2)/cols + eps) (norm.cpp:20-28) from per-thread
@@ -271,9 +330,12 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_kernel(GemvArgs a, int
 #pragma unroll
   for (int j = 0; j < XJ; ++j) {
     const int c2 = min(wave + j * WAVES, C2 - 1);
-    load_x4(a.x, k0 + c2 * kRotChunk, a.cols, lane, xv[j][0], xv[j][1], xv[j][2], xv[j][3]);
+    if (a.xmode == kXModeAttnMerge)
+      load_x4_attn(a, k0 + c2 * kRotChunk, lane, xv[j][0], xv[j][1], xv[j][2], xv[j][3]);
+    else
+      load_x4(a.x, k0 + c2 * kRotChunk, a.cols, lane, xv[j][0], xv[j][1], xv[j][2], xv[j][3]);
   }
-  if (a.xmode != kXModeNone) {
+  if (a.xmode == kXModeRmsNorm || a.xmode == kXModeSiluMul) {
 #pragma unroll
     for (int j = 0; j < XJ; ++j) load_aux4(a, k0 + min(wave + j * WAVES, C2 - 1) * kRotChunk, lane, aux[j]);
   }
@@ -345,7 +407,9 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_kernel(GemvArgs a, int
 
   // ---- split-K reduction --------------------------------------------------
   if (splits == 1) {
-    if (active && row < a.rows) a.y[row] = a.bias ? acc + a.bias[row] : acc;
+    const float out = a.bias && active && row < a.rows ? acc + a.bias[row] : acc;
+    if (active && row < a.rows) a.y[row] = out;
+    if (a.amax) wave_argmax(a.amax, blockIdx.x * WAVES + wave, out, row, active && row < a.rows);
     return;
   }
   float *part = a.partials + size_t(split) * a.Npad;
@@ -376,6 +440,7 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_kernel(GemvArgs a, int
     if (ticket != unsigned(splits - 1)) return;
   }
   const int r = rb * ROWS + threadIdx.x;
+  float out = 0.0f;
   if (r < a.rows) {
     // Sum the partials in split order; loads go out 8 at a time so their
     // latencies overlap.
@@ -391,8 +456,10 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_kernel(GemvArgs a, int
 #pragma unroll
       for (int j = 0; j < 8; ++j) s += v[j];
     }
-    a.y[r] = a.bias ? s + a.bias[r] : s;
+    out = a.bias ? s + a.bias[r] : s;
+    a.y[r] = out;
   }
+  if (a.amax) wave_argmax(a.amax, rb * WAVES + wave, out, r, r < a.rows);
   if (threadIdx.x == 0) __hip_atomic_store(a.counters + rb, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -402,7 +469,7 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_kernel(GemvArgs a, int
 // in a fixed order.
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restrict__ partials, int splits, int Npad,
                                                             int rows, const float *__restrict__ bias,
-                                                            float *__restrict__ y) {
+                                                            float *__restrict__ y, unsigned long long *amax) {
   __shared__ float q[4][kWave];
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
   const int r = blockIdx.x * kWave + lane;
@@ -411,9 +478,13 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restr
     for (int k = wave; k < splits; k += 4) s += partials[size_t(k) * Npad + r];
   q[wave][lane] = s;
   __syncthreads();
-  if (wave == 0 && r < rows) {
-    const float t = (q[0][lane] + q[1][lane]) + (q[2][lane] + q[3][lane]);
-    y[r] = bias ? t + bias[r] : t;
+  if (wave == 0) {
+    float t = (q[0][lane] + q[1][lane]) + (q[2][lane] + q[3][lane]);
+    if (r < rows) {
+      t = bias ? t + bias[r] : t;
+      y[r] = t;
+    }
+    if (amax) wave_argmax(amax, blockIdx.x, t, r, r < rows);
   }
 }
 
@@ -466,9 +537,12 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_fullk_kernel(GemvArgs 
 #pragma unroll
   for (int j = 0; j < XJ; ++j) {
     const int c2 = min(wave + j * WAVES, C2n - 1);
-    load_x4(a.x, c2 * kRotChunk, a.cols, lane, xv[j][0], xv[j][1], xv[j][2], xv[j][3]);
+    if (a.xmode == kXModeAttnMerge)
+      load_x4_attn(a, c2 * kRotChunk, lane, xv[j][0], xv[j][1], xv[j][2], xv[j][3]);
+    else
+      load_x4(a.x, c2 * kRotChunk, a.cols, lane, xv[j][0], xv[j][1], xv[j][2], xv[j][3]);
   }
-  if (a.xmode != kXModeNone) {
+  if (a.xmode == kXModeRmsNorm || a.xmode == kXModeSiluMul) {
 #pragma unroll
     for (int j = 0; j < XJ; ++j) load_aux4(a, min(wave + j * WAVES, C2n - 1) * kRotChunk, lane, aux[j]);
   }
@@ -561,13 +635,17 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_fullk_kernel(GemvArgs 
   // ---- in-workgroup reduction over the k-slices, fixed order --------------
   red[s * RW + rl] = acc;
   __syncthreads();
+  const int r = blockIdx.x * RW + threadIdx.x;
+  float t = 0.0f;
   if (threadIdx.x < RW) {
-    const int r = blockIdx.x * RW + threadIdx.x;
-    float t = 0.0f;
 #pragma unroll 8
     for (int k = 0; k < NS; ++k) t += red[k * RW + threadIdx.x];
-    if (r < a.rows) a.y[r] = a.bias ? t + a.bias[r] : t;
+    if (r < a.rows) {
+      t = a.bias ? t + a.bias[r] : t;
+      a.y[r] = t;
+    }
   }
+  if (a.amax && threadIdx.x < kWave) wave_argmax(a.amax, blockIdx.x, t, r, threadIdx.x < RW && r < a.rows);
 }
 
 template <int FMT, int WAVES, int H, int CPS, bool STAGED>
@@ -635,10 +713,18 @@ static int launch_fmt(const GemvArgs &a, hipStream_t st) {
   const int splits = a.Kp / a.kslice;
   if (splits > 1 && a.reduce == kReduceTwoPass)
     splitk_reduce_kernel<<<dim3((a.rows + kWave - 1) / kWave), dim3(256), 0, st>>>(a.partials, splits, a.Npad,
-                                                                                  a.rows, a.bias, a.y);
+                                                                                  a.rows, a.bias, a.y, a.amax);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(LMX_ERR_LAUNCH_FAILED, "lut_gemv launch: %s", hipGetErrorString(e));
   return LMX_OK;
+}
+
+size_t gemv_argmax_slots(const GemvArgs &a) {
+  if (a.fullk) return size_t((a.Npad + kWave / fullk_shape(a.fullk).h - 1) / (kWave / fullk_shape(a.fullk).h));
+  const int splits = a.Kp / a.kslice;
+  if (splits == 1) return size_t((a.Npad + a.waves * kWave - 1) / (a.waves * kWave)) * size_t(a.waves);
+  if (a.reduce == kReduceTwoPass) return size_t((a.rows + kWave - 1) / kWave);
+  return size_t((a.Npad + a.waves * kWave - 1) / (a.waves * kWave)) * size_t(a.waves);
 }
 
 int launch_gemv(int fmt, const GemvArgs &a, void *stream) {

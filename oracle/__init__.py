@@ -218,17 +218,23 @@ class OracleDecoder:
         return logits
 
 
+_SPREAD = None
+
+
 def int4_blocks_from_planes(planes, scales):
     """Canonical 4-bit planes [4, rows, cols/8] + group-256 scales [1, rows, cols/256]
     -> the reference's Int4Block bytes (types.hpp:174-202: even index in the high nibble)."""
-    rows = planes.shape[1]
-    bits = np.unpackbits(planes, axis=-1, bitorder="big")            # [4, rows, cols]
-    q = (bits[0] | (bits[1] << 1) | (bits[2] << 2) | (bits[3] << 3)).astype(np.uint8)
-    cols = q.shape[1]
-    nb = cols // 256
-    q = q.reshape(rows, nb, 256)
-    out = np.zeros((rows, nb, 132), np.uint8)
-    out[:, :, :128] = (q[:, :, 0::2] << 4) | q[:, :, 1::2]
+    global _SPREAD
+    if _SPREAD is None:   # plane byte -> its 8 bits at nibble positions, weight j at nibble 7-j
+        b = np.arange(256, dtype=np.uint32)
+        _SPREAD = sum(((b >> (7 - j)) & 1) << (4 * (7 - j)) for j in range(8)).astype(np.uint32)
+    rows, rb = planes.shape[1], planes.shape[2]
+    codes = (_SPREAD[planes[0]] | (_SPREAD[planes[1]] << 1) | (_SPREAD[planes[2]] << 2)
+             | (_SPREAD[planes[3]] << 3))                                  # [rows, cols/8] x 8 nibbles
+    data = codes.astype(">u4").view(np.uint8).reshape(rows, rb * 4)      # byte i = q[2i] << 4 | q[2i+1]
+    nb = rb * 8 // 256
+    out = np.empty((rows, nb, 132), np.uint8)
+    out[:, :, :128] = data.reshape(rows, nb, 128)
     out[:, :, 128:] = f32(scales[0].reshape(rows, nb)).view(np.uint8).reshape(rows, nb, 4)
     return out.reshape(-1)
 
