@@ -71,9 +71,11 @@ int lmx_decoder_set_layer(lmx_decoder *d, size_t layer, const lmx_weight *qkv,
                           const lmx_weight *o, const lmx_weight *gate_up,
                           const lmx_weight *down, const float *input_norm,
                           const float *post_norm, const float *qkv_bias);
-/* Tied embedding / LM head (borrowed) and the final norm weight (host). */
-int lmx_decoder_set_head(lmx_decoder *d, const lmx_weight *embed_head,
-                         const float *final_norm);
+/* Embedding table and LM head (borrowed; the same handle when tied, as
+ * model.cpp:667-689 ties them), both vocab x hidden, and the final norm
+ * weight (host). */
+int lmx_decoder_set_head(lmx_decoder *d, const lmx_weight *embed,
+                         const lmx_weight *head, const float *final_norm);
 /* Starts a sequence: position 0, tokens[0..n) = tokens (host).  Positions
  * below n are teacher-forced: their argmax does not overwrite the next
  * token. */

@@ -42,6 +42,8 @@ EXPORTS = [
     "lmx_decoder_reset", "lmx_decoder_step", "lmx_decoder_tokens", "lmx_decoder_generate",
     # include/lutmac_synth.h
     "lmx_quantize_int4", "lmx_synth_int4_normal", "lmx_synth_normal",
+    # include/lutmac_model.h
+    "lmx_model_load", "lmx_model_destroy", "lmx_model_config", "lmx_model_decoder", "lmx_model_weight_format",
 ]
 
 
@@ -97,10 +99,15 @@ _SIGS = {
     "lmx_quantize_int4": ([_p, _sz, _sz, _sz, _p, _p], _i),
     "lmx_synth_int4_normal": ([ctypes.c_uint64, ctypes.c_uint64, _sz, _sz, ctypes.c_float, _sz, _p, _p], _i),
     "lmx_synth_normal": ([ctypes.c_uint64, ctypes.c_uint64, _sz, _sz, ctypes.c_float, _p], _i),
+    "lmx_model_load": ([ctypes.c_char_p, _sz, ctypes.POINTER(_p)], _i),
+    "lmx_model_destroy": ([_p], _i),
+    "lmx_model_config": ([_p, ctypes.POINTER(DecoderConfigC)], _i),
+    "lmx_model_decoder": ([_p], _p),
+    "lmx_model_weight_format": ([_p, _i, _i, ctypes.POINTER(_i)], _i),
     "lmx_decoder_create": ([ctypes.POINTER(DecoderConfigC), ctypes.POINTER(_p)], _i),
     "lmx_decoder_destroy": ([_p], _i),
     "lmx_decoder_set_layer": ([_p, _sz, _p, _p, _p, _p, _p, _p, _p], _i),
-    "lmx_decoder_set_head": ([_p, _p, _p], _i),
+    "lmx_decoder_set_head": ([_p, _p, _p, _p], _i),
     "lmx_decoder_reset": ([_p, _p, _sz], _i),
     "lmx_decoder_step": ([_p, _p, _p], _i),
     "lmx_decoder_tokens": ([_p, _p, _sz, _p], _i),

@@ -306,7 +306,7 @@ struct lmx_decoder {
     float *in_norm = nullptr, *post_norm = nullptr, *qkv_bias = nullptr;
   };
   std::vector<Layer> layers;
-  const lmx_weight *head = nullptr;
+  const lmx_weight *embed = nullptr, *head = nullptr;   // equal when tied
   float *final_norm = nullptr;
   float *hidden = nullptr, *qkv = nullptr, *gate_up = nullptr, *logits = nullptr;
   float *kcache = nullptr, *vcache = nullptr, *freq = nullptr;
@@ -419,7 +419,7 @@ int upload(lmx_decoder *d, float **dst, const float *src, size_t n) {
 
 int step(lmx_decoder *d, float *logits_out, hipStream_t st) {
   const lmx_decoder_config &c = d->cfg;
-  int r = embed(d->head, d->tokens, d->pos, d->hidden, st);
+  int r = embed(d->embed, d->tokens, d->pos, d->hidden, st);
   if (r) return r;
   for (size_t l = 0; l < c.n_layers; ++l) {
     const lmx_decoder::Layer &L = d->layers[l];
@@ -547,17 +547,21 @@ int lmx_decoder_set_layer(lmx_decoder *d, size_t layer, const lmx_weight *qkv, c
   return LMX_OK;
 }
 
-int lmx_decoder_set_head(lmx_decoder *d, const lmx_weight *embed_head, const float *final_norm) {
+int lmx_decoder_set_head(lmx_decoder *d, const lmx_weight *embed, const lmx_weight *head, const float *final_norm) {
   if (!d) return fail(LMX_ERR_INVALID_ARGUMENT, "decoder is NULL");
   if (!final_norm) return fail(LMX_ERR_INVALID_ARGUMENT, "final norm is NULL");
-  int st = check_shape(embed_head, d->cfg.vocab, d->cfg.hidden, "embedding/head");
-  if (st) return st;
-  if (embed_head->device != d->device) return fail(LMX_ERR_INVALID_ARGUMENT, "weight on another device");
+  int st;
+  if ((st = check_shape(embed, d->cfg.vocab, d->cfg.hidden, "embedding")) ||
+      (st = check_shape(head, d->cfg.vocab, d->cfg.hidden, "head")))
+    return st;
+  if (embed->device != d->device || head->device != d->device)
+    return fail(LMX_ERR_INVALID_ARGUMENT, "weight on another device");
   if ((st = upload(d, &d->final_norm, final_norm, d->cfg.hidden))) return st;
-  const size_t slots = gemv_argmax_slots(weight_args(embed_head));
+  const size_t slots = gemv_argmax_slots(weight_args(head));
   if ((st = d->alloc(reinterpret_cast<void **>(&d->amax), slots * sizeof(unsigned long long)))) return st;
   d->amax_slots = slots;
-  d->head = embed_head;
+  d->embed = embed;
+  d->head = head;
   return LMX_OK;
 }
 

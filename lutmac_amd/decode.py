@@ -126,29 +126,11 @@ class SyntheticModel:
                 "gate_up": (2 * c.ffn, c.hidden), "down": (c.hidden, c.ffn)}
 
 
-class Decoder:
-    """Device decoder over LUT-GEMV weight handles (lutmac_decode.h)."""
+class _DecoderOps:
+    """Token-step operations over an lmx_decoder handle (self._h)."""
 
-    def __init__(self, model):
-        self.model, self.cfg = model, model.cfg
-        self._h = None
-        self.weights = []
-        shapes = model.shapes()
-        c = self.cfg
-        h = ctypes.c_void_p()
-        cs = c.c_struct()
-        check(lib().lmx_decoder_create(ctypes.byref(cs), ctypes.byref(h)))
-        self._h = h
-        for i, L in enumerate(model.layers):
-            ws = [Weight.from_planes(FMT_INT4, L[n][0], L[n][1], *shapes[n], model.group)
-                  for n in ("qkv", "o", "gate_up", "down")]
-            self.weights += ws
-            bias = None if L["qkv_bias"] is None else L["qkv_bias"]
-            check(lib().lmx_decoder_set_layer(self._h, i, *[w.handle for w in ws], _np_ptr(L["in_norm"]),
-                                              _np_ptr(L["post_norm"]),
-                                              None if bias is None else _np_ptr(bias)))
-        self.head = Weight.from_planes(FMT_INT4, model.head[0], model.head[1], c.vocab, c.hidden, model.group)
-        check(lib().lmx_decoder_set_head(self._h, self.head.handle, _np_ptr(model.final_norm)))
+    cfg = None
+    _h = None
 
     def reset(self, tokens):
         t = np.ascontiguousarray(tokens, np.int32)
@@ -175,6 +157,38 @@ class Decoder:
                                          ctypes.byref(t0), ctypes.byref(t1), _stream_ptr(stream)))
         return out, t0.value, t1.value
 
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Decoder(_DecoderOps):
+    """Device decoder over LUT-GEMV weight handles built from a SyntheticModel."""
+
+    def __init__(self, model):
+        self.model, self.cfg = model, model.cfg
+        self._h = None
+        self.weights = []
+        self.head = None
+        shapes = model.shapes()
+        c = self.cfg
+        h = ctypes.c_void_p()
+        cs = c.c_struct()
+        check(lib().lmx_decoder_create(ctypes.byref(cs), ctypes.byref(h)))
+        self._h = h
+        for i, L in enumerate(model.layers):
+            ws = [Weight.from_planes(FMT_INT4, L[n][0], L[n][1], *shapes[n], model.group)
+                  for n in ("qkv", "o", "gate_up", "down")]
+            self.weights += ws
+            bias = None if L["qkv_bias"] is None else L["qkv_bias"]
+            check(lib().lmx_decoder_set_layer(self._h, i, *[w.handle for w in ws], _np_ptr(L["in_norm"]),
+                                              _np_ptr(L["post_norm"]),
+                                              None if bias is None else _np_ptr(bias)))
+        self.head = Weight.from_planes(FMT_INT4, model.head[0], model.head[1], c.vocab, c.hidden, model.group)
+        check(lib().lmx_decoder_set_head(self._h, self.head.handle, self.head.handle, _np_ptr(model.final_norm)))
+
     def close(self):
         if self._h:
             lib().lmx_decoder_destroy(self._h)
@@ -182,15 +196,37 @@ class Decoder:
         for w in self.weights:
             w.close()
         self.weights = []
-        if getattr(self, "head", None) is not None:
+        if self.head is not None:
             self.head.close()
             self.head = None
 
-    def __del__(self):
-        try:
-            self.close()
-        except Exception:
-            pass
+
+class LutmacModel(_DecoderOps):
+    """A .lutmac v1 file loaded onto the device decoder (lutmac_model.h): the
+    counterpart of load_model (src/model.cpp:576-701)."""
+
+    def __init__(self, path, max_seq=0):
+        m = ctypes.c_void_p()
+        check(lib().lmx_model_load(str(path).encode(), max_seq, ctypes.byref(m)))
+        self._m = m
+        cs = DecoderConfigC()
+        check(lib().lmx_model_config(self._m, ctypes.byref(cs)))
+        self.config_c = cs
+        self.cfg = DecoderConfig(cs.hidden, cs.n_layers, cs.n_heads, cs.n_kv_heads, cs.head_dim, cs.ffn, cs.vocab,
+                                 cs.max_seq, cs.rms_eps, cs.rope_theta, cs.rope_mode, cs.rope_factor,
+                                 cs.rope_low_freq_factor, cs.rope_high_freq_factor, cs.rope_orig_max_pos)
+        self._h = ctypes.c_void_p(lib().lmx_model_decoder(self._m))
+
+    def weight_format(self, layer, which=0):
+        f = ctypes.c_int()
+        check(lib().lmx_model_weight_format(self._m, layer, which, ctypes.byref(f)))
+        return f.value
+
+    def close(self):
+        if getattr(self, "_m", None):
+            lib().lmx_model_destroy(self._m)
+            self._m = None
+            self._h = None
 
 
 def small_config(**kw):

@@ -243,7 +243,8 @@ class RefDecoder:
     """The reference's own Model::forward (oracle/_ref/libref.so) on a 4-bit model with
     group-256 scales and the reference's RoPE form: teacher-forced logits."""
 
-    def __init__(self, model, blocks=None):
+    @staticmethod
+    def _bind():
         R = ref()
         if R is None:
             raise RuntimeError("oracle/_ref/libref.so not built")
@@ -252,14 +253,44 @@ class RefDecoder:
             ("ref_model_set_linear", [_p, _sz, ctypes.c_int, _p, _sz, _sz, _sz], None),
             ("ref_model_set_norms", [_p, _sz, _p, _p], None),
             ("ref_model_set_embed", [_p, _p, _sz, _p], None),
+            ("ref_model_set_embed_fmt", [_p, ctypes.c_int, _p, _sz, _p], None),
+            ("ref_model_set_biases", [_p, _sz, _p, _p, _p], None),
+            ("ref_model_save", [_p, ctypes.c_char_p, ctypes.c_int], ctypes.c_int),
+            ("ref_model_load", [ctypes.c_char_p], _p),
             ("ref_model_forward", [_p, ctypes.c_int, _sz, _p], None),
             ("ref_model_destroy", [_p], None),
         ]:
             f = getattr(R, name)
             f.argtypes, f.restype = args, res
+        return R
+
+    @classmethod
+    def from_file(cls, path, vocab):
+        """The reference's own load_model of a .lutmac file."""
+        R = cls._bind()
+        self = cls.__new__(cls)
+        self.h = R.ref_model_load(str(path).encode())
+        if not self.h:
+            raise ValueError(f"reference load_model failed for {path}")
+        self.vocab = vocab
+        return self
+
+    def save(self, path, with_biases=False):
+        """Writes the model with the reference's own save_lutmac."""
+        if ref().ref_model_save(self.h, str(path).encode(), int(with_biases)) != 1:
+            raise ValueError("reference save_lutmac failed")
+
+    def set_embedding(self, fmt, blocks, final_norm):
+        """Replaces the (tied) embedding with reference blocks of format 6 or 7."""
+        blocks = np.ascontiguousarray(blocks, np.uint8)
+        fn = f32(final_norm)
+        ref().ref_model_set_embed_fmt(self.h, fmt, _ptr(blocks), blocks.size // BLOCK_BYTES[fmt], _ptr(fn))
+
+    def __init__(self, model, blocks=None):
+        R = self._bind()
         c = model.cfg
         assert model.group == 256 and c.rope_mode == 0, "reference model: group-256 blocks, reference RoPE"
-        self.cfg = c
+        self.cfg, self.vocab = c, c.vocab
         self.h = R.ref_model_create(c.hidden, c.n_layers, c.n_heads, c.n_kv_heads, c.head_dim, c.ffn, c.vocab,
                                     c.max_seq, c.rms_eps, c.rope_theta, c.rope_factor)
         qd, kvd = c.q_dim, c.kv_dim
@@ -275,6 +306,10 @@ class RefDecoder:
             self._set(i, 6, *Ly["down"], c.hidden, c.ffn)
             a, b = f32(Ly["in_norm"]), f32(Ly["post_norm"])
             R.ref_model_set_norms(self.h, i, _ptr(a), _ptr(b))
+            if Ly["qkv_bias"] is not None:
+                qb = f32(Ly["qkv_bias"])
+                R.ref_model_set_biases(self.h, i, _ptr(qb[:qd].copy()), _ptr(qb[qd:qd + kvd].copy()),
+                                       _ptr(qb[qd + kvd:].copy()))
         blk = int4_blocks_from_planes(*model.head)
         fn = f32(model.final_norm)
         R.ref_model_set_embed(self.h, _ptr(blk), blk.size // 132, _ptr(fn))
@@ -284,7 +319,7 @@ class RefDecoder:
         ref().ref_model_set_linear(self.h, layer, which, _ptr(blk), blk.size // 132, rows, cols)
 
     def step(self, token, pos):
-        logits = np.zeros(self.cfg.vocab, np.float32)
+        logits = np.zeros(self.vocab, np.float32)
         ref().ref_model_forward(self.h, int(token), pos, _ptr(logits))
         return logits
 

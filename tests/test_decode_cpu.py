@@ -128,3 +128,64 @@ def test_synthetic_model_shapes_and_determinism():
         assert np.array_equal(m1.layers[1][n][0], m2.layers[1][n][0])
     assert m1.head[0].shape == (4, cfg.vocab, cfg.hidden // 8)
     assert m1.layers[0]["qkv_bias"].shape == (cfg.q_dim + 2 * cfg.kv_dim,)
+
+
+@needs_ref
+def test_oracle_decode_matches_reference_model_bias_and_rope_factor():
+    cfg = D.small_config(rope_mode=D.ROPE_REFERENCE, rope_factor=2.0, rope_theta=10000.0, qkv_bias=True)
+    m = D.SyntheticModel(cfg, seed=21, group=256, random_norms=True)
+    toks = np.random.default_rng(22).integers(0, cfg.vocab, 10)
+    assert teacher_forced(oracle.OracleDecoder(m), oracle.RefDecoder(m), toks) < TOL
+
+
+@needs_ref
+def test_reference_lutmac_round_trip(tmp_path):
+    # the reference's own save_lutmac + load_model reproduce the in-memory model exactly
+    cfg = D.small_config(rope_mode=D.ROPE_REFERENCE, rope_factor=1.0, rope_theta=10000.0, qkv_bias=True)
+    m = D.SyntheticModel(cfg, seed=23, group=256, random_norms=True)
+    r = oracle.RefDecoder(m)
+    path = tmp_path / "m.lutmac"
+    r.save(path, with_biases=True)
+    r2 = oracle.RefDecoder.from_file(path, cfg.vocab)
+    for pos, t in enumerate(np.random.default_rng(24).integers(0, cfg.vocab, 4)):
+        assert np.array_equal(r.step(t, pos), r2.step(t, pos))
+
+
+def _lutmac_bytes(meta, data=b""):
+    import json
+    import struct
+    js = json.dumps(meta).encode()
+    head = b"LUTMAC01" + struct.pack("<II", 1, len(js)) + js
+    return head + b"\0" * ((-len(head)) % 256) + data
+
+
+def test_lutmac_loader_rejects_bad_files(tmp_path):
+    import ctypes
+    h = ctypes.c_void_p()
+    L.lib().lmx_model_load(b"/nonexistent/x.lutmac", 0, ctypes.byref(h))
+    assert L.lib().lmx_model_load(b"/nonexistent/x.lutmac", 0, ctypes.byref(h)) == L.ERR_INVALID_ARGUMENT
+    p = tmp_path / "bad.lutmac"
+    p.write_bytes(b"NOTLUTMAC" * 4)
+    assert L.lib().lmx_model_load(str(p).encode(), 0, ctypes.byref(h)) == L.ERR_INVALID_ARGUMENT
+    cfg = {"model_type": "llama", "vocab_size": 512, "hidden_size": 256, "intermediate_size": 512,
+           "num_hidden_layers": 1, "num_attention_heads": 4, "num_key_value_heads": 2, "head_dim": 64,
+           "rms_norm_eps": 1e-5, "rope_theta": 10000.0, "activation": 2, "norm_type": 1}
+    def t(name, shape, typ, nb):
+        return {"name": name, "shape": shape, "offset": 0, "type": typ, "num_blocks": nb}
+    lin = lambda n, r, c, typ="int4": t(f"model.layers.0.{n}", [r, c], typ, r * (c // 256))
+    tensors = [t("model.embed_tokens.weight", [512, 256], "int4", 512),
+               lin("self_attn.q_proj.weight", 256, 256), lin("self_attn.k_proj.weight", 128, 256),
+               lin("self_attn.v_proj.weight", 128, 256), lin("self_attn.o_proj.weight", 256, 256),
+               lin("mlp.gate_proj.weight", 512, 256, "int5"), lin("mlp.up_proj.weight", 512, 256),
+               lin("mlp.down_proj.weight", 256, 512)]
+    p.write_bytes(_lutmac_bytes({"config": cfg, "tensors": tensors}))
+    st = L.lib().lmx_model_load(str(p).encode(), 0, ctypes.byref(h))
+    assert st == L.ERR_UNSUPPORTED_FORMAT and b"int5" in L.lib().lmx_last_error()
+    bad = dict(cfg, activation=1)   # GELU
+    p.write_bytes(_lutmac_bytes({"config": bad, "tensors": tensors}))
+    assert L.lib().lmx_model_load(str(p).encode(), 0, ctypes.byref(h)) == L.ERR_UNSUPPORTED_FORMAT
+    p.write_bytes(_lutmac_bytes({"config": cfg, "tensors": tensors[1:]}))   # no embedding
+    assert L.lib().lmx_model_load(str(p).encode(), 0, ctypes.byref(h)) == L.ERR_INVALID_ARGUMENT
+    raw = b"LUTMAC01" + (2).to_bytes(4, "little") + (2).to_bytes(4, "little") + b"{}"
+    p.write_bytes(raw)                                                        # version 2
+    assert L.lib().lmx_model_load(str(p).encode(), 0, ctypes.byref(h)) == L.ERR_UNSUPPORTED_FORMAT

@@ -123,3 +123,42 @@ def test_decoder_rejects_bad_arguments(cuda):
         assert st == L.ERR_INVALID_ARGUMENT
     finally:
         L.lib().lmx_decoder_destroy(h)
+
+
+# ---- .lutmac v1 files (lutmac_model.h) ---------------------------------------
+needs_ref = pytest.mark.skipif(oracle.ref() is None, reason="oracle/_ref/libref.so not built")
+
+
+@needs_ref
+def test_lutmac_file_matches_reference_load_model(cuda, tmp_path):
+    # written by the reference's own save_lutmac; read by its load_model and by ours
+    cfg = D.small_config(rope_mode=D.ROPE_REFERENCE, rope_factor=2.0, rope_theta=10000.0, qkv_bias=True)
+    m = D.SyntheticModel(cfg, seed=31, group=256, random_norms=True)
+    path = tmp_path / "model.lutmac"
+    oracle.RefDecoder(m).save(path, with_biases=True)
+    ours = D.LutmacModel(path, max_seq=64)
+    assert ours.cfg.vocab == cfg.vocab and ours.cfg.n_kv_heads == cfg.n_kv_heads
+    assert ours.cfg.rope_factor == 2.0 and ours.weight_format(-1) == L.FMT_INT4
+    toks = np.random.default_rng(32).integers(0, cfg.vocab, 16)
+    check_against(ours, oracle.RefDecoder.from_file(path, cfg.vocab), toks)
+    out, _, _ = ours.generate(toks[:4], 8)
+    assert np.array_equal(out[:4], toks[:4])
+
+
+@needs_ref
+def test_lutmac_file_int8_embedding(cuda, tmp_path):
+    # real reference files carry int8 tied embeddings (tools/lutmac-quantize.cpp:385)
+    cfg = D.small_config(rope_mode=D.ROPE_REFERENCE, rope_factor=1.0, rope_theta=10000.0)
+    m = D.SyntheticModel(cfg, seed=33, group=256, random_norms=True)
+    ref = oracle.RefDecoder(m)
+    w = L.synth_normal(33, 999, cfg.vocab, cfg.hidden, 0.02)
+    nb = cfg.vocab * (cfg.hidden // 256)
+    blocks = np.zeros(nb * 260, np.uint8)
+    oracle.ref().ref_quantize(7, oracle._ptr(w), cfg.vocab, cfg.hidden, oracle._ptr(blocks), blocks.size)
+    ref.set_embedding(7, blocks, m.final_norm)
+    path = tmp_path / "int8emb.lutmac"
+    ref.save(path)
+    ours = D.LutmacModel(path, max_seq=64)
+    assert ours.weight_format(-1) == L.FMT_INT8 and ours.weight_format(-2) == L.FMT_INT8
+    toks = np.random.default_rng(34).integers(0, cfg.vocab, 10)
+    check_against(ours, oracle.RefDecoder.from_file(path, cfg.vocab), toks)
