@@ -198,6 +198,62 @@ def cpu_decode_baseline(budget_s, seed=2024):
                       f"in {el:.1f} s, 1 thread"}
 
 
+QWEN_SHAPES = {   # BASELINE config 5 linears (rows, cols): q|k|v fused, o, gate|up fused, down, tied head
+    "qkv": (2048, 1536), "o": (1536, 1536), "gate_up": (17920, 1536), "down": (1536, 8960),
+    "head": (151936, 1536)}
+
+
+def batched_bench(torch, L, batches=(1, 4, 16), steps=100):
+    """BASELINE config 5's question: the 4-bit LUT-GEMVs of a Qwen-2.5-1.5B
+    architecture at batch 1/4/16, weights streamed once per group of vectors
+    (batched kernel from batch 4).  Per shape: us per call; per batch: the
+    time of one decode step's linears (28 layers + head) and the implied
+    linear-layer tokens/s (attention and the rest of the step excluded)."""
+    out = {"shapes": {}, "per_batch": {}}
+    rng = np.random.default_rng(11)
+    for name, (n, k) in QWEN_SHAPES.items():
+        planes = rng.integers(0, 256, (4, n, k // 8), dtype=np.uint8)
+        scales = (np.abs(rng.standard_normal((1, n, k // 128))) * 0.02).astype(np.float32)
+        wbytes = n * k // 2 + n * (k // 128) * 4
+        copies = max(2, -(-ROTATE_BYTES // wbytes))
+        ws = [L.Weight.from_planes(L.FMT_INT4, planes, scales, n, k, 128) for _ in range(copies)]
+        res = {}
+        for B in batches:
+            x = torch.randn(B * k, device="cuda")
+            y = torch.empty(B * n, device="cuda")
+            stream = torch.cuda.current_stream()
+            for w in ws:                      # first batched call per handle grows its scratch
+                w.gemv(x, y, stream=stream)
+            torch.cuda.synchronize()
+            cg = torch.cuda.CUDAGraph()
+            side = torch.cuda.Stream()
+            side.wait_stream(stream)
+            with torch.cuda.graph(cg, stream=side):
+                for i in range(steps):
+                    ws[i % copies].gemv(x, y)
+            stream.wait_stream(side)
+            cg.replay()
+            torch.cuda.synchronize()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            cg.replay()
+            b.record(stream)
+            torch.cuda.synchronize()
+            us = a.elapsed_time(b) * 1e3 / steps
+            res[str(B)] = {"us": round(us, 3), "weight_GB_per_s": round(wbytes / us / 1e3, 1),
+                           "us_per_vector": round(us / B, 3)}
+            del cg
+        out["shapes"][name] = {"rows": n, "cols": k, **res}
+        for w in ws:
+            w.close()
+    for B in batches:
+        per_layer = sum(out["shapes"][s][str(B)]["us"] for s in ("qkv", "o", "gate_up", "down"))
+        step_us = 28 * per_layer + out["shapes"]["head"][str(B)]["us"]
+        out["per_batch"][str(B)] = {"linears_us_per_step": round(step_us, 1),
+                                    "linear_tokens_per_s": round(B / (step_us * 1e-6), 1)}
+    return out
+
+
 def calibrate_copy(nbytes=35717120, steps=200):
     """Plain device copy of a known size (torch's copy kernel), the yardstick
     that scales rocprofv3's FETCH_SIZE / WRITE_SIZE counters to bytes."""
@@ -229,6 +285,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true", help="skip the 1B-architecture decode")
+    ap.add_argument("--no-batched", action="store_true", help="skip the Qwen-shape batch 1/4/16 sweep")
     ap.add_argument("--decode-prompt", type=int, default=64)
     ap.add_argument("--decode-tokens", type=int, default=256)
     ap.add_argument("--cpu-decode-seconds", type=float, default=10.0)
@@ -264,6 +321,11 @@ def main():
         decode = decode_bench(args.decode_prompt, args.decode_tokens)
         print(f"# decode: {decode['tokens_per_s']} tokens/s ({decode['ms_per_token']} ms/token)",
               file=sys.stderr, flush=True)
+    batched = None if args.no_batched else batched_bench(torch, L)
+    if batched is not None:
+        print("# batched linears per step: " + ", ".join(
+            f"bs {b}: {v['linears_us_per_step']} us" for b, v in batched["per_batch"].items()),
+            file=sys.stderr, flush=True)
     cpu = None if args.no_cpu else cpu_baseline(args.size, args.cpu_seconds)
     if decode is not None and not args.no_cpu:
         decode["cpu_baseline"] = cpu_decode_baseline(args.cpu_decode_seconds)
@@ -290,6 +352,7 @@ def main():
                      "traffic": load_traffic(f"{head['format']}_{args.size}")},
         "cpu_baseline": cpu,
         "decode": decode,
+        "batched_qwen_linears": batched,
         "sweep": sweep,
     }
     print(json.dumps(line), flush=True)

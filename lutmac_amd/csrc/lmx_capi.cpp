@@ -125,6 +125,7 @@ void free_weight(lmx_weight *w) {
   if (w->d_partials) (void)hipFree(w->d_partials);
   if (w->d_counters) (void)hipFree(w->d_counters);
   if (w->d_xrot) (void)hipFree(w->d_xrot);
+  if (w->d_bpartials) (void)hipFree(w->d_bpartials);
   delete w;
 }
 
@@ -154,6 +155,7 @@ int upload(int fmt, size_t rows, size_t cols, size_t group, const uint8_t *plane
   w->reduce = choose_reduce();
   w->fullk = choose_fullk(fmt, w->Npad, w->Kp);
   w->staged = choose_staged();
+  w->batched = env_int("LMX_BATCHED", 1) != 0;
 
   std::vector<uint8_t> tiles;
   std::vector<float> sc;
@@ -217,6 +219,39 @@ int stage_if_needed(const lmx_weight *w, GemvArgs &a, void *stream) {
 }
 
 }  // namespace
+
+// Batched vectors in groups of 16/8/4 through the batched kernel (weights
+// read once per group; below 4 vectors one GEMV per vector is faster);
+// returns the number of vectors done.  Needs x
+// 16-byte aligned with cols % 4 == 0 (every vector then is).  The handle's
+// batched partials grow on first use (an allocation: make the first batched
+// call before capturing a graph).
+int gemv_batched(lmx_weight *w, GemvArgs a, const float *x, float *y, size_t batch, void *stream, size_t *done) {
+  *done = 0;
+  if (!w->batched || batch < 4 || reinterpret_cast<size_t>(x) % 16 || w->cols % 4) return LMX_OK;
+  const size_t splits = w->Kp / kRotChunk;
+  while (batch - *done >= 4) {
+    const size_t left = batch - *done;
+    const int nb = left >= 16 ? 16 : left >= 8 ? 8 : 4;
+    const size_t need = size_t(nb) * splits * w->Npad;
+    if (need > w->bpartials_cap) {
+      if (w->d_bpartials) (void)hipFree(w->d_bpartials);
+      w->d_bpartials = nullptr;
+      w->bpartials_cap = 0;
+      hipError_t e = hipMalloc(reinterpret_cast<void **>(&w->d_bpartials), 16 * splits * w->Npad * sizeof(float));
+      if (e != hipSuccess) return hip_fail(e, "hipMalloc (batched partials)");
+      w->bpartials_cap = 16 * splits * w->Npad;
+    }
+    a.x = x + *done * w->cols;
+    a.y = y + *done * w->rows;
+    a.cols = int(w->cols);
+    a.partials = w->d_bpartials;
+    int st = launch_gemv_batch(w->format, a, nb, stream);
+    if (st) return st;
+    *done += size_t(nb);
+  }
+  return LMX_OK;
+}
 
 GemvArgs weight_args(const lmx_weight *w) {
   GemvArgs a{};
@@ -426,10 +461,16 @@ int lmx_gemv(const lmx_weight *w, const float *x, float *y, size_t batch, unsign
     return fail(LMX_ERR_INVALID_ARGUMENT, "length-K FWHT needs cols a power of two in [256, 16384], got %zu",
                 w->cols);
   GemvArgs a = weight_args(w);
-  for (size_t b = 0; b < batch; ++b) {
+  size_t b0 = 0;
+  if (flags != LMX_ROTATE_FWHT_FULL) {
+    a.rotate = flags == LMX_ROTATE_FWHT256 ? LMX_ROTATE_FWHT256 : LMX_ROTATE_NONE;
+    if ((st = gemv_batched(const_cast<lmx_weight *>(w), a, x, y, batch, stream, &b0))) return st;
+  }
+  for (size_t b = b0; b < batch; ++b) {
     a.x = x + b * w->cols;
     a.y = y + b * w->rows;
     a.cols = int(w->cols);
+    a.partials = w->d_partials;
     a.rotate = flags == LMX_ROTATE_FWHT256 ? LMX_ROTATE_FWHT256 : LMX_ROTATE_NONE;
     if (flags == LMX_ROTATE_FWHT_FULL) {
       st = launch_fwht_full(a.x, w->d_xrot, w->cols, stream);
@@ -454,10 +495,13 @@ int lmx_linear(const lmx_weight *w, const float *bias, const float *x, float *y,
   GemvArgs a = weight_args(w);
   a.bias = bias;
   a.rotate = rotate ? LMX_ROTATE_FWHT256 : LMX_ROTATE_NONE;
-  for (size_t b = 0; b < batch; ++b) {
+  size_t b0 = 0;
+  if ((st = gemv_batched(const_cast<lmx_weight *>(w), a, x, y, batch, stream, &b0))) return st;
+  for (size_t b = b0; b < batch; ++b) {
     a.x = x + b * w->cols;
     a.y = y + b * w->rows;
     a.cols = int(w->cols);
+    a.partials = w->d_partials;
     if ((st = stage_if_needed(w, a, stream)) != LMX_OK) return st;
     st = launch_gemv(w->format, a, stream);
     if (st) return st;

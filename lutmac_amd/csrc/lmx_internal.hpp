@@ -124,6 +124,9 @@ constexpr int kReduceFenceAll = 1;  // same, with a device fence in every thread
 constexpr int kReduceTwoPass = 2;   // partials, then a separate reduce kernel
 
 int launch_gemv(int fmt, const GemvArgs &a, void *stream);
+// nb (2, 4, 8, 16) vectors at a.x + n*cols -> a.y + n*rows; a.partials holds
+// nb * (Kp/256) * Npad floats.
+int launch_gemv_batch(int fmt, const GemvArgs &a, int nb, void *stream);
 // Number of argmax key slots a launch with these arguments writes.
 size_t gemv_argmax_slots(const GemvArgs &a);
 int launch_fwht256(float *x, size_t n, void *stream);
@@ -156,6 +159,9 @@ struct lmx_weight {
   float *d_partials = nullptr;
   unsigned *d_counters = nullptr;
   float *d_xrot = nullptr;  // staging for LMX_ROTATE_FWHT_FULL (cols floats)
+  bool batched = true;           // batch >= 2 through the batched kernel (LMX_BATCHED=0: one GEMV per vector)
+  float *d_bpartials = nullptr;  // batched partials, grown on the first batched call
+  size_t bpartials_cap = 0;      // floats
 };
 
 namespace lmx {

@@ -727,6 +727,175 @@ size_t gemv_argmax_slots(const GemvArgs &a) {
   return size_t((a.Npad + a.waves * kWave - 1) / (a.waves * kWave)) * size_t(a.waves);
 }
 
+// ---------------------------------------------------------------------------
+// Batched GEMV: y_b = W x_b for NB activation vectors with the weights read
+// once (replaces lut_linear's per-row loop, lut_gemm_scalar.cpp:76-79).  A
+// workgroup owns 256 rows (4 waves, one row per lane) and a k-slice of 256;
+// the tables of the NB vectors sit interleaved per group in LDS, table
+// (chunk c, group g, vector b) at ((c*32 + g)*NB + b)*64 bytes, so one v_perm
+// address serves all NB vectors and the vector picks the ds_read immediate.
+// Partials [NB][splits][Npad] go through batched_reduce_kernel.
+template <int NB>
+__device__ __forceinline__ void word_lookups_batch(uint32_t v, int i, uint32_t cbase, float *out) {
+  const uint32_t hi = (v >> 2) & 0x3C3C3C3Cu, lo = (v << 2) & 0x3C3C3C3Cu;
+  uint32_t ad[8];
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    ad[2 * b] = __builtin_amdgcn_perm(cbase, hi, 0x0C060500u | b);
+    ad[2 * b + 1] = __builtin_amdgcn_perm(cbase, lo, 0x0C060500u | b);
+  }
+#pragma unroll
+  for (int n = 0; n < NB; ++n) {
+    float t[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) t[j] = lds_load(ad[j] + ((8 * i + j) * NB + n) * 64);
+    out[n] += ((t[0] + t[1]) + (t[2] + t[3])) + ((t[4] + t[5]) + (t[6] + t[7]));
+  }
+}
+
+template <int FMT, int NB>
+__global__ __launch_bounds__(256) void lut_gemv_batch_kernel(GemvArgs a, int row_blocks, int splits) {
+  constexpr int P = Fmt<FMT>::P, NA = Fmt<FMT>::NA, S = Fmt<FMT>::S;
+  constexpr int CH = kRotChunk / kChunk;   // 2 chunks of 128 per slice
+  __shared__ __attribute__((aligned(256))) float tables[CH * 32 * NB * 16];
+  __shared__ float xsum[NB][CH];
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  const int rb = blockIdx.x % row_blocks, split = blockIdx.x / row_blocks;
+  const int k0 = split * kRotChunk;
+  const int row = rb * 256 + wave * kWave + lane;
+  const bool active = rb * 256 + wave * kWave < a.Npad;
+  const int lr = min(row, a.Npad - 1);
+
+  // activations: wave w builds the tables of vectors w, w+4, ...
+  constexpr int XV = (NB + 3) / 4;
+  float xv[XV][4];
+#pragma unroll
+  for (int j = 0; j < XV; ++j) {
+    const int n = min(wave + 4 * j, NB - 1);
+    load_x4(a.x + size_t(n) * a.cols, k0, a.cols, lane, xv[j][0], xv[j][1], xv[j][2], xv[j][3]);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  u32x4 w[CH][P];
+  float sc[CH][S];
+  {
+    const u32x4 *__restrict__ pl = reinterpret_cast<const u32x4 *>(a.planes);
+    const size_t Npad = size_t(a.Npad);
+    const int c0 = k0 / kChunk;
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+#pragma unroll
+      for (int p = 0; p < P; ++p) w[c][p] = __builtin_nontemporal_load(pl + (size_t(c0 + c) * P + p) * Npad + lr);
+      const int g = (c0 + c) / a.group_chunks;
+#pragma unroll
+      for (int t = 0; t < S; ++t) sc[c][t] = a.scales[(size_t(t) * a.n_groups + g) * Npad + lr];
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < XV; ++j) {
+    const int n = wave + 4 * j;
+    if (n >= NB) break;   // wave-uniform
+    float x0 = xv[j][0], x1 = xv[j][1], x2 = xv[j][2], x3 = xv[j][3];
+    if (a.rotate == LMX_ROTATE_FWHT256) fwht256_regs(x0, x1, x2, x3, lane);
+    float t[16];
+    group_table(x0, x1, x2, x3, t);
+    const int c = lane >> 5, g = lane & 31;
+    float4 *dst = reinterpret_cast<float4 *>(tables + ((c * 32 + g) * NB + n) * 16);
+    dst[0] = make_float4(t[0], t[1], t[2], t[3]);
+    dst[1] = make_float4(t[4], t[5], t[6], t[7]);
+    dst[2] = make_float4(t[8], t[9], t[10], t[11]);
+    dst[3] = make_float4(t[12], t[13], t[14], t[15]);
+    if constexpr (Fmt<FMT>::XS) {
+      float xs = t[15];
+#pragma unroll
+      for (int d = 16; d >= 1; d >>= 1) xs += __shfl_xor(xs, d, 64);
+      if ((lane & 31) == 0) xsum[n][c] = xs;
+    }
+  }
+  __syncthreads();
+  if (!active) return;   // whole wavefronts; no barrier follows
+
+  float acc[NB];
+#pragma unroll
+  for (int n = 0; n < NB; ++n) acc[n] = 0.0f;
+  const uint32_t tbase = lds_addr(tables);
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    float A[NA][NB];
+#pragma unroll
+    for (int q = 0; q < NA; ++q)
+#pragma unroll
+      for (int n = 0; n < NB; ++n) A[q][n] = 0.0f;
+    const uint32_t cbase = tbase + c * 32 * NB * 64;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      uint32_t wi[P], v[NA];
+#pragma unroll
+      for (int p = 0; p < P; ++p) wi[p] = w[c][p][i];
+      lookup_words<FMT>(wi, v);
+#pragma unroll
+      for (int q = 0; q < NA; ++q) word_lookups_batch<NB>(v[q], i, cbase, A[q]);
+    }
+#pragma unroll
+    for (int n = 0; n < NB; ++n) {
+      float An[NA];
+#pragma unroll
+      for (int q = 0; q < NA; ++q) An[q] = A[q][n];
+      float xs = 0.0f;
+      if constexpr (Fmt<FMT>::XS) xs = xsum[n][c];
+      acc[n] = finish_chunk<FMT>(An, xs, sc[c], acc[n]);
+    }
+  }
+#pragma unroll
+  for (int n = 0; n < NB; ++n) a.partials[(size_t(n) * splits + split) * a.Npad + row] = acc[n];
+}
+
+// y[n*rows + r] = sum_s partials[n][s][r] (+ bias[r]) in split order.
+__global__ __launch_bounds__(64) void batched_reduce_kernel(const float *__restrict__ partials, int splits, int Npad,
+                                                            int rows, const float *__restrict__ bias,
+                                                            float *__restrict__ y) {
+  const int r = blockIdx.x * kWave + threadIdx.x, n = blockIdx.y;
+  if (r >= rows) return;
+  const float *p = partials + size_t(n) * splits * Npad + r;
+  float s = 0.0f;
+  for (int k = 0; k < splits; ++k) s += p[size_t(k) * Npad];
+  y[size_t(n) * rows + r] = bias ? s + bias[r] : s;
+}
+
+template <int FMT, int NB>
+static int launch_batch_nb(const GemvArgs &a, hipStream_t st) {
+  const int row_blocks = (a.Npad + 255) / 256, splits = a.Kp / kRotChunk;
+  lut_gemv_batch_kernel<FMT, NB><<<dim3(row_blocks * splits), dim3(256), 0, st>>>(a, row_blocks, splits);
+  batched_reduce_kernel<<<dim3((a.rows + kWave - 1) / kWave, NB), dim3(kWave), 0, st>>>(a.partials, splits, a.Npad,
+                                                                                     a.rows, a.bias, a.y);
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? LMX_OK : fail(LMX_ERR_LAUNCH_FAILED, "batched lut_gemv launch: %s", hipGetErrorString(e));
+}
+
+template <int FMT>
+static int launch_batch_fmt(const GemvArgs &a, int nb, hipStream_t st) {
+  switch (nb) {
+  case 2: return launch_batch_nb<FMT, 2>(a, st);
+  case 4: return launch_batch_nb<FMT, 4>(a, st);
+  case 8: return launch_batch_nb<FMT, 8>(a, st);
+  case 16: return launch_batch_nb<FMT, 16>(a, st);
+  }
+  return fail(LMX_ERR_INVALID_ARGUMENT, "batch group %d (2, 4, 8 or 16)", nb);
+}
+
+int launch_gemv_batch(int fmt, const GemvArgs &a, int nb, void *stream) {
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (fmt) {
+  case LMX_FMT_TERNARY: return launch_batch_fmt<LMX_FMT_TERNARY>(a, nb, st);
+  case LMX_FMT_BINARY: return launch_batch_fmt<LMX_FMT_BINARY>(a, nb, st);
+  case LMX_FMT_RRQ2: return launch_batch_fmt<LMX_FMT_RRQ2>(a, nb, st);
+  case LMX_FMT_RRQ3: return launch_batch_fmt<LMX_FMT_RRQ3>(a, nb, st);
+  case LMX_FMT_INT3: return launch_batch_fmt<LMX_FMT_INT3>(a, nb, st);
+  case LMX_FMT_INT4: return launch_batch_fmt<LMX_FMT_INT4>(a, nb, st);
+  case LMX_FMT_INT8: return launch_batch_fmt<LMX_FMT_INT8>(a, nb, st);
+  }
+  return fail(LMX_ERR_UNSUPPORTED_FORMAT, "unknown format %d", fmt);
+}
+
 int launch_gemv(int fmt, const GemvArgs &a, void *stream) {
   hipStream_t st = static_cast<hipStream_t>(stream);
   switch (fmt) {

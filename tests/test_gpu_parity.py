@@ -232,3 +232,31 @@ def test_forced_kernel_plans(cuda, monkeypatch, fmt, cfg, staged):
     y = w.gemv(dev(x), flags=L.ROTATE_FWHT256).cpu().numpy()
     ref = oracle_planes_gemv(fmt, planes, scales, rows, cols, g, x, L.ROTATE_FWHT256)
     assert rel_max_err(y, ref) < TOL
+
+
+# ---- batched GEMV (weights read once per group of 2/4/8/16 vectors) ----------
+@pytest.mark.parametrize("fmt", [1, 2, 3, 4, 5, 6, 7])
+@pytest.mark.parametrize("batch", [4, 7, 8, 16, 21])
+@pytest.mark.parametrize("rows,cols", [(300, 640), (513, 1536)])
+def test_batched_gemv(cuda, fmt, batch, rows, cols):
+    planes, scales, g = synth.make_weights(fmt, rows, cols, seed=fmt * 100 + batch, group=128)
+    xs = np.stack([synth.make_activations(cols, seed=1000 + s, outliers=True) for s in range(batch)])
+    w = L.Weight.from_planes(fmt, planes, scales, rows, cols, g)
+    y = w.gemv(dev(xs.ravel()), flags=L.ROTATE_FWHT256).cpu().numpy().reshape(batch, rows)
+    for b in range(batch):
+        ref = oracle_planes_gemv(fmt, planes, scales, rows, cols, g, xs[b], L.ROTATE_FWHT256)
+        assert rel_max_err(y[b], ref) < TOL, f"vector {b}"
+
+
+def test_batched_linear_bias_and_repeat(cuda):
+    rows, cols, batch = 2048, 2048, 16
+    planes, scales, g = synth.make_weights(L.FMT_INT4, rows, cols, seed=5)
+    xs = np.stack([synth.make_activations(cols, seed=s) for s in range(batch)])
+    bias = np.random.default_rng(3).standard_normal(rows).astype(np.float32)
+    w = L.Weight.from_planes(L.FMT_INT4, planes, scales, rows, cols, g)
+    y1 = w.linear(dev(xs.ravel()), bias=dev(bias)).cpu().numpy().reshape(batch, rows)
+    y2 = w.linear(dev(xs.ravel()), bias=dev(bias)).cpu().numpy().reshape(batch, rows)
+    assert np.array_equal(y1.view(np.uint32), y2.view(np.uint32))            # deterministic
+    for b in (0, 7, 15):
+        ref = oracle.planes_gemv(6, planes, scales, rows, cols, g, xs[b]) + bias
+        assert rel_max_err(y1[b], ref) < TOL
