@@ -30,6 +30,7 @@
 #include <vector>
 
 #include "lmx_internal.hpp"
+#include "lmx_lanes.hpp"
 #include "lutmac_decode.h"
 
 namespace lmx {
@@ -188,13 +189,9 @@ __global__ __launch_bounds__(512) void attn_chunk_kernel(const float *__restrict
     }
     sc = acc * scale;
   }
-  float m = sc;
-#pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) m = fmaxf(m, __shfl_xor(m, d, 64));
+  const float m = lane_max<32>(sc, lane);
   const float e = valid ? expf(sc - m) : 0.0f;
-  float l = e;
-#pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) l += __shfl_xor(l, d, 64);
+  const float l = lane_sum<32>(e, lane);
   pw[wave][lane] = lane < nold ? e : 0.0f;          // cached positions only
   const float enew = __shfl(e, jnew < 0 ? 0 : jnew, 64);
   __syncthreads();
@@ -233,12 +230,7 @@ __global__ __launch_bounds__(1024) void argmax_finish_kernel(const unsigned long
   __shared__ unsigned long long best[16];
   unsigned long long key = 0;
   for (int i = threadIdx.x; i < n_slots; i += 1024) key = slots[i] > key ? slots[i] : key;
-#pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) {
-    const uint32_t lo = __shfl_xor(uint32_t(key), d, 64), hi = __shfl_xor(uint32_t(key >> 32), d, 64);
-    const unsigned long long o = (static_cast<unsigned long long>(hi) << 32) | lo;
-    key = o > key ? o : key;
-  }
+  key = wave_max_key(key, threadIdx.x & (kWave - 1));
   if ((threadIdx.x & (kWave - 1)) == 0) best[threadIdx.x / kWave] = key;
   __syncthreads();
   if (threadIdx.x != 0) return;

@@ -29,6 +29,7 @@
 #include <hip/hip_runtime.h>
 
 #include "lmx_internal.hpp"
+#include "lmx_lanes.hpp"
 
 namespace lmx {
 
@@ -151,19 +152,28 @@ __device__ __forceinline__ void chunk_lookups(const u32x4 *wc, uint32_t cbase, u
 // output is produced by the same sequence of (a+b, a-b) as the reference's
 // scalar stage loop (transform_simd.cpp:14-23,26-45) followed by x(1/16),
 // so the result is bit-identical.
+template <int D>
+__device__ __forceinline__ void fwht_lane_stage(float &x0, float &x1, float &x2, float &x3, int lane) {
+  const bool top = (lane & D) == 0;
+  const float p0 = lane_xor<D>(x0, lane), p1 = lane_xor<D>(x1, lane);
+  const float p2 = lane_xor<D>(x2, lane), p3 = lane_xor<D>(x3, lane);
+  x0 = top ? x0 + p0 : p0 - x0;
+  x1 = top ? x1 + p1 : p1 - x1;
+  x2 = top ? x2 + p2 : p2 - x2;
+  x3 = top ? x3 + p3 : p3 - x3;
+}
+
+// The cross-lane stages exchange through DPP and permlane swaps (VALU), not
+// through the LDS, which the table reads keep busy.
 __device__ __forceinline__ void fwht256_regs(float &x0, float &x1, float &x2, float &x3, int lane) {
   float a0 = x0 + x1, a1 = x0 - x1, a2 = x2 + x3, a3 = x2 - x3;   // h = 1
   x0 = a0 + a2; x2 = a0 - a2; x1 = a1 + a3; x3 = a1 - a3;          // h = 2
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {                               // h = 4d
-    const bool top = (lane & d) == 0;
-    float p0 = __shfl_xor(x0, d, 64), p1 = __shfl_xor(x1, d, 64);
-    float p2 = __shfl_xor(x2, d, 64), p3 = __shfl_xor(x3, d, 64);
-    x0 = top ? x0 + p0 : p0 - x0;
-    x1 = top ? x1 + p1 : p1 - x1;
-    x2 = top ? x2 + p2 : p2 - x2;
-    x3 = top ? x3 + p3 : p3 - x3;
-  }
+  fwht_lane_stage<1>(x0, x1, x2, x3, lane);                        // h = 4
+  fwht_lane_stage<2>(x0, x1, x2, x3, lane);
+  fwht_lane_stage<4>(x0, x1, x2, x3, lane);
+  fwht_lane_stage<8>(x0, x1, x2, x3, lane);
+  fwht_lane_stage<16>(x0, x1, x2, x3, lane);
+  fwht_lane_stage<32>(x0, x1, x2, x3, lane);                       // h = 128
   x0 *= 0.0625f; x1 *= 0.0625f; x2 *= 0.0625f; x3 *= 0.0625f;
 }
 
@@ -187,6 +197,22 @@ __device__ __forceinline__ void load_x4(const float *__restrict__ x, int k0, int
   const int k = k0 + 4 * lane;
   const float4 v = *reinterpret_cast<const float4 *>(x + min(k, cols - 4));
   const bool in = k < cols;
+  x0 = in ? v.x : 0.0f;
+  x1 = in ? v.y : 0.0f;
+  x2 = in ? v.z : 0.0f;
+  x3 = in ? v.w : 0.0f;
+}
+
+// load_x4 in two halves: the raw (clamped) load, and the zeroing of lanes
+// past cols, applied where the values are first used so that no
+// instruction between the load and the weight stream waits for the data.
+__device__ __forceinline__ float4 load_x4_raw(const float *__restrict__ x, int k0, int cols, int lane) {
+  return *reinterpret_cast<const float4 *>(x + min(k0 + 4 * lane, cols - 4));
+}
+
+__device__ __forceinline__ void mask_x4(const float4 v, int k0, int cols, int lane, float &x0, float &x1, float &x2,
+                                        float &x3) {
+  const bool in = k0 + 4 * lane < cols;
   x0 = in ? v.x : 0.0f;
   x1 = in ? v.y : 0.0f;
   x2 = in ? v.z : 0.0f;
@@ -226,10 +252,13 @@ __device__ __forceinline__ void load_x4_attn(const GemvArgs &a, int k0, int lane
 
 // Second operand of the fused activation transform for the lane's 4
 // activations at k0 + 4*lane: the norm weights (kXModeRmsNorm) or the up
-// half of a gate|up vector (kXModeSiluMul).  Clamped in bounds like load_x4.
+// half of a gate|up vector (kXModeSiluMul).  Other modes load x[0..3] in
+// every lane (one cache line, result unused), so the load needs no branch.
+// Clamped in bounds like load_x4.
 __device__ __forceinline__ void load_aux4(const GemvArgs &a, int k0, int lane, float *aux) {
-  const float *p = a.xmode == kXModeRmsNorm ? a.xw : a.x + a.cols;
-  const float4 v = *reinterpret_cast<const float4 *>(p + min(k0 + 4 * lane, a.cols - 4));
+  const bool used = a.xmode == kXModeRmsNorm || a.xmode == kXModeSiluMul;
+  const float *p = a.xmode == kXModeRmsNorm ? a.xw : a.xmode == kXModeSiluMul ? a.x + a.cols : a.x;
+  const float4 v = *reinterpret_cast<const float4 *>(p + (used ? min(k0 + 4 * lane, a.cols - 4) : 0));
   aux[0] = v.x; aux[1] = v.y; aux[2] = v.z; aux[3] = v.w;
 }
 
@@ -258,13 +287,7 @@ __device__ __forceinline__ unsigned long long wave_argmax_key(float v, int row, 
     u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
     key = (static_cast<unsigned long long>(u) << 32) | (0xFFFFFFFFu - uint32_t(row));
   }
-#pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) {
-    const uint32_t lo = __shfl_xor(uint32_t(key), d, 64), hi = __shfl_xor(uint32_t(key >> 32), d, 64);
-    const unsigned long long o = (static_cast<unsigned long long>(hi) << 32) | lo;
-    key = o > key ? o : key;
-  }
-  return key;
+  return wave_max_key(key, threadIdx.x & (kWave - 1));
 }
 
 // Writes the wave's key into its slot: one slot per wave of the launch
@@ -279,8 +302,7 @@ __device__ __forceinline__ void wave_argmax(unsigned long long *slots, int slot,
 // workgroup gets the same bits.  red: NT/64 floats of LDS.
 template <int NT>
 __device__ float wg_inv_rms_from(float s, int cols, float eps, float *red) {
-#pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) s += __shfl_xor(s, d, 64);
+  s = lane_sum<32>(s, threadIdx.x & (kWave - 1));
   if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = s;
   __syncthreads();
   float t = 0.0f;
@@ -378,8 +400,7 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_kernel(GemvArgs a, int
     dst[3] = make_float4(t[12], t[13], t[14], t[15]);
     if constexpr (Fmt<FMT>::XS) {
       float s = t[15];
-#pragma unroll
-      for (int d = 16; d >= 1; d >>= 1) s += __shfl_xor(s, d, 64);
+      s = lane_sum<16>(s, lane);
       if ((lane & 31) == 0) xsum[c2 * 2 + (lane >> 5)] = s;
     }
   }
@@ -514,7 +535,9 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_fullk_kernel(GemvArgs 
   constexpr int RW = kWave / H;
   constexpr int NS = WAVES * H;
   constexpr uint32_t SSTRIDE = CPS * 32 * 64 + 256;
-  constexpr int XJ = (NS * CPS / 2 + WAVES - 1) / WAVES;   // 256-chunks per wave (upper bound)
+  // Wave w owns the 128-chunks of its k-slices, [w*H*CPS, (w+1)*H*CPS), and
+  // builds exactly their tables (XJ 256-chunks), so no other wave waits on it.
+  constexpr int XJ = H * CPS >= 2 ? H * CPS / 2 : 1;
   constexpr uint32_t PREFIX = fullk_prefix_bytes<WAVES, H, CPS>();
   extern __shared__ __attribute__((aligned(256))) float lds[];
   const int Kc = a.Kp / kChunk;
@@ -533,18 +556,15 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_fullk_kernel(GemvArgs 
 
   // ---- loads: activations for this wave's 256-chunks, then the weights ----
   const int C2n = a.Kp / kRotChunk;
-  float xv[XJ][4], aux[XJ][4];
+  const int own0 = wave * H * CPS, own1 = own0 + H * CPS;   // owned 128-chunks [own0, own1)
+  const int c2base = own0 / 2;
+  float4 xr[XJ];
+  float aux[XJ][4];
 #pragma unroll
   for (int j = 0; j < XJ; ++j) {
-    const int c2 = min(wave + j * WAVES, C2n - 1);
-    if (a.xmode == kXModeAttnMerge)
-      load_x4_attn(a, c2 * kRotChunk, lane, xv[j][0], xv[j][1], xv[j][2], xv[j][3]);
-    else
-      load_x4(a.x, c2 * kRotChunk, a.cols, lane, xv[j][0], xv[j][1], xv[j][2], xv[j][3]);
-  }
-  if (a.xmode == kXModeRmsNorm || a.xmode == kXModeSiluMul) {
-#pragma unroll
-    for (int j = 0; j < XJ; ++j) load_aux4(a, min(wave + j * WAVES, C2n - 1) * kRotChunk, lane, aux[j]);
+    const int c2 = min(c2base + j, C2n - 1);
+    xr[j] = load_x4_raw(a.x, c2 * kRotChunk, a.cols, lane);
+    load_aux4(a, c2 * kRotChunk, lane, aux[j]);
   }
   __builtin_amdgcn_sched_barrier(0);
   // Weight loads.  STAGED (CPS > 1 only) issues chunk 0 before the table
@@ -569,40 +589,55 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_fullk_kernel(GemvArgs 
   }
   if constexpr (STAGED) __builtin_amdgcn_sched_barrier(0);
 
-  // ---- prologue: (transform) -> (FWHT-256) -> group tables of the whole K -
-  // The waves' x registers cover all of x once (chunks past C2n are clamped
-  // duplicates and skipped), so the norm needs no second read of x.
+  // ---- prologue: (transform) -> (FWHT-256) -> this wave's group tables ---
+  // Lanes 0-31 / 32-63 hold the first / second 128-chunk of a 256-chunk; a
+  // lane's values count (norm, tables) only where the wave owns that chunk,
+  // which partitions x exactly, so the norm needs no second read of x.
+  // The attention merge (its own dependent loads) runs after the weight
+  // loads are issued, so the plain path has no branch between its loads; it
+  // replaces the raw x (zero past cols, like the mask applied below).
+  if (a.xmode == kXModeAttnMerge) {
+#pragma unroll
+    for (int j = 0; j < XJ; ++j)
+      load_x4_attn(a, min(c2base + j, C2n - 1) * kRotChunk, lane, xr[j].x, xr[j].y, xr[j].z, xr[j].w);
+  }
   float inv_rms = 1.0f;
   if (a.xmode == kXModeRmsNorm) {
     float ss = 0.0f;
 #pragma unroll
-    for (int j = 0; j < XJ; ++j)
-      if (wave + j * WAVES < C2n)
-        ss += (xv[j][0] * xv[j][0] + xv[j][1] * xv[j][1]) + (xv[j][2] * xv[j][2] + xv[j][3] * xv[j][3]);
+    for (int j = 0; j < XJ; ++j) {
+      const int ch = (c2base + j) * 2 + (lane >> 5);
+      float x0, x1, x2, x3;
+      mask_x4(xr[j], (c2base + j) * kRotChunk, a.cols, lane, x0, x1, x2, x3);
+      if (ch >= own0 && ch < own1 && c2base + j < C2n) ss += (x0 * x0 + x1 * x1) + (x2 * x2 + x3 * x3);
+    }
     inv_rms = wg_inv_rms_from<WAVES * kWave>(ss, a.cols, a.eps, red);
   }
 #pragma unroll
   for (int j = 0; j < XJ; ++j) {
-    const int c2 = wave + j * WAVES;
+    const int c2 = c2base + j;
     if (c2 >= C2n) break;   // wave-uniform
-    float x0 = xv[j][0], x1 = xv[j][1], x2 = xv[j][2], x3 = xv[j][3];
+    float x0, x1, x2, x3;
+    mask_x4(xr[j], c2 * kRotChunk, a.cols, lane, x0, x1, x2, x3);
     xform4(a.xmode, inv_rms, aux[j], x0, x1, x2, x3);
     if (a.rotate == LMX_ROTATE_FWHT256) fwht256_regs(x0, x1, x2, x3, lane);
     float t[16];
     group_table(x0, x1, x2, x3, t);
     const int ch = c2 * 2 + (lane >> 5);                      // 128-chunk of this group
+    const bool mine = ch >= own0 && ch < own1;
     const int ts = ch / CPS;                                  // its k-slice
     float4 *dst = reinterpret_cast<float4 *>(tables + ts * SSTRIDE + slice_shift<H>(ts) + (ch % CPS) * 2048 +
                                              (lane & 31) * 64);
-    dst[0] = make_float4(t[0], t[1], t[2], t[3]);
-    dst[1] = make_float4(t[4], t[5], t[6], t[7]);
-    dst[2] = make_float4(t[8], t[9], t[10], t[11]);
-    dst[3] = make_float4(t[12], t[13], t[14], t[15]);
+    if (mine) {
+      dst[0] = make_float4(t[0], t[1], t[2], t[3]);
+      dst[1] = make_float4(t[4], t[5], t[6], t[7]);
+      dst[2] = make_float4(t[8], t[9], t[10], t[11]);
+      dst[3] = make_float4(t[12], t[13], t[14], t[15]);
+    }
     if constexpr (Fmt<FMT>::XS) {
       float xs = t[15];
-#pragma unroll
-      for (int d = 16; d >= 1; d >>= 1) xs += __shfl_xor(xs, d, 64);
-      if ((lane & 31) == 0) xsum[ch] = xs;
+      xs = lane_sum<16>(xs, lane);
+      if ((lane & 31) == 0 && mine) xsum[ch] = xs;
     }
   }
   if constexpr (STAGED) {
@@ -610,12 +645,17 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_fullk_kernel(GemvArgs 
 #pragma unroll
     for (int c = 1; c < CPS; ++c) load_planes(c);
   }
-  __syncthreads();
+  // Each wave reads only the tables it wrote: a wave-scope fence (LDS
+  // operations of a wave complete in order) instead of a workgroup barrier,
+  // so every wave starts its lookups as soon as its own data is in.
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
 
   // ---- lookups over this lane's k-slice -----------------------------------
   float acc = 0.0f;
   {
-    // Lanes whose slice lies past K read slice used-1 (in bounds) and discard it.
+    // Lanes whose slice lies past K read slice used-1 (in bounds, possibly
+    // another wave's, possibly mid-write) and discard the result.
     const uint32_t tbase = lds_addr(lds) + PREFIX + min(s, used - 1) * SSTRIDE;   // 256-byte aligned
     const uint32_t shift = slice_shift<H>(s) * 0x01010101u;   // bits 6-7 of each byte
 #pragma unroll
@@ -806,8 +846,7 @@ __global__ __launch_bounds__(256) void lut_gemv_batch_kernel(GemvArgs a, int row
     dst[3] = make_float4(t[12], t[13], t[14], t[15]);
     if constexpr (Fmt<FMT>::XS) {
       float xs = t[15];
-#pragma unroll
-      for (int d = 16; d >= 1; d >>= 1) xs += __shfl_xor(xs, d, 64);
+      xs = lane_sum<16>(xs, lane);
       if ((lane & 31) == 0) xsum[n][c] = xs;
     }
   }
