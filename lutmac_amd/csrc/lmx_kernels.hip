@@ -152,15 +152,30 @@ __device__ __forceinline__ void chunk_lookups(const u32x4 *wc, uint32_t cbase, u
 // output is produced by the same sequence of (a+b, a-b) as the reference's
 // scalar stage loop (transform_simd.cpp:14-23,26-45) followed by x(1/16),
 // so the result is bit-identical.
+// One butterfly stage between lanes l and l ^ D: the lower lane keeps
+// own + partner, the upper lane partner - own.  For D = 16, 32 both lanes
+// read the pair as (lo, hi) and form lo + hi or lo - hi: the same operands.
 template <int D>
 __device__ __forceinline__ void fwht_lane_stage(float &x0, float &x1, float &x2, float &x3, int lane) {
   const bool top = (lane & D) == 0;
-  const float p0 = lane_xor<D>(x0, lane), p1 = lane_xor<D>(x1, lane);
-  const float p2 = lane_xor<D>(x2, lane), p3 = lane_xor<D>(x3, lane);
-  x0 = top ? x0 + p0 : p0 - x0;
-  x1 = top ? x1 + p1 : p1 - x1;
-  x2 = top ? x2 + p2 : p2 - x2;
-  x3 = top ? x3 + p3 : p3 - x3;
+  if constexpr (D >= 16) {
+    float l0, h0, l1, h1, l2, h2, l3, h3;
+    lane_pair<D>(x0, l0, h0);
+    lane_pair<D>(x1, l1, h1);
+    lane_pair<D>(x2, l2, h2);
+    lane_pair<D>(x3, l3, h3);
+    x0 = top ? l0 + h0 : l0 - h0;
+    x1 = top ? l1 + h1 : l1 - h1;
+    x2 = top ? l2 + h2 : l2 - h2;
+    x3 = top ? l3 + h3 : l3 - h3;
+  } else {
+    const float p0 = lane_xor<D>(x0, lane), p1 = lane_xor<D>(x1, lane);
+    const float p2 = lane_xor<D>(x2, lane), p3 = lane_xor<D>(x3, lane);
+    x0 = top ? x0 + p0 : p0 - x0;
+    x1 = top ? x1 + p1 : p1 - x1;
+    x2 = top ? x2 + p2 : p2 - x2;
+    x3 = top ? x3 + p3 : p3 - x3;
+  }
 }
 
 // The cross-lane stages exchange through DPP and permlane swaps (VALU), not
@@ -567,6 +582,16 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_fullk_kernel(GemvArgs 
     load_aux4(a, c2 * kRotChunk, lane, aux[j]);
   }
   __builtin_amdgcn_sched_barrier(0);
+#ifdef LMX_XWAIT
+#pragma unroll
+  for (int j = 0; j < XJ; ++j)
+    asm volatile("" ::"v"(xr[j].x), "v"(xr[j].y), "v"(xr[j].z), "v"(xr[j].w), "v"(aux[j][0]), "v"(aux[j][1]),
+                 "v"(aux[j][2]), "v"(aux[j][3]));
+#endif
+  // A CU returns vector loads roughly in issue order, so every wave's x
+  // requests go out before any wave's weight requests (the barrier does not
+  // wait for the loads): no wave's tables wait behind the weight stream.
+  __builtin_amdgcn_s_barrier();
   // Weight loads.  STAGED (CPS > 1 only) issues chunk 0 before the table
   // prologue and the later chunks after it, so that HBM serves chunk 0 of
   // every wave first and chunk 1 streams in while chunk 0 is looked up.

@@ -26,7 +26,7 @@ namespace lmx {
 
 template <int CTRL>
 __device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
-  return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, 0xF, 0xF, false));
+  return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), CTRL, 0xF, 0xF, true));
 }
 
 template <int D>
@@ -46,6 +46,23 @@ __device__ __forceinline__ uint32_t lane_xor_u32(uint32_t v, int lane) {
   } else {
     const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
     return (lane & 32) ? r[0] : r[1];
+  }
+}
+
+// For D = 16 or 32: lo / hi = the values of v in the lower / upper lane of
+// the pair (l, l ^ D) that holds this lane, in both lanes of the pair.
+template <int D>
+__device__ __forceinline__ void lane_pair(float v, float &lo, float &hi) {
+  static_assert(D == 16 || D == 32, "permlane swap distance");
+  const uint32_t u = __float_as_uint(v);
+  if constexpr (D == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    lo = __uint_as_float(r[0]);
+    hi = __uint_as_float(r[1]);
+  } else {
+    const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    lo = __uint_as_float(r[0]);
+    hi = __uint_as_float(r[1]);
   }
 }
 
