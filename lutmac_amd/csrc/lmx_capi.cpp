@@ -114,8 +114,8 @@ int choose_staged() {
 }
 
 int choose_reduce() {
-  const int env = env_int("LMX_REDUCE", kReduceTwoPass);
-  return (env == kReduceTicket || env == kReduceFenceAll) ? env : kReduceTwoPass;
+  const int env = env_int("LMX_REDUCE", kReduceTicket);
+  return (env == kReduceTwoPass || env == kReduceFenceAll) ? env : kReduceTicket;
 }
 
 void free_weight(lmx_weight *w) {

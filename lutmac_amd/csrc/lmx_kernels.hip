@@ -96,21 +96,29 @@ __device__ __forceinline__ float finish_chunk(const float *A, float xs, const fl
 
 
 // The 8 lookups of one 32-bit lookup word (word i of a 128-k chunk = groups
-// 8i..8i+7), summed as a balanced tree.  Addresses come from v_perm (table
-// base bytes 1-2, 4*nibble in byte 0, plus an optional bank shift in bits
-// 6-7); the group's table offset is the ds_read immediate.  All 64 lanes
-// read the same 16-entry table at a time: 16 consecutive dwords, no bank
-// conflicts.
-__device__ __forceinline__ float word_lookups(uint32_t v, int i, uint32_t cbase, uint32_t shift) {
+// 8i..8i+7).  Addresses come from v_perm (table base bytes 1-2, 4*nibble in
+// byte 0, plus an optional bank shift in bits 6-7); the group's table offset
+// is the ds_read immediate.  All 64 lanes read the same 16-entry table at a
+// time: 16 consecutive dwords, no bank conflicts.  word_reads issues the
+// reads, word_sum adds them as a balanced tree.
+__device__ __forceinline__ void word_reads(uint32_t v, int i, uint32_t cbase, uint32_t shift, float *t) {
   const uint32_t hi = ((v >> 2) & 0x3C3C3C3Cu) | shift;  // byte b: 4*nibble of group 8i+2b
   const uint32_t lo = ((v << 2) & 0x3C3C3C3Cu) | shift;  // byte b: 4*nibble of group 8i+2b+1
-  float t[8];
 #pragma unroll
   for (int b = 0; b < 4; ++b) {
     t[2 * b] = lds_load(__builtin_amdgcn_perm(cbase, hi, 0x0C060500u | b) + (8 * i + 2 * b) * 64);
     t[2 * b + 1] = lds_load(__builtin_amdgcn_perm(cbase, lo, 0x0C060500u | b) + (8 * i + 2 * b + 1) * 64);
   }
+}
+
+__device__ __forceinline__ float word_sum(const float *t) {
   return ((t[0] + t[1]) + (t[2] + t[3])) + ((t[4] + t[5]) + (t[6] + t[7]));
+}
+
+__device__ __forceinline__ float word_lookups(uint32_t v, int i, uint32_t cbase, uint32_t shift) {
+  float t[8];
+  word_reads(v, i, cbase, shift, t);
+  return word_sum(t);
 }
 
 // Table lookups of one 128-k chunk for one lane: NA accumulators over the
@@ -118,6 +126,27 @@ __device__ __forceinline__ float word_lookups(uint32_t v, int i, uint32_t cbase,
 template <int FMT>
 __device__ __forceinline__ void chunk_lookups(const u32x4 *wc, uint32_t cbase, uint32_t shift, float *A) {
   constexpr int P = Fmt<FMT>::P, NA = Fmt<FMT>::NA;
+  if constexpr (FMT != LMX_FMT_TERNARY) {
+    // Accumulator q reads plane q only.  Software pipeline over the NA*4
+    // words: the reads of word n+1 are in flight while word n is summed
+    // (workgroups with one wave per SIMD would otherwise wait out the LDS
+    // latency once per word).
+    float t[2][8];
+    auto word_of = [&](int n) {
+      uint32_t wi[P], v[NA];
+#pragma unroll
+      for (int p = 0; p < P; ++p) wi[p] = wc[p][n & 3];
+      lookup_words<FMT>(wi, v);
+      return v[n >> 2];
+    };
+    word_reads(word_of(0), 0, cbase, shift, t[0]);
+#pragma unroll
+    for (int n = 0; n < NA * 4; ++n) {
+      if (n + 1 < NA * 4) word_reads(word_of(n + 1), (n + 1) & 3, cbase, shift, t[(n + 1) & 1]);
+      A[n >> 2] += word_sum(t[n & 1]);
+    }
+    return;
+  }
   if constexpr (FMT == LMX_FMT_TERNARY) {
     // Both accumulators need both planes: word-outer.
 #pragma unroll
@@ -128,20 +157,6 @@ __device__ __forceinline__ void chunk_lookups(const u32x4 *wc, uint32_t cbase, u
       lookup_words<FMT>(wi, v);
 #pragma unroll
       for (int q = 0; q < NA; ++q) A[q] += word_lookups(v[q], i, cbase, shift);
-    }
-  } else {
-    // Accumulator q reads plane q only: plane-outer, so the lookups of a
-    // plane can start as soon as its load has landed.
-#pragma unroll
-    for (int q = 0; q < NA; ++q) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        uint32_t wi[P], v[NA];
-#pragma unroll
-        for (int p = 0; p < P; ++p) wi[p] = wc[p][i];
-        lookup_words<FMT>(wi, v);
-        A[q] += word_lookups(v[q], i, cbase, shift);
-      }
     }
   }
 }

@@ -234,6 +234,50 @@ def test_forced_kernel_plans(cuda, monkeypatch, fmt, cfg, staged):
     assert rel_max_err(y, ref) < TOL
 
 
+# ---- split-K reductions: last-workgroup ticket and two-pass ----------------
+@pytest.mark.parametrize("reduce", [0, 2])
+@pytest.mark.parametrize("kslice", [256, 512])
+@pytest.mark.parametrize("fmt", [1, 6, 7])
+def test_splitk_reductions(cuda, monkeypatch, reduce, kslice, fmt):
+    import torch
+    rows, cols = 1000, 4096
+    monkeypatch.setenv("LMX_FULLK", "0")
+    monkeypatch.setenv("LMX_REDUCE", str(reduce))
+    monkeypatch.setenv("LMX_KSLICE", str(kslice))
+    planes, scales, g = synth.make_weights(fmt, rows, cols, seed=60 + fmt, group=128)
+    x = synth.make_activations(cols, seed=61, outliers=True)
+    bias = np.random.default_rng(62).standard_normal(rows).astype(np.float32)
+    w = L.Weight.from_planes(fmt, planes, scales, rows, cols, g)
+    assert w.kernel_config()[:2] == (0, kslice)
+    ref = oracle_planes_gemv(fmt, planes, scales, rows, cols, g, x, L.ROTATE_FWHT256)
+    xd, bd = dev(x), dev(bias)
+    y1 = w.gemv(xd, flags=L.ROTATE_FWHT256).cpu().numpy()
+    y2 = w.gemv(xd, flags=L.ROTATE_FWHT256).cpu().numpy()     # counters were reset by call 1
+    assert rel_max_err(y1, ref) < TOL
+    assert np.array_equal(y1.view(np.uint32), y2.view(np.uint32))
+    # graph replays, with eager calls on the same handle in between
+    out = torch.empty(rows, dtype=torch.float32, device="cuda")
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        w.gemv(xd, y=out, flags=L.ROTATE_FWHT256)             # warm up off the capture
+    torch.cuda.current_stream().wait_stream(s)
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gr):
+        w.gemv(xd, y=out, flags=L.ROTATE_FWHT256)
+    for _ in range(3):
+        out.zero_()
+        gr.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(out.cpu().numpy().view(np.uint32), y1.view(np.uint32))
+        w.gemv(xd, flags=L.ROTATE_FWHT256)
+        torch.cuda.synchronize()
+    yb = w.linear(xd, bias=bd).cpu().numpy()                  # lmx_linear rotates 1-2 bit formats only
+    refb = oracle_planes_gemv(fmt, planes, scales, rows, cols, g, x,
+                              L.ROTATE_FWHT256 if fmt in (1, 2, 3, 4) else L.ROTATE_NONE) + bias
+    assert rel_max_err(yb, refb) < TOL
+
+
 # ---- batched GEMV (weights read once per group of 2/4/8/16 vectors) ----------
 @pytest.mark.parametrize("fmt", [1, 2, 3, 4, 5, 6, 7])
 @pytest.mark.parametrize("batch", [4, 7, 8, 16, 21])
