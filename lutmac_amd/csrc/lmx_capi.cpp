@@ -264,6 +264,9 @@ GemvArgs weight_args(const lmx_weight *w) {
   a.cols = int(w->cols);
   a.Kp = int(w->Kp);
   a.group_chunks = int(w->group / kChunk);
+  a.gshift = -1;
+  for (int sh = 0; sh < 31; ++sh)
+    if ((1 << sh) == a.group_chunks) a.gshift = sh;
   a.n_groups = int(w->n_groups);
   a.kslice = w->kslice;
   a.reduce = w->reduce;

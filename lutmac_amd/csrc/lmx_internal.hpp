@@ -52,6 +52,7 @@ struct GemvArgs {
   unsigned *counters;      // [row_blocks]
   int rows, Npad, cols, Kp;
   int group_chunks;        // chunks per scale group
+  int gshift;              // log2(group_chunks) when it is a power of two, else -1
   int n_groups;
   int kslice;              // k per workgroup (multiple of 256, divides Kp)
   unsigned rotate;         // LMX_ROTATE_NONE / LMX_ROTATE_FWHT256

@@ -728,6 +728,196 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_fullk_kernel(GemvArgs 
   if (a.amax && threadIdx.x < kWave) wave_argmax(a.amax, blockIdx.x, t, r, threadIdx.x < RW && r < a.rows);
 }
 
+// FWHT-256 of the lane's 4 values without the final 1/16: every output is
+// exactly 16x the reference's (the butterflies are the same exact sums and
+// differences, and a power-of-two scale commutes with rounding), so the
+// caller folds 1/16 into the group scale.  Cross-lane butterflies are
+// fma(sgn, own, partner) with sgn = +1 in the lower lane of a pair (own +
+// partner) and -1 in the upper lane (partner - own): the same roundings as
+// the reference's a + b and a - b.
+__device__ __forceinline__ void fwht256_regs_x16(float &x0, float &x1, float &x2, float &x3, int lane) {
+  float a0 = x0 + x1, a1 = x0 - x1, a2 = x2 + x3, a3 = x2 - x3;   // h = 1
+  x0 = a0 + a2; x2 = a0 - a2; x1 = a1 + a3; x3 = a1 - a3;          // h = 2
+#define LMX_XSTAGE(D)                                                           \
+  {                                                                             \
+    const float sg = (lane & (D)) ? -1.0f : 1.0f;                               \
+    const float p0 = lane_xor<D>(x0, lane), p1 = lane_xor<D>(x1, lane);         \
+    const float p2 = lane_xor<D>(x2, lane), p3 = lane_xor<D>(x3, lane);         \
+    x0 = fmaf(sg, x0, p0); x1 = fmaf(sg, x1, p1);                               \
+    x2 = fmaf(sg, x2, p2); x3 = fmaf(sg, x3, p3);                               \
+  }
+  LMX_XSTAGE(1) LMX_XSTAGE(2) LMX_XSTAGE(4) LMX_XSTAGE(8)
+#undef LMX_XSTAGE
+#define LMX_PSTAGE(D)                                                           \
+  {                                                                             \
+    const float sg = (lane & (D)) ? -1.0f : 1.0f;                               \
+    float l0, h0, l1, h1, l2, h2, l3, h3;                                       \
+    lane_pair<D>(x0, l0, h0); lane_pair<D>(x1, l1, h1);                         \
+    lane_pair<D>(x2, l2, h2); lane_pair<D>(x3, l3, h3);                         \
+    x0 = fmaf(sg, h0, l0); x1 = fmaf(sg, h1, l1);                               \
+    x2 = fmaf(sg, h2, l2); x3 = fmaf(sg, h3, l3);                               \
+  }
+  LMX_PSTAGE(16) LMX_PSTAGE(32)
+#undef LMX_PSTAGE
+}
+
+// Full-K kernel for plain activations (no fused transform, no argmax): the
+// same geometry, LDS layout, lookups and slice reduction as
+// lut_gemv_fullk_kernel, with a lean front end.  Weight and scale
+// addresses use 32-bit offsets and a shift for the scale group; x is
+// rotated (ROT) without its final 1/16, which is folded into the scales;
+// every wave builds the tables of its own 256-chunks only.  Needs H*CPS
+// even (each wave owns whole 256-chunks).
+template <int FMT, bool ROT, int WAVES, int H, int CPS>
+__global__ __launch_bounds__(WAVES * kWave) void lut_gemv_plain_kernel(GemvArgs a) {
+  constexpr int P = Fmt<FMT>::P, NA = Fmt<FMT>::NA, S = Fmt<FMT>::S;
+  constexpr int RW = kWave / H;
+  constexpr int NS = WAVES * H;
+  constexpr uint32_t SSTRIDE = CPS * 32 * 64 + 256;
+  constexpr int XJ = H * CPS / 2;
+  static_assert(H * CPS % 2 == 0, "whole 256-chunks per wave");
+  constexpr uint32_t PREFIX = fullk_prefix_bytes<WAVES, H, CPS>();
+  extern __shared__ __attribute__((aligned(256))) float lds[];
+  const int Kc = a.Kp / kChunk;
+  const int used = (Kc + CPS - 1) / CPS;
+  float *xsum = lds;
+  float *red = lds + NS * CPS;
+  char *tables = reinterpret_cast<char *>(lds) + PREFIX;
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int s = wave * H + lane / RW;
+  const int rl = lane % RW;
+  const int row = blockIdx.x * RW + rl;
+  const int lr = min(row, a.Npad - 1);
+
+  // ---- x of this wave's 256-chunks (clamped in bounds, masked below) ----
+  const int C2n = a.Kp / kRotChunk;
+  const int c2base = wave * XJ;
+  float4 xr[XJ];
+#pragma unroll
+  for (int j = 0; j < XJ; ++j) xr[j] = load_x4_raw(a.x, min(c2base + j, C2n - 1) * kRotChunk, a.cols, lane);
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_barrier();   // every wave's x requests ahead of the weight stream
+
+  // ---- weights (chunk 0 now, the rest after the prologue) and scales ----
+  u32x4 w[CPS][P];
+  float sc[CPS][S];
+  const u32x4 *__restrict__ pl = reinterpret_cast<const u32x4 *>(a.planes);
+  const uint32_t Npad = uint32_t(a.Npad);
+  auto load_planes = [&](int c) {
+    const uint32_t ch = uint32_t(min(s * CPS + c, Kc - 1));
+#pragma unroll
+    for (int p = 0; p < P; ++p) w[c][p] = __builtin_nontemporal_load(pl + ((ch * P + p) * Npad + uint32_t(lr)));
+  };
+  load_planes(0);
+#pragma unroll
+  for (int c = 0; c < CPS; ++c) {
+    const int ch = min(s * CPS + c, Kc - 1);
+    const int g = a.gshift >= 0 ? ch >> a.gshift : ch / a.group_chunks;
+#pragma unroll
+    for (int t = 0; t < S; ++t) sc[c][t] = a.scales[(uint32_t(t * a.n_groups + g)) * Npad + uint32_t(lr)];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- prologue: (FWHT-256 x16) -> group tables of this wave's chunks ----
+#pragma unroll
+  for (int j = 0; j < XJ; ++j) {
+    const int c2 = c2base + j;
+    if (c2 >= C2n) break;   // wave-uniform
+    float x0, x1, x2, x3;
+    mask_x4(xr[j], c2 * kRotChunk, a.cols, lane, x0, x1, x2, x3);
+    if constexpr (ROT) fwht256_regs_x16(x0, x1, x2, x3, lane);
+    float t[16];
+    group_table(x0, x1, x2, x3, t);
+    const int ch = c2 * 2 + (lane >> 5);
+    const int ts = ch / CPS;
+    float4 *dst = reinterpret_cast<float4 *>(tables + ts * SSTRIDE + slice_shift<H>(ts) + (ch % CPS) * 2048 +
+                                             (lane & 31) * 64);
+    dst[0] = make_float4(t[0], t[1], t[2], t[3]);
+    dst[1] = make_float4(t[4], t[5], t[6], t[7]);
+    dst[2] = make_float4(t[8], t[9], t[10], t[11]);
+    dst[3] = make_float4(t[12], t[13], t[14], t[15]);
+    if constexpr (Fmt<FMT>::XS) {
+      float xs = t[15];
+      xs = lane_sum<16>(xs, lane);
+      if ((lane & 31) == 0) xsum[ch] = xs;
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int c = 1; c < CPS; ++c) load_planes(c);
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+
+  // ---- lookups over this lane's k-slice ----------------------------------
+  constexpr float kScale = ROT ? 0.0625f : 1.0f;   // the FWHT's 1/16, exact
+  float acc = 0.0f;
+  {
+    const uint32_t tbase = lds_addr(lds) + PREFIX + min(s, used - 1) * SSTRIDE;
+    const uint32_t shift = slice_shift<H>(s) * 0x01010101u;
+#pragma unroll
+    for (int c = 0; c < CPS; ++c) {
+      float A[NA];
+#pragma unroll
+      for (int i = 0; i < NA; ++i) A[i] = 0.0f;
+      chunk_lookups<FMT>(w[c], tbase + c * 2048, shift, A);
+      const int ch = s * CPS + c;
+      float xs = 0.0f;
+      if constexpr (Fmt<FMT>::XS) xs = xsum[min(ch, Kc - 1)];
+      float scl[S];
+#pragma unroll
+      for (int t = 0; t < S; ++t) scl[t] = sc[c][t] * kScale;
+      const float nacc = finish_chunk<FMT>(A, xs, scl, acc);
+      acc = ch < Kc ? nacc : acc;
+    }
+  }
+
+  // ---- in-workgroup reduction over the k-slices, fixed order --------------
+  red[s * RW + rl] = acc;
+  __syncthreads();
+  if (threadIdx.x < RW) {
+    const int r = blockIdx.x * RW + threadIdx.x;
+    float t = 0.0f;
+#pragma unroll 8
+    for (int k = 0; k < NS; ++k) t += red[k * RW + threadIdx.x];
+    if (r < a.rows) a.y[r] = a.bias ? t + a.bias[r] : t;
+  }
+}
+
+template <int FMT, bool ROT, int WAVES, int H, int CPS>
+static int launch_plain_kernel(const GemvArgs &a, hipStream_t st) {
+  const size_t lds = fullk_lds_bytes(WAVES, H, CPS, a.Kp / kChunk);
+  static const hipError_t attr = hipFuncSetAttribute(
+      reinterpret_cast<const void *>(&lut_gemv_plain_kernel<FMT, ROT, WAVES, H, CPS>),
+      hipFuncAttributeMaxDynamicSharedMemorySize, int(kMaxLdsBytes));
+  if (attr != hipSuccess) return fail(LMX_ERR_LAUNCH_FAILED, "hipFuncSetAttribute: %s", hipGetErrorString(attr));
+  if (lds > kMaxLdsBytes) return fail(LMX_ERR_INVALID_ARGUMENT, "full-K tables need %zu B of LDS", lds);
+  constexpr int RW = kWave / H;
+  lut_gemv_plain_kernel<FMT, ROT, WAVES, H, CPS><<<dim3((a.Npad + RW - 1) / RW), dim3(WAVES * kWave), lds, st>>>(a);
+  return LMX_OK;
+}
+
+template <int FMT, int WAVES, int H, int CPS>
+static int launch_plain_cfg(const GemvArgs &a, hipStream_t st) {
+  if (a.rotate == LMX_ROTATE_FWHT256) return launch_plain_kernel<FMT, true, WAVES, H, CPS>(a, st);
+  return launch_plain_kernel<FMT, false, WAVES, H, CPS>(a, st);
+}
+
+// The plain kernel serves full-K launches without a fused transform or an
+// argmax epilogue; returns 1 when the configuration is not covered.
+template <int FMT>
+static int launch_plain(const GemvArgs &a, hipStream_t st) {
+  switch (a.fullk) {
+  case kFullK_16x2x2: return launch_plain_cfg<FMT, 16, 2, 2>(a, st);
+  case kFullK_16x2x3: return launch_plain_cfg<FMT, 16, 2, 3>(a, st);
+  case kFullK_8x2x1: return launch_plain_cfg<FMT, 8, 2, 1>(a, st);
+  case kFullK_16x4x1: return launch_plain_cfg<FMT, 16, 4, 1>(a, st);
+  case kFullK_4x4x1: return launch_plain_cfg<FMT, 4, 4, 1>(a, st);
+  }
+  return 1;
+}
+
 template <int FMT, int WAVES, int H, int CPS, bool STAGED>
 static int launch_fullk_kernel(const GemvArgs &a, hipStream_t st) {
   const size_t lds = fullk_lds_bytes(WAVES, H, CPS, a.Kp / kChunk);
@@ -776,7 +966,11 @@ static int launch_fullk(const GemvArgs &a, hipStream_t st) {
 template <int FMT>
 static int launch_fmt(const GemvArgs &a, hipStream_t st) {
   if (a.fullk) {
-    int r = launch_fullk<FMT>(a, st);
+    int r = 1;
+#ifndef LMX_NO_PLAIN
+    if (a.xmode == kXModeNone && !a.amax) r = launch_plain<FMT>(a, st);
+#endif
+    if (r == 1) r = launch_fullk<FMT>(a, st);
     if (r) return r;
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(LMX_ERR_LAUNCH_FAILED, "lut_gemv_fullk launch: %s", hipGetErrorString(e));
