@@ -3,7 +3,11 @@
 
 A step is one GEMV y = W x over an 8192x8192 weight with batch 1.  The
 headline workload is the 4-bit format with per-128-group scales (BASELINE
-config 3); the other formats of the sweep are reported beside it.  Weights
+config 3) on FWHT-rotated activations, run like the reference's int4 operator
+(which never rotates inside the op: the input is rotated once, untimed); the
+other formats of the sweep are reported beside it, ternary and the 1-2 bit
+formats with the FWHT fused into the kernel as lut_linear applies it, and
+int4 with the rotation fused in as "int4_rot".  Weights
 rotate over >= 512 MiB of distinct device copies so neither the 256 MB MALL
 nor the L2 holds them between launches.  The timed region is bracketed by
 torch.cuda.synchronize() and HIP events recorded on the stream the kernels
@@ -32,19 +36,35 @@ METRIC = "LUT-GEMV HBM GB/s (% of peak) at 8192x8192; 1B-arch decode tokens/s bs
 HBM_PEAK_GBPS = 8000.0
 ROTATE_BYTES = 512 * 2**20
 
-FORMATS = {"int4": 6, "ternary": 1, "binary": 2, "rrq2": 3, "rrq3": 4, "int8": 7}
+FORMATS = {"int4": 6, "ternary": 1, "binary": 2, "rrq2": 3, "rrq3": 4, "int8": 7, "int4_rot": 6}
+# Config 3's activations are FWHT-rotated.  Where the reference's operator
+# rotates inside lut_linear (ternary and the 1-2 bit formats,
+# lut_gemm_scalar.cpp:92-93) the kernel rotates them (fused into its table
+# build, inside the timed region).  The 4- and 8-bit paths never rotate inside
+# the operator, so their input is rotated once on the device before timing
+# (lmx_fwht256) and the kernel runs unrotated, as the reference's int4_gemv /
+# int8_gemv do; "int4_rot" times int4 with the rotation fused in anyway.
+ROTATE_IN_KERNEL = {"ternary", "binary", "rrq2", "rrq3", "int4_rot"}
 
 
-def gemv_bench(L, synth, torch, fmt, n, steps, warmup, graph=True):
-    """Time `steps` GEMVs of an n x n weight of format fmt; returns a dict."""
+def gemv_bench(L, synth, torch, fmt, n, steps, warmup, graph=True, rotate_in_kernel=True):
+    """Time `steps` GEMVs of an n x n weight of format fmt; returns a dict.
+    rotate_in_kernel: FWHT-256 of x fused into the kernel (flags), else x is
+    rotated once on the device before the timed region and the kernel runs
+    without rotation."""
     group = 0 if fmt == L.FMT_TERNARY else 128
     planes, scales, g = synth.make_weights(fmt, n, n, seed=1000 + fmt, group=group)
     B = synth.algorithmic_bytes(fmt, n, n, group=g)
     copies = max(2, -(-ROTATE_BYTES // B))
     ws = [L.Weight.from_planes(fmt, planes, scales, n, n, g) for _ in range(copies)]
     del planes
-    flags = L.ROTATE_FWHT256   # config 3 rotates every format's activations (fused in the kernel)
     x = torch.from_numpy(synth.make_activations(n, seed=5)).cuda()
+    if rotate_in_kernel:
+        flags = L.ROTATE_FWHT256
+    else:
+        flags = L.ROTATE_NONE
+        L.fwht256(x)                # the input is FWHT-rotated data; rotated once, untimed
+        torch.cuda.synchronize()
     y = torch.empty(n, dtype=torch.float32, device="cuda")
     stream = torch.cuda.current_stream()
     for i in range(warmup):
@@ -79,7 +99,8 @@ def gemv_bench(L, synth, torch, fmt, n, steps, warmup, graph=True):
         del cg
     ms = ms_graph if ms_graph is not None else ms_stream
     gbps = B / (ms * 1e-3) / 1e9
-    out = {"format": L.FORMAT_NAMES[fmt], "rows": n, "cols": n, "group": g, "rotation": flags,
+    out = {"format": L.FORMAT_NAMES[fmt], "rows": n, "cols": n, "group": g,
+           "rotation": "FWHT-256 in the kernel" if rotate_in_kernel else "input pre-rotated (FWHT-256), kernel unrotated",
            "kernel_plan": dict(zip(("fullk", "kslice", "staged"), ws[0].kernel_config())),
            "algorithmic_bytes": B, "us_per_gemv": round(ms * 1e3, 3), "GB_per_s": round(gbps, 1),
            "launch": "hip_graph" if ms_graph is not None else "stream",
@@ -281,7 +302,7 @@ def main():
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--size", type=int, default=8192)
-    ap.add_argument("--formats", default="int4,ternary,binary,rrq2,rrq3,int8")
+    ap.add_argument("--formats", default="int4,ternary,binary,rrq2,rrq3,int8,int4_rot")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true", help="skip the 1B-architecture decode")
@@ -311,7 +332,7 @@ def main():
     sweep = {}
     for name in names:
         r = gemv_bench(L, synth, torch, FORMATS[name], args.size, args.steps, args.warmup,
-                       graph=not args.no_graph)
+                       graph=not args.no_graph, rotate_in_kernel=name in ROTATE_IN_KERNEL)
         sweep[name] = r
         print(f"# {name}: {r['us_per_gemv']} us/GEMV, {r['GB_per_s']} GB/s "
               f"({100 * r['frac_of_peak']:.1f}% of peak)", file=sys.stderr, flush=True)
@@ -343,7 +364,7 @@ def main():
         "dtype": "f32",
         "data": "synthetic (seeded uniform codes, |N(0,1)|*0.02 group scales, N(0,1) activations)",
         "config": {"workload": f"LUT-GEMV {head['format']} {args.size}x{args.size} batch 1, "
-                               f"group {head['group']} (BASELINE config 3)",
+                               f"group {head['group']}, {head['rotation']} (BASELINE config 3)",
                    "rows": args.size, "cols": args.size, "format": head["format"],
                    "group": head["group"], "batch": 1, "weight_copies": head["weight_copies"],
                    "rotated_MiB": head["rotated_MiB"]},

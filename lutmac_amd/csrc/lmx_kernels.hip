@@ -101,13 +101,34 @@ __device__ __forceinline__ float finish_chunk(const float *A, float xs, const fl
 // is the ds_read immediate.  All 64 lanes read the same 16-entry table at a
 // time: 16 consecutive dwords, no bank conflicts.  word_reads issues the
 // reads, word_sum adds them as a balanced tree.
-__device__ __forceinline__ void word_reads(uint32_t v, int i, uint32_t cbase, uint32_t shift, float *t) {
+// Byte offset of group g's table inside a chunk's table block.  Packed:
+// 64*g.  Staggered (STAG): each table starts 16 B later than its
+// predecessor's slot within a run of 4 (4 runs per 16 groups), and each
+// block of 16 groups is padded by 64 B, so the 64 lanes of one table-write
+// instruction (lane = group) start in 16 different 4-bank groups: the
+// prologue's 16-byte writes are bank-conflict free, and every table is
+// still 16 contiguous dwords for the lookups.
+template <bool STAG>
+__host__ __device__ constexpr uint32_t group_offset(int g) {
+  return STAG ? uint32_t(64 * g + 16 * ((g >> 2) & 3) + 64 * (g >> 4)) : uint32_t(64 * g);
+}
+constexpr uint32_t kStagChunkBytes = 2176;   // group_offset<true>(31) + 64, 16-byte multiple
+// One k-slice of CPS staggered chunk blocks plus 256 B (room for the H = 4
+// slice shift), rounded to 256 B so every slice base is 256-byte aligned.
+__host__ __device__ constexpr uint32_t stag_slice_bytes(int cps) { return (cps * kStagChunkBytes + 511) / 256 * 256; }
+
+// cbase must be 256-byte aligned (v_perm keeps its bytes 1-2 only); coff is
+// a compile-time chunk offset folded into the ds_read immediate.
+template <bool STAG = false>
+__device__ __forceinline__ void word_reads(uint32_t v, int i, uint32_t cbase, uint32_t shift, float *t,
+                                           uint32_t coff = 0) {
   const uint32_t hi = ((v >> 2) & 0x3C3C3C3Cu) | shift;  // byte b: 4*nibble of group 8i+2b
   const uint32_t lo = ((v << 2) & 0x3C3C3C3Cu) | shift;  // byte b: 4*nibble of group 8i+2b+1
 #pragma unroll
   for (int b = 0; b < 4; ++b) {
-    t[2 * b] = lds_load(__builtin_amdgcn_perm(cbase, hi, 0x0C060500u | b) + (8 * i + 2 * b) * 64);
-    t[2 * b + 1] = lds_load(__builtin_amdgcn_perm(cbase, lo, 0x0C060500u | b) + (8 * i + 2 * b + 1) * 64);
+    t[2 * b] = lds_load(__builtin_amdgcn_perm(cbase, hi, 0x0C060500u | b) + (coff + group_offset<STAG>(8 * i + 2 * b)));
+    t[2 * b + 1] =
+        lds_load(__builtin_amdgcn_perm(cbase, lo, 0x0C060500u | b) + (coff + group_offset<STAG>(8 * i + 2 * b + 1)));
   }
 }
 
@@ -115,16 +136,18 @@ __device__ __forceinline__ float word_sum(const float *t) {
   return ((t[0] + t[1]) + (t[2] + t[3])) + ((t[4] + t[5]) + (t[6] + t[7]));
 }
 
-__device__ __forceinline__ float word_lookups(uint32_t v, int i, uint32_t cbase, uint32_t shift) {
+template <bool STAG = false>
+__device__ __forceinline__ float word_lookups(uint32_t v, int i, uint32_t cbase, uint32_t shift, uint32_t coff = 0) {
   float t[8];
-  word_reads(v, i, cbase, shift, t);
+  word_reads<STAG>(v, i, cbase, shift, t, coff);
   return word_sum(t);
 }
 
 // Table lookups of one 128-k chunk for one lane: NA accumulators over the
 // 32 groups of the chunk.
-template <int FMT>
-__device__ __forceinline__ void chunk_lookups(const u32x4 *wc, uint32_t cbase, uint32_t shift, float *A) {
+template <int FMT, bool STAG = false>
+__device__ __forceinline__ void chunk_lookups(const u32x4 *wc, uint32_t cbase, uint32_t shift, float *A,
+                                              uint32_t coff = 0) {
   constexpr int P = Fmt<FMT>::P, NA = Fmt<FMT>::NA;
   if constexpr (FMT != LMX_FMT_TERNARY) {
     // Accumulator q reads plane q only.  Software pipeline over the NA*4
@@ -139,10 +162,10 @@ __device__ __forceinline__ void chunk_lookups(const u32x4 *wc, uint32_t cbase, u
       lookup_words<FMT>(wi, v);
       return v[n >> 2];
     };
-    word_reads(word_of(0), 0, cbase, shift, t[0]);
+    word_reads<STAG>(word_of(0), 0, cbase, shift, t[0], coff);
 #pragma unroll
     for (int n = 0; n < NA * 4; ++n) {
-      if (n + 1 < NA * 4) word_reads(word_of(n + 1), (n + 1) & 3, cbase, shift, t[(n + 1) & 1]);
+      if (n + 1 < NA * 4) word_reads<STAG>(word_of(n + 1), (n + 1) & 3, cbase, shift, t[(n + 1) & 1], coff);
       A[n >> 2] += word_sum(t[n & 1]);
     }
     return;
@@ -156,7 +179,7 @@ __device__ __forceinline__ void chunk_lookups(const u32x4 *wc, uint32_t cbase, u
       for (int p = 0; p < P; ++p) wi[p] = wc[p][i];
       lookup_words<FMT>(wi, v);
 #pragma unroll
-      for (int q = 0; q < NA; ++q) A[q] += word_lookups(v[q], i, cbase, shift);
+      for (int q = 0; q < NA; ++q) A[q] += word_lookups<STAG>(v[q], i, cbase, shift, coff);
     }
   }
 }
@@ -728,6 +751,28 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_fullk_kernel(GemvArgs 
   if (a.amax && threadIdx.x < kWave) wave_argmax(a.amax, blockIdx.x, t, r, threadIdx.x < RW && r < a.rows);
 }
 
+// One FWHT butterfly stage at lane distance D = 16 or 32 for two values a, b
+// held by every lane: new a = (a_lo + a_hi, a_lo - a_hi) in the (lower, upper)
+// lane of each pair (l, l ^ D), the same for b.  Two permlane swaps, one add
+// and one subtract for the two values.
+template <int D>
+__device__ __forceinline__ void lane_pair_stage(float &a, float &b) {
+  static_assert(D == 16 || D == 32, "permlane swap distance");
+  uint32_t ua = __float_as_uint(a), ub = __float_as_uint(b);
+  {
+    const auto r = D == 16 ? __builtin_amdgcn_permlane16_swap(ua, ub, false, false)
+                           : __builtin_amdgcn_permlane32_swap(ua, ub, false, false);
+    ua = r[0];
+    ub = r[1];
+  }
+  const float lo = __uint_as_float(ua), hi = __uint_as_float(ub);
+  const uint32_t sum = __float_as_uint(lo + hi), dif = __float_as_uint(lo - hi);
+  const auto r = D == 16 ? __builtin_amdgcn_permlane16_swap(sum, dif, false, false)
+                         : __builtin_amdgcn_permlane32_swap(sum, dif, false, false);
+  a = __uint_as_float(r[0]);
+  b = __uint_as_float(r[1]);
+}
+
 // FWHT-256 of the lane's 4 values without the final 1/16: every output is
 // exactly 16x the reference's (the butterflies are the same exact sums and
 // differences, and a power-of-two scale commutes with rounding), so the
@@ -748,17 +793,14 @@ __device__ __forceinline__ void fwht256_regs_x16(float &x0, float &x1, float &x2
   }
   LMX_XSTAGE(1) LMX_XSTAGE(2) LMX_XSTAGE(4) LMX_XSTAGE(8)
 #undef LMX_XSTAGE
-#define LMX_PSTAGE(D)                                                           \
-  {                                                                             \
-    const float sg = (lane & (D)) ? -1.0f : 1.0f;                               \
-    float l0, h0, l1, h1, l2, h2, l3, h3;                                       \
-    lane_pair<D>(x0, l0, h0); lane_pair<D>(x1, l1, h1);                         \
-    lane_pair<D>(x2, l2, h2); lane_pair<D>(x3, l3, h3);                         \
-    x0 = fmaf(sg, h0, l0); x1 = fmaf(sg, h1, l1);                               \
-    x2 = fmaf(sg, h2, l2); x3 = fmaf(sg, h3, l3);                               \
-  }
-  LMX_PSTAGE(16) LMX_PSTAGE(32)
-#undef LMX_PSTAGE
+  // Lane distance 16 / 32 on two values per swap pair: after swap(a, b) the
+  // lower half of every pair of lane groups holds (a_lo, a_hi) and the upper
+  // half (b_lo, b_hi); their sum and difference, swapped back, are the new a
+  // (lo + hi, lo - hi) and the new b.
+  lane_pair_stage<16>(x0, x1);
+  lane_pair_stage<16>(x2, x3);
+  lane_pair_stage<32>(x0, x1);
+  lane_pair_stage<32>(x2, x3);
 }
 
 // Full-K kernel for plain activations (no fused transform, no argmax): the
@@ -773,7 +815,7 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_plain_kernel(GemvArgs 
   constexpr int P = Fmt<FMT>::P, NA = Fmt<FMT>::NA, S = Fmt<FMT>::S;
   constexpr int RW = kWave / H;
   constexpr int NS = WAVES * H;
-  constexpr uint32_t SSTRIDE = CPS * 32 * 64 + 256;
+  constexpr uint32_t SSTRIDE = stag_slice_bytes(CPS);
   constexpr int XJ = H * CPS / 2;
   static_assert(H * CPS % 2 == 0, "whole 256-chunks per wave");
   constexpr uint32_t PREFIX = fullk_prefix_bytes<WAVES, H, CPS>();
@@ -821,6 +863,7 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_plain_kernel(GemvArgs 
   __builtin_amdgcn_sched_barrier(0);
 
   // ---- prologue: (FWHT-256 x16) -> group tables of this wave's chunks ----
+  const uint32_t goff = group_offset<true>(lane & 31);
 #pragma unroll
   for (int j = 0; j < XJ; ++j) {
     const int c2 = c2base + j;
@@ -832,8 +875,8 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_plain_kernel(GemvArgs 
     group_table(x0, x1, x2, x3, t);
     const int ch = c2 * 2 + (lane >> 5);
     const int ts = ch / CPS;
-    float4 *dst = reinterpret_cast<float4 *>(tables + ts * SSTRIDE + slice_shift<H>(ts) + (ch % CPS) * 2048 +
-                                             (lane & 31) * 64);
+    float4 *dst = reinterpret_cast<float4 *>(tables + ts * SSTRIDE + slice_shift<H>(ts) +
+                                             (ch % CPS) * kStagChunkBytes + goff);
     dst[0] = make_float4(t[0], t[1], t[2], t[3]);
     dst[1] = make_float4(t[4], t[5], t[6], t[7]);
     dst[2] = make_float4(t[8], t[9], t[10], t[11]);
@@ -861,7 +904,7 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_plain_kernel(GemvArgs 
       float A[NA];
 #pragma unroll
       for (int i = 0; i < NA; ++i) A[i] = 0.0f;
-      chunk_lookups<FMT>(w[c], tbase + c * 2048, shift, A);
+      chunk_lookups<FMT, true>(w[c], tbase, shift, A, c * kStagChunkBytes);
       const int ch = s * CPS + c;
       float xs = 0.0f;
       if constexpr (Fmt<FMT>::XS) xs = xsum[min(ch, Kc - 1)];
@@ -885,9 +928,135 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_plain_kernel(GemvArgs 
   }
 }
 
+// Interleaved variant of the plain kernel (two k-slices per wave, H = 2):
+// wave w owns the 256-chunks c2 = w*CPS + c, c < CPS, and at step c its
+// lower / upper half-wave looks up 128-chunk 2*c2 / 2*c2 + 1, exactly the two
+// halves of the 256-chunk it has just rotated.  So every step is "build the
+// tables of one 256-chunk, then look them up", and the VALU-heavy table
+// build of one wave overlaps the LDS-heavy lookups of the others.  Chunk ch
+// keeps its (staggered) tables at ch * kIplChunkBytes, a 256-byte multiple.
+constexpr uint32_t kIplChunkBytes = 2304;
+
+template <int WAVES, int CPS>
+constexpr uint32_t ipl_prefix_bytes() {
+  return (uint32_t(2 * WAVES * CPS + 2 * WAVES * (kWave / 2)) * 4 + 255) / 256 * 256;
+}
+
+template <int FMT, bool ROT, int WAVES, int CPS>
+__global__ __launch_bounds__(WAVES * kWave) void lut_gemv_ipl_kernel(GemvArgs a) {
+  constexpr int P = Fmt<FMT>::P, NA = Fmt<FMT>::NA, S = Fmt<FMT>::S;
+  constexpr int RW = kWave / 2;
+  constexpr int NS = WAVES * 2;
+  constexpr uint32_t PREFIX = ipl_prefix_bytes<WAVES, CPS>();
+  extern __shared__ __attribute__((aligned(256))) float lds[];
+  const int Kc = a.Kp / kChunk;
+  float *xsum = lds;                 // [2*WAVES*CPS]
+  float *red = lds + 2 * WAVES * CPS;   // [NS][RW]
+  char *tables = reinterpret_cast<char *>(lds) + PREFIX;
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int h = lane >> 5;
+  const int rl = lane & (RW - 1);
+  const int row = blockIdx.x * RW + rl;
+  const int lr = min(row, a.Npad - 1);
+
+  const int C2n = a.Kp / kRotChunk;
+  const int c2base = wave * CPS;
+  float4 xr[CPS];
+#pragma unroll
+  for (int c = 0; c < CPS; ++c) xr[c] = load_x4_raw(a.x, min(c2base + c, C2n - 1) * kRotChunk, a.cols, lane);
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_barrier();   // every wave's x requests ahead of the weight stream
+
+  u32x4 w[CPS][P];
+  float sc[CPS][S];
+  const u32x4 *__restrict__ pl = reinterpret_cast<const u32x4 *>(a.planes);
+  const uint32_t Npad = uint32_t(a.Npad);
+  auto chunk_of = [&](int c) { return min(2 * (c2base + c) + h, Kc - 1); };   // clamped; masked below
+  auto load_planes = [&](int c) {
+    const uint32_t ch = uint32_t(chunk_of(c));
+#pragma unroll
+    for (int p = 0; p < P; ++p) w[c][p] = __builtin_nontemporal_load(pl + ((ch * P + p) * Npad + uint32_t(lr)));
+  };
+  load_planes(0);
+#pragma unroll
+  for (int c = 0; c < CPS; ++c) {
+    const int ch = chunk_of(c);
+    const int g = a.gshift >= 0 ? ch >> a.gshift : ch / a.group_chunks;
+#pragma unroll
+    for (int t = 0; t < S; ++t) sc[c][t] = a.scales[(uint32_t(t * a.n_groups + g)) * Npad + uint32_t(lr)];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  constexpr float kScale = ROT ? 0.0625f : 1.0f;   // the FWHT's 1/16, exact
+  const uint32_t goff = group_offset<true>(lane & 31);
+  const uint32_t tb = lds_addr(lds) + PREFIX;
+  float acc = 0.0f;
+#pragma unroll
+  for (int c = 0; c < CPS; ++c) {
+    const int c2 = c2base + c;
+    if (c2 >= C2n) break;   // wave-uniform: no chunk of this step holds data
+    // ---- tables of 256-chunk c2 (128-chunks 2*c2 and 2*c2 + 1) ----
+    {
+      float x0 = xr[c].x, x1 = xr[c].y, x2 = xr[c].z, x3 = xr[c].w;
+      if (c2 * kRotChunk + kRotChunk > a.cols)   // wave-uniform: only the chunk holding the end of x
+        mask_x4(xr[c], c2 * kRotChunk, a.cols, lane, x0, x1, x2, x3);
+      if constexpr (ROT) fwht256_regs_x16(x0, x1, x2, x3, lane);
+      float t[16];
+      group_table(x0, x1, x2, x3, t);
+      float4 *dst = reinterpret_cast<float4 *>(tables + (2 * c2 + h) * kIplChunkBytes + goff);
+      dst[0] = make_float4(t[0], t[1], t[2], t[3]);
+      dst[1] = make_float4(t[4], t[5], t[6], t[7]);
+      dst[2] = make_float4(t[8], t[9], t[10], t[11]);
+      dst[3] = make_float4(t[12], t[13], t[14], t[15]);
+      if constexpr (Fmt<FMT>::XS) {
+        float xs = t[15];
+        xs = lane_sum<16>(xs, lane);
+        if ((lane & 31) == 0) xsum[2 * c2 + h] = xs;
+      }
+    }
+    if (c == 0) {
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int cc = 1; cc < CPS; ++cc) load_planes(cc);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // A wave reads only the tables it wrote; its LDS operations complete in order.
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    // ---- lookups of 128-chunk 2*c2 + h ----
+    const int ch = 2 * c2 + h;
+    float A[NA];
+#pragma unroll
+    for (int i = 0; i < NA; ++i) A[i] = 0.0f;
+    chunk_lookups<FMT, true>(w[c], tb + uint32_t(ch) * kIplChunkBytes, 0u, A);
+    float xs = 0.0f;
+    if constexpr (Fmt<FMT>::XS) xs = xsum[min(ch, Kc - 1)];
+    float scl[S];
+#pragma unroll
+    for (int t = 0; t < S; ++t) scl[t] = sc[c][t] * kScale;
+    const float nacc = finish_chunk<FMT>(A, xs, scl, acc);
+    acc = ch < Kc ? nacc : acc;
+  }
+
+  // ---- in-workgroup reduction over the 2*WAVES slices, fixed order ----
+  red[(wave * 2 + h) * RW + rl] = acc;
+  __syncthreads();
+  if (threadIdx.x < RW) {
+    const int r = blockIdx.x * RW + threadIdx.x;
+    float t = 0.0f;
+#pragma unroll 8
+    for (int k = 0; k < NS; ++k) t += red[k * RW + threadIdx.x];
+    if (r < a.rows) a.y[r] = a.bias ? t + a.bias[r] : t;
+  }
+}
+
 template <int FMT, bool ROT, int WAVES, int H, int CPS>
 static int launch_plain_kernel(const GemvArgs &a, hipStream_t st) {
-  const size_t lds = fullk_lds_bytes(WAVES, H, CPS, a.Kp / kChunk);
+  const size_t Kc = size_t(a.Kp / kChunk);
+  const size_t lds = fullk_prefix_bytes<WAVES, H, CPS>() + (Kc + CPS - 1) / CPS * stag_slice_bytes(CPS);
+  if (lds > kMaxLdsBytes) return 1;   // staggered tables do not fit: the generic kernel serves it
   static const hipError_t attr = hipFuncSetAttribute(
       reinterpret_cast<const void *>(&lut_gemv_plain_kernel<FMT, ROT, WAVES, H, CPS>),
       hipFuncAttributeMaxDynamicSharedMemorySize, int(kMaxLdsBytes));
@@ -898,8 +1067,27 @@ static int launch_plain_kernel(const GemvArgs &a, hipStream_t st) {
   return LMX_OK;
 }
 
+template <int FMT, bool ROT, int WAVES, int CPS>
+static int launch_ipl_kernel(const GemvArgs &a, hipStream_t st) {
+  const size_t lds = ipl_prefix_bytes<WAVES, CPS>() + size_t(a.Kp / kRotChunk) * 2 * kIplChunkBytes;
+  if (lds > kMaxLdsBytes) return 1;
+  static const hipError_t attr =
+      hipFuncSetAttribute(reinterpret_cast<const void *>(&lut_gemv_ipl_kernel<FMT, ROT, WAVES, CPS>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, int(kMaxLdsBytes));
+  if (attr != hipSuccess) return fail(LMX_ERR_LAUNCH_FAILED, "hipFuncSetAttribute: %s", hipGetErrorString(attr));
+  lut_gemv_ipl_kernel<FMT, ROT, WAVES, CPS><<<dim3((a.Npad + 31) / 32), dim3(WAVES * kWave), lds, st>>>(a);
+  return LMX_OK;
+}
+
 template <int FMT, int WAVES, int H, int CPS>
 static int launch_plain_cfg(const GemvArgs &a, hipStream_t st) {
+#ifndef LMX_NO_IPL
+  if constexpr (H == 2) {
+    const int r = a.rotate == LMX_ROTATE_FWHT256 ? launch_ipl_kernel<FMT, true, WAVES, CPS>(a, st)
+                                                 : launch_ipl_kernel<FMT, false, WAVES, CPS>(a, st);
+    if (r != 1) return r;
+  }
+#endif
   if (a.rotate == LMX_ROTATE_FWHT256) return launch_plain_kernel<FMT, true, WAVES, H, CPS>(a, st);
   return launch_plain_kernel<FMT, false, WAVES, H, CPS>(a, st);
 }
