@@ -155,6 +155,10 @@ int upload(int fmt, size_t rows, size_t cols, size_t group, const uint8_t *plane
   w->reduce = choose_reduce();
   w->fullk = choose_fullk(fmt, w->Npad, w->Kp);
   w->staged = choose_staged();
+  {
+    const int fam = env_int("LMX_KERNEL", kKernelAuto);
+    w->kfamily = (fam == kKernelGeneric || fam == kKernelLean) ? fam : kKernelAuto;
+  }
   w->batched = env_int("LMX_BATCHED", 1) != 0;
 
   std::vector<uint8_t> tiles;
@@ -272,6 +276,7 @@ GemvArgs weight_args(const lmx_weight *w) {
   a.reduce = w->reduce;
   a.waves = w->waves;
   a.fullk = w->fullk;
+  a.kfamily = w->kfamily;
   a.staged = w->staged;
   a.xmode = kXModeNone;
   return a;

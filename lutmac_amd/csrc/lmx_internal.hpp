@@ -59,6 +59,7 @@ struct GemvArgs {
   int reduce;              // split-K reduction strategy (kReduce*)
   int waves;               // wavefronts (64-row slabs) per workgroup: 1, 2 or 4
   int fullk;               // 0: split-K kernel; else a kFullK_* configuration
+  int kfamily;             // full-K kernel family for plain activations (kKernel*)
   int staged;              // full-K: issue part of the weight loads after the table prologue
   int xmode;               // activation transform fused into the table prologue (kXMode*)
   const float *xw;         // kXModeRmsNorm: norm weight [cols]
@@ -119,6 +120,16 @@ inline FullKShape fullk_shape(int cfg) {
   return {0, 0, 0};
 }
 
+// Full-K kernel families for plain activations (no fused transform, no
+// argmax): the interleaved table-build/lookup kernel where it applies and
+// measured faster (two k-slices and at least two steps per wave, its tables
+// fit, not RRQ-3), else the lean kernel, else the generic one (which also
+// serves every fused transform).  LMX_KERNEL forces one for tests:
+// 1 generic, 2 lean.
+constexpr int kKernelAuto = 0;
+constexpr int kKernelGeneric = 1;
+constexpr int kKernelLean = 2;
+
 // Split-K reduction strategies.
 constexpr int kReduceTicket = 0;    // last workgroup of a row block sums (one release per group)
 constexpr int kReduceFenceAll = 1;  // same, with a device fence in every thread
@@ -154,6 +165,7 @@ struct lmx_weight {
   int reduce = 0;          // split-K reduction strategy
   int waves = 4;           // wavefronts per workgroup
   int fullk = 0;           // full-K kernel configuration (kFullK_*), 0 = split-K
+  int kfamily = 0;         // full-K kernel family for plain activations (kKernel*)
   int staged = 1;          // full-K: later chunks' weight loads after the prologue
   void *d_planes = nullptr;
   float *d_scales = nullptr;

@@ -1,7 +1,10 @@
 // lmx_kernels.hip -- gfx950 kernels of the bit-serial LUT-GEMV path.
 //
-// One GEMV is one launch of lut_gemv_fullk_kernel where its tables fit, or
-// lut_gemv_kernel (split-K) + splitk_reduce_kernel elsewhere.  Both share:
+// One GEMV is one launch of a full-K kernel where its tables fit, or
+// lut_gemv_kernel (split-K, last-workgroup reduction) elsewhere.  Full-K
+// launches with plain activations run lut_gemv_ipl_kernel (interleaved table
+// build and lookups) or lut_gemv_plain_kernel (lean front end); fused
+// transforms and the argmax epilogue run lut_gemv_fullk_kernel.  All share:
 //   * a fused prologue: each wavefront takes 256-chunks of x, rotates them
 //     with an in-register FWHT-256 (cross-lane butterflies via shuffles)
 //     when asked, and writes the 16-entry partial-sum table of every group
@@ -620,12 +623,6 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_fullk_kernel(GemvArgs 
     load_aux4(a, c2 * kRotChunk, lane, aux[j]);
   }
   __builtin_amdgcn_sched_barrier(0);
-#ifdef LMX_XWAIT
-#pragma unroll
-  for (int j = 0; j < XJ; ++j)
-    asm volatile("" ::"v"(xr[j].x), "v"(xr[j].y), "v"(xr[j].z), "v"(xr[j].w), "v"(aux[j][0]), "v"(aux[j][1]),
-                 "v"(aux[j][2]), "v"(aux[j][3]));
-#endif
   // A CU returns vector loads roughly in issue order, so every wave's x
   // requests go out before any wave's weight requests (the barrier does not
   // wait for the loads): no wave's tables wait behind the weight stream.
@@ -1016,7 +1013,7 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_ipl_kernel(GemvArgs a)
         if ((lane & 31) == 0) xsum[2 * c2 + h] = xs;
       }
     }
-    if (c == 0) {
+    if (c == 0) {   // later chunks stream in while this one is looked up
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int cc = 1; cc < CPS; ++cc) load_planes(cc);
@@ -1081,13 +1078,16 @@ static int launch_ipl_kernel(const GemvArgs &a, hipStream_t st) {
 
 template <int FMT, int WAVES, int H, int CPS>
 static int launch_plain_cfg(const GemvArgs &a, hipStream_t st) {
-#ifndef LMX_NO_IPL
-  if constexpr (H == 2) {
-    const int r = a.rotate == LMX_ROTATE_FWHT256 ? launch_ipl_kernel<FMT, true, WAVES, CPS>(a, st)
-                                                 : launch_ipl_kernel<FMT, false, WAVES, CPS>(a, st);
-    if (r != 1) return r;
+  // Interleaved where it measured faster: two k-slices per wave and at least
+  // two steps per wave (one step has nothing to interleave; 17920 x 1536
+  // ran 40% slower that way), RRQ-3 excepted (4% slower at 8192^2).
+  if constexpr (H == 2 && CPS >= 2 && FMT != LMX_FMT_RRQ3) {
+    if (a.kfamily != kKernelLean) {
+      const int r = a.rotate == LMX_ROTATE_FWHT256 ? launch_ipl_kernel<FMT, true, WAVES, CPS>(a, st)
+                                                   : launch_ipl_kernel<FMT, false, WAVES, CPS>(a, st);
+      if (r != 1) return r;
+    }
   }
-#endif
   if (a.rotate == LMX_ROTATE_FWHT256) return launch_plain_kernel<FMT, true, WAVES, H, CPS>(a, st);
   return launch_plain_kernel<FMT, false, WAVES, H, CPS>(a, st);
 }
@@ -1155,9 +1155,7 @@ template <int FMT>
 static int launch_fmt(const GemvArgs &a, hipStream_t st) {
   if (a.fullk) {
     int r = 1;
-#ifndef LMX_NO_PLAIN
-    if (a.xmode == kXModeNone && !a.amax) r = launch_plain<FMT>(a, st);
-#endif
+    if (a.xmode == kXModeNone && !a.amax && a.kfamily != kKernelGeneric) r = launch_plain<FMT>(a, st);
     if (r == 1) r = launch_fullk<FMT>(a, st);
     if (r) return r;
     hipError_t e = hipGetLastError();

@@ -169,6 +169,12 @@ def test_config3_8192(cuda, fmt):
     yb = w.gemv(dev(x2), flags=L.ROTATE_FWHT256).cpu().numpy()
     assert rel_max_err(ya, 2.0 * y.astype(np.float64) - 3.0 * yb) < 1e-5 * 4  # linearity
     assert not w.gemv(torch.zeros(n, device="cuda"), flags=L.ROTATE_FWHT256).any()
+    # the bench's 4/8-bit workload: input rotated once on the device, kernel unrotated
+    if fmt in (L.FMT_INT4, L.FMT_INT8):
+        xr = dev(x)
+        L.fwht256(xr)
+        yr = w.gemv(xr, flags=L.ROTATE_NONE).cpu().numpy()
+        assert rel_max_err(yr, oracle.planes_gemv(fmt, planes, scales, n, n, g, oracle.fwht256(x))) < TOL
 
 
 def test_batch_rows_independent(cuda):
@@ -216,13 +222,16 @@ PLAN_SHAPES = {
 }
 
 
+# family: 0 auto (interleaved where it applies, else lean, else generic),
+# 1 the generic full-K kernel, 2 the lean one; staged only affects the generic.
 @pytest.mark.parametrize("fmt", [1, 2, 3, 4, 5, 6, 7])
 @pytest.mark.parametrize("cfg", sorted(PLAN_SHAPES))
-@pytest.mark.parametrize("staged", [0, 1])
-def test_forced_kernel_plans(cuda, monkeypatch, fmt, cfg, staged):
+@pytest.mark.parametrize("staged,family", [(0, 1), (1, 1), (1, 0), (1, 2)])
+def test_forced_kernel_plans(cuda, monkeypatch, fmt, cfg, staged, family):
     rows, cols = PLAN_SHAPES[cfg]
     monkeypatch.setenv("LMX_FULLK", str(cfg))
     monkeypatch.setenv("LMX_STAGED", str(staged))
+    monkeypatch.setenv("LMX_KERNEL", str(family))
     planes, scales, g = synth.make_weights(fmt, rows, cols, seed=cfg * 10 + fmt, group=128)
     x = synth.make_activations(cols, seed=cfg + 40, outliers=True)
     w = L.Weight.from_planes(fmt, planes, scales, rows, cols, g)
