@@ -71,14 +71,19 @@ int choose_kslice(size_t Npad, size_t Kp, int waves) {
 // A configuration must cover all Kc chunks with its k-slices, fit the LDS
 // and keep its weight words in registers.  LMX_FULLK: 0 forces split-K,
 // 1..6 forces a configuration (when it fits).
-int choose_fullk(int fmt, size_t Npad, size_t Kp) {
+int choose_fullk(int fmt, size_t Npad, size_t Kp, int kfamily) {
   const int env = env_int("LMX_FULLK", -1);
   const size_t Kc = Kp / kChunk;
   FormatInfo fi;
   format_info(fmt, &fi);
   auto fits = [&](int cfg) {
     const FullKShape f = fullk_shape(cfg);
-    if (f.cps * fi.planes > 8) return false;  // keeps the weight words in registers (no spills)
+    // Weight words stay in registers (no spills): up to 8 plane words per
+    // lane in the generic kernel; 16 (int8 over two steps) in the
+    // interleaved kernel, which always serves 16x2x2 when it is allowed.
+    const bool regs = f.cps * fi.planes <= 8 ||
+                      (cfg == kFullK_16x2x2 && f.cps * fi.planes <= 16 && kfamily == kKernelAuto);
+    if (!regs) return false;
     return size_t(f.waves * f.h * f.cps) >= Kc && fullk_lds_bytes(f.waves, f.h, f.cps, Kc) <= kMaxLdsBytes;
   };
   if (env >= 0) return (env == 0 || !fits(env)) ? kFullK_None : env;
@@ -153,12 +158,12 @@ int upload(int fmt, size_t rows, size_t cols, size_t group, const uint8_t *plane
   w->waves = choose_waves();
   w->kslice = choose_kslice(w->Npad, w->Kp, w->waves);
   w->reduce = choose_reduce();
-  w->fullk = choose_fullk(fmt, w->Npad, w->Kp);
-  w->staged = choose_staged();
   {
     const int fam = env_int("LMX_KERNEL", kKernelAuto);
     w->kfamily = (fam == kKernelGeneric || fam == kKernelLean) ? fam : kKernelAuto;
   }
+  w->fullk = choose_fullk(fmt, w->Npad, w->Kp, w->kfamily);
+  w->staged = choose_staged();
   w->batched = env_int("LMX_BATCHED", 1) != 0;
 
   std::vector<uint8_t> tiles;
