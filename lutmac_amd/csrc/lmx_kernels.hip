@@ -116,9 +116,9 @@ __host__ __device__ constexpr uint32_t group_offset(int g) {
   return STAG ? uint32_t(64 * g + 16 * ((g >> 2) & 3) + 64 * (g >> 4)) : uint32_t(64 * g);
 }
 constexpr uint32_t kStagChunkBytes = 2176;   // group_offset<true>(31) + 64, 16-byte multiple
-// One k-slice of CPS staggered chunk blocks plus 256 B (room for the H = 4
-// slice shift), rounded to 256 B so every slice base is 256-byte aligned.
-__host__ __device__ constexpr uint32_t stag_slice_bytes(int cps) { return (cps * kStagChunkBytes + 511) / 256 * 256; }
+// One k-slice of CPS staggered chunk blocks plus 64 B (room for the H = 4
+// slice shift), rounded up to 256 B so every slice base is 256-byte aligned.
+__host__ __device__ constexpr uint32_t stag_slice_bytes(int cps) { return (cps * kStagChunkBytes + 64 + 255) / 256 * 256; }
 
 // cbase must be 256-byte aligned (v_perm keeps its bytes 1-2 only); coff is
 // a compile-time chunk offset folded into the ds_read immediate.
@@ -800,14 +800,14 @@ __device__ __forceinline__ void fwht256_regs_x16(float &x0, float &x1, float &x2
   lane_pair_stage<32>(x2, x3);
 }
 
-// Full-K kernel for plain activations (no fused transform, no argmax): the
-// same geometry, LDS layout, lookups and slice reduction as
-// lut_gemv_fullk_kernel, with a lean front end.  Weight and scale
-// addresses use 32-bit offsets and a shift for the scale group; x is
-// rotated (ROT) without its final 1/16, which is folded into the scales;
-// every wave builds the tables of its own 256-chunks only.  Needs H*CPS
-// even (each wave owns whole 256-chunks).
-template <int FMT, bool ROT, int WAVES, int H, int CPS>
+// Full-K kernel with a lean front end: the same geometry, lookups and
+// slice reduction as lut_gemv_fullk_kernel, staggered tables, weight and
+// scale addresses in 32-bit offsets with a shift for the scale group, x
+// rotated (ROT) without its final 1/16 (folded into the scales), every wave
+// building the tables of its own 256-chunks only, and the activation
+// transform XM (kXMode*) fixed at compile time.  Needs H*CPS even (each
+// wave owns whole 256-chunks).  No argmax epilogue.
+template <int FMT, bool ROT, int WAVES, int H, int CPS, int XM>
 __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_plain_kernel(GemvArgs a) {
   constexpr int P = Fmt<FMT>::P, NA = Fmt<FMT>::NA, S = Fmt<FMT>::S;
   constexpr int RW = kWave / H;
@@ -833,9 +833,15 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_plain_kernel(GemvArgs 
   // ---- x of this wave's 256-chunks (clamped in bounds, masked below) ----
   const int C2n = a.Kp / kRotChunk;
   const int c2base = wave * XJ;
-  float4 xr[XJ];
+  constexpr bool AUX = XM == kXModeRmsNorm || XM == kXModeSiluMul;
+  float4 xr[XJ], xa[XJ];
 #pragma unroll
-  for (int j = 0; j < XJ; ++j) xr[j] = load_x4_raw(a.x, min(c2base + j, C2n - 1) * kRotChunk, a.cols, lane);
+  for (int j = 0; j < XJ; ++j) {
+    const int k = min(min(c2base + j, C2n - 1) * kRotChunk + 4 * lane, a.cols - 4);
+    if constexpr (XM != kXModeAttnMerge) xr[j] = *reinterpret_cast<const float4 *>(a.x + k);
+    // norm weight, or the up half of a gate|up vector
+    if constexpr (AUX) xa[j] = *reinterpret_cast<const float4 *>((XM == kXModeRmsNorm ? a.xw : a.x + a.cols) + k);
+  }
   __builtin_amdgcn_sched_barrier(0);
   __builtin_amdgcn_s_barrier();   // every wave's x requests ahead of the weight stream
 
@@ -859,7 +865,28 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_plain_kernel(GemvArgs 
   }
   __builtin_amdgcn_sched_barrier(0);
 
-  // ---- prologue: (FWHT-256 x16) -> group tables of this wave's chunks ----
+  // The attention merge (its own dependent loads) after the weight loads.
+  if constexpr (XM == kXModeAttnMerge) {
+#pragma unroll
+    for (int j = 0; j < XJ; ++j)
+      load_x4_attn(a, min(c2base + j, C2n - 1) * kRotChunk, lane, xr[j].x, xr[j].y, xr[j].z, xr[j].w);
+  }
+  // RMSNorm: the waves' 256-chunks partition x, so the sum of squares over
+  // them (zero past cols) is the norm's, summed in the same order in every
+  // workgroup (norm.cpp:18-34).
+  float inv_rms = 1.0f;
+  if constexpr (XM == kXModeRmsNorm) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < XJ; ++j) {
+      float x0, x1, x2, x3;
+      mask_x4(xr[j], (c2base + j) * kRotChunk, a.cols, lane, x0, x1, x2, x3);
+      if (c2base + j < C2n) ss += (x0 * x0 + x1 * x1) + (x2 * x2 + x3 * x3);
+    }
+    inv_rms = wg_inv_rms_from<WAVES * kWave>(ss, a.cols, a.eps, red);
+  }
+
+  // ---- prologue: (transform) -> (FWHT-256 x16) -> group tables of this wave's chunks ----
   const uint32_t goff = group_offset<true>(lane & 31);
 #pragma unroll
   for (int j = 0; j < XJ; ++j) {
@@ -867,6 +894,10 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_plain_kernel(GemvArgs 
     if (c2 >= C2n) break;   // wave-uniform
     float x0, x1, x2, x3;
     mask_x4(xr[j], c2 * kRotChunk, a.cols, lane, x0, x1, x2, x3);
+    if constexpr (AUX) {
+      const float aux[4] = {xa[j].x, xa[j].y, xa[j].z, xa[j].w};
+      xform4(XM, inv_rms, aux, x0, x1, x2, x3);
+    }
     if constexpr (ROT) fwht256_regs_x16(x0, x1, x2, x3, lane);
     float t[16];
     group_table(x0, x1, x2, x3, t);
@@ -1049,18 +1080,19 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_ipl_kernel(GemvArgs a)
   }
 }
 
-template <int FMT, bool ROT, int WAVES, int H, int CPS>
+template <int FMT, bool ROT, int WAVES, int H, int CPS, int XM>
 static int launch_plain_kernel(const GemvArgs &a, hipStream_t st) {
   const size_t Kc = size_t(a.Kp / kChunk);
   const size_t lds = fullk_prefix_bytes<WAVES, H, CPS>() + (Kc + CPS - 1) / CPS * stag_slice_bytes(CPS);
   if (lds > kMaxLdsBytes) return 1;   // staggered tables do not fit: the generic kernel serves it
   static const hipError_t attr = hipFuncSetAttribute(
-      reinterpret_cast<const void *>(&lut_gemv_plain_kernel<FMT, ROT, WAVES, H, CPS>),
+      reinterpret_cast<const void *>(&lut_gemv_plain_kernel<FMT, ROT, WAVES, H, CPS, XM>),
       hipFuncAttributeMaxDynamicSharedMemorySize, int(kMaxLdsBytes));
   if (attr != hipSuccess) return fail(LMX_ERR_LAUNCH_FAILED, "hipFuncSetAttribute: %s", hipGetErrorString(attr));
   if (lds > kMaxLdsBytes) return fail(LMX_ERR_INVALID_ARGUMENT, "full-K tables need %zu B of LDS", lds);
   constexpr int RW = kWave / H;
-  lut_gemv_plain_kernel<FMT, ROT, WAVES, H, CPS><<<dim3((a.Npad + RW - 1) / RW), dim3(WAVES * kWave), lds, st>>>(a);
+  lut_gemv_plain_kernel<FMT, ROT, WAVES, H, CPS, XM>
+      <<<dim3((a.Npad + RW - 1) / RW), dim3(WAVES * kWave), lds, st>>>(a);
   return LMX_OK;
 }
 
@@ -1081,6 +1113,20 @@ static int launch_plain_cfg(const GemvArgs &a, hipStream_t st) {
   // Interleaved where it measured faster: two k-slices per wave and at least
   // two steps per wave (one step has nothing to interleave; 17920 x 1536
   // ran 40% slower that way), RRQ-3 excepted (4% slower at 8192^2).
+  if (a.xmode != kXModeNone) {
+    // Fused transforms on the lean kernel: the decode step's linears (4-bit,
+    // unrotated); other formats take the generic kernel.
+    if constexpr (FMT == LMX_FMT_INT4) {
+      if (a.rotate == LMX_ROTATE_NONE) {
+        switch (a.xmode) {
+        case kXModeRmsNorm: return launch_plain_kernel<FMT, false, WAVES, H, CPS, kXModeRmsNorm>(a, st);
+        case kXModeSiluMul: return launch_plain_kernel<FMT, false, WAVES, H, CPS, kXModeSiluMul>(a, st);
+        case kXModeAttnMerge: return launch_plain_kernel<FMT, false, WAVES, H, CPS, kXModeAttnMerge>(a, st);
+        }
+      }
+    }
+    return 1;
+  }
   if constexpr (H == 2 && CPS >= 2 && FMT != LMX_FMT_RRQ3) {
     if (a.kfamily != kKernelLean) {
       const int r = a.rotate == LMX_ROTATE_FWHT256 ? launch_ipl_kernel<FMT, true, WAVES, CPS>(a, st)
@@ -1088,8 +1134,8 @@ static int launch_plain_cfg(const GemvArgs &a, hipStream_t st) {
       if (r != 1) return r;
     }
   }
-  if (a.rotate == LMX_ROTATE_FWHT256) return launch_plain_kernel<FMT, true, WAVES, H, CPS>(a, st);
-  return launch_plain_kernel<FMT, false, WAVES, H, CPS>(a, st);
+  if (a.rotate == LMX_ROTATE_FWHT256) return launch_plain_kernel<FMT, true, WAVES, H, CPS, kXModeNone>(a, st);
+  return launch_plain_kernel<FMT, false, WAVES, H, CPS, kXModeNone>(a, st);
 }
 
 // The plain kernel serves full-K launches without a fused transform or an
@@ -1155,7 +1201,7 @@ template <int FMT>
 static int launch_fmt(const GemvArgs &a, hipStream_t st) {
   if (a.fullk) {
     int r = 1;
-    if (a.xmode == kXModeNone && !a.amax && a.kfamily != kKernelGeneric) r = launch_plain<FMT>(a, st);
+    if (!a.amax && a.kfamily != kKernelGeneric) r = launch_plain<FMT>(a, st);
     if (r == 1) r = launch_fullk<FMT>(a, st);
     if (r) return r;
     hipError_t e = hipGetLastError();
