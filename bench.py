@@ -193,6 +193,39 @@ def decode_bench(n_prompt, n_new, seed=2024):
             "setup_s": round(setup_s, 1)}
 
 
+def qwen_decode_bench(context, n_new, seed=2025):
+    """BASELINE config 5 at batch 1: greedy decode of a random-init
+    Qwen-2.5-1.5B architecture (QKV bias, GQA 12/2, head_dim 128, tied
+    151936 x 1536 4-bit head) with a KV context of `context` positions: a
+    seeded prompt of context - n_new tokens prefilled token by token, then
+    n_new generated tokens, each attending over ~context positions."""
+    from lutmac_amd import decode as D
+    from dataclasses import replace
+    cfg = replace(D.QWEN_2_5_1_5B, max_seq=context)
+    t0 = time.perf_counter()
+    model = D.SyntheticModel(cfg, seed=seed, group=128)
+    dec = D.Decoder(model)
+    setup_s = time.perf_counter() - t0
+    prompt = np.random.default_rng(seed + 1).integers(0, cfg.vocab, context - n_new)
+    out, pre_ms, dec_ms = dec.generate(prompt, n_new)
+    tok_s = (n_new - 1) / (dec_ms / 1e3)
+    B = decode_weight_bytes(cfg, 128)
+    kv = 2 * cfg.n_layers * cfg.kv_dim * 4 * (context - n_new / 2)
+    dec.close()
+    return {"metric": "Qwen-2.5-1.5B-arch decode tokens/s bs=1", "tokens_per_s": round(tok_s, 1),
+            "ms_per_token": round(dec_ms / (n_new - 1), 4), "kv_context": context,
+            "prefill_tokens": context - n_new, "n_new": n_new,
+            "weight_bytes_per_token": B, "kv_bytes_per_token_mean": int(kv),
+            "achieved_GB_s": round((B + kv) * tok_s / 1e9, 1),
+            "frac_of_peak": round((B + kv) * tok_s / 1e9 / HBM_PEAK_GBPS, 4),
+            "config": {"workload": "Qwen-2.5-1.5B architecture, random-init N(0,0.02) weights, 4-bit per-128-group "
+                                   "linears, QKV bias, tied 4-bit embedding/head, greedy, batch 1 (BASELINE config 5; "
+                                   "batch 4/16 in batched_qwen_linears)",
+                       "layers": cfg.n_layers, "hidden": cfg.hidden, "heads": cfg.n_heads,
+                       "kv_heads": cfg.n_kv_heads, "head_dim": cfg.head_dim, "ffn": cfg.ffn, "vocab": cfg.vocab},
+            "setup_s": round(setup_s, 1)}
+
+
 def cpu_decode_baseline(budget_s, seed=2024):
     """The reference's own Model::forward (oracle/_ref/libref.so, 1 thread:
     lut_linear -> int4_gemv scalar) on the same architecture in its native
@@ -307,6 +340,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true", help="skip the 1B-architecture decode")
     ap.add_argument("--no-batched", action="store_true", help="skip the Qwen-shape batch 1/4/16 sweep")
+    ap.add_argument("--no-qwen-decode", action="store_true", help="skip the Qwen-2.5-1.5B batch-1 decode")
+    ap.add_argument("--qwen-context", type=int, default=2048)
+    ap.add_argument("--qwen-tokens", type=int, default=64)
     ap.add_argument("--decode-prompt", type=int, default=64)
     ap.add_argument("--decode-tokens", type=int, default=256)
     ap.add_argument("--cpu-decode-seconds", type=float, default=10.0)
@@ -342,6 +378,11 @@ def main():
         decode = decode_bench(args.decode_prompt, args.decode_tokens)
         print(f"# decode: {decode['tokens_per_s']} tokens/s ({decode['ms_per_token']} ms/token)",
               file=sys.stderr, flush=True)
+    qwen = None
+    if not args.no_decode and not args.no_qwen_decode:
+        qwen = qwen_decode_bench(args.qwen_context, args.qwen_tokens)
+        print(f"# qwen decode (KV {qwen['kv_context']}): {qwen['tokens_per_s']} tokens/s "
+              f"({qwen['ms_per_token']} ms/token)", file=sys.stderr, flush=True)
     batched = None if args.no_batched else batched_bench(torch, L)
     if batched is not None:
         print("# batched linears per step: " + ", ".join(
@@ -373,6 +414,7 @@ def main():
                      "traffic": load_traffic(f"{head['format']}_{args.size}")},
         "cpu_baseline": cpu,
         "decode": decode,
+        "qwen_decode": qwen,
         "batched_qwen_linears": batched,
         "sweep": sweep,
     }

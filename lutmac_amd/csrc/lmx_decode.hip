@@ -7,12 +7,12 @@
 //   per layer:
 //     GEMV qkv             RMSNorm(input_norm) fused into the table prologue,
 //                          q|k|v rows in one weight, + bias (model.cpp:296-323)
-//     attn_chunk_kernel    RoPE of q and k, KV-cache append, scores, partial
-//                          softmax and weighted V sums over 64-position chunks
-//                          (model.cpp:326-372, embedding.cpp:36-75,
-//                          attention.cpp:23-42)
-//     GEMV o               merges the chunks while loading its activations;
-//                          + residual: the hidden state is the bias and the
+//     attn_kernel          RoPE of q and k, KV-cache append, scores, partial
+//                          softmax and weighted V sums over 64-position chunks,
+//                          and the merge of the chunks by the last workgroup
+//                          of each KV head (model.cpp:326-372,
+//                          embedding.cpp:36-75, attention.cpp:23-42)
+//     GEMV o               + residual: the hidden state is the bias and the
 //                          output (model.cpp:376-388)
 //     GEMV gate|up         RMSNorm(post_norm) fused (model.cpp:390-403)
 //     GEMV down            SiLU(gate)*up fused into the prologue, + residual
@@ -92,14 +92,8 @@ __global__ __launch_bounds__(256) void embed_kernel(const uint8_t *__restrict__ 
   out[k] = weight_value<FMT>(b, s);
 }
 
-// Decode attention split over the sequence in chunks of kAttnChunk = 64
-// positions, so the work spreads over n_kv * chunks workgroups instead of
-// n_kv: workgroup (kv head, chunk); wave w serves query head kvh * group + w
-// over the chunk's positions and writes the chunk's partial softmax (max
-// score m, sum of exp l, sum of exp * v) for that head; chunks past the
-// sequence write an empty partial.  The o-projection GEMV merges the chunks
-// while it loads its activations (kXModeAttnMerge).  The workgroup whose
-// chunk holds `pos` also rotates k and appends k, v at `pos`.
+// RoPE of one head vector: pairs (d, d + HD/2) rotated by pf * freq[d]
+// (embedding.cpp:36-75 pairs the halves the same way).
 template <int HD>
 __device__ __forceinline__ void rope_pair(const float *in, float *out, const float *freq, float pf, int lane) {
   constexpr int HALF = HD / 2;
@@ -110,115 +104,6 @@ __device__ __forceinline__ void rope_pair(const float *in, float *out, const flo
     out[d] = a0 * cs - a1 * sn;
     out[d + HALF] = a0 * sn + a1 * cs;
   }
-}
-
-template <int HD>
-__global__ __launch_bounds__(512) void attn_chunk_kernel(const float *__restrict__ qkv, float *__restrict__ kc,
-                                                         float *__restrict__ vc, const int *__restrict__ pos_p,
-                                                         const float *__restrict__ freq, float pos_div, int n_heads,
-                                                         int n_kv, int group, int max_seq, float scale,
-                                                         float *__restrict__ part, int n_chunks) {
-  constexpr int VD = HD / kWave;                  // value columns per lane
-  constexpr bool kPrefetchV = HD == 64;           // 64 value registers per lane
-  __shared__ float qs[8][HD];
-  __shared__ float pw[8][kAttnChunk];
-  __shared__ float knew[HD];
-  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
-  const int kvh = blockIdx.x % n_kv, chunk = blockIdx.x / n_kv;
-  const size_t row = size_t(n_kv) * HD;
-  const int head = kvh * group + wave;
-  const int t0 = chunk * kAttnChunk;
-  const float *kin = qkv + size_t(n_heads) * HD + kvh * HD;
-  const float *vin = kin + row;
-  // Loads first, none depending on the position, so the kernel pays about one
-  // memory round trip: the position, this lane's cached key row t0 + lane
-  // and (head_dim 64) the chunk's value column d = lane.  The cache holds
-  // n_chunks * 64 rows, so every row is in bounds; rows at or past the
-  // position are masked below.
-  const int pos = min(*pos_p, max_seq - 1);
-  float4 kr[HD / 4];
-  {
-    const float4 *src = reinterpret_cast<const float4 *>(kc + size_t(t0 + lane) * row + kvh * HD);
-#pragma unroll
-    for (int d4 = 0; d4 < HD / 4; ++d4) kr[d4] = src[d4];
-  }
-  float vv[kPrefetchV ? kAttnChunk : 1];
-  if constexpr (kPrefetchV) {
-    const float *vb = vc + size_t(t0) * row + kvh * HD + lane;
-#pragma unroll
-    for (int j = 0; j < kAttnChunk; ++j) vv[j] = vb[size_t(j) * row];
-  }
-  float *dst = part + (size_t(head) * n_chunks + chunk) * (HD + 4);   // m, l, -, -, o[HD]
-  if (t0 > pos) {   // chunk past the sequence: an empty partial (weight 0 in the merge)
-#pragma unroll
-    for (int u = 0; u < VD; ++u) dst[4 + u * kWave + lane] = 0.0f;
-    if (lane == 0) dst[0] = -INFINITY, dst[1] = 0.0f;
-    return;   // uniform over the workgroup
-  }
-  const float pf = float(pos) / pos_div;
-  const int t = t0 + lane;
-  const bool valid = t <= pos;
-  const int n = min(kAttnChunk, pos - t0 + 1);     // positions of the chunk in the sequence
-  const bool own = pos / kAttnChunk == chunk;      // the chunk holds the new position
-  const int jnew = own ? pos - t0 : -1;            // its index in the chunk
-  const int nold = own ? n - 1 : n;                // positions already in the cache
-
-  if (own && wave == 0) rope_pair<HD>(kin, knew, freq, pf, lane);
-  rope_pair<HD>(qkv + size_t(head) * HD, qs[wave], freq, pf, lane);
-  __syncthreads();
-  if (own && wave == 0) {   // append the new position to the cache
-    for (int d = lane; d < HD; d += kWave) {
-      kc[size_t(pos) * row + kvh * HD + d] = knew[d];
-      vc[size_t(pos) * row + kvh * HD + d] = vin[d];
-    }
-  }
-
-  // scores q.k_t * scale of positions t0 + lane (model.cpp:341-351)
-  float sc = -INFINITY;
-  if (valid) {
-    float acc = 0.0f;
-    const bool isnew = lane == jnew;
-#pragma unroll
-    for (int d4 = 0; d4 < HD / 4; ++d4) {
-      const float4 kv = isnew ? make_float4(knew[4 * d4], knew[4 * d4 + 1], knew[4 * d4 + 2], knew[4 * d4 + 3])
-                              : kr[d4];
-      acc += qs[wave][4 * d4] * kv.x;
-      acc += qs[wave][4 * d4 + 1] * kv.y;
-      acc += qs[wave][4 * d4 + 2] * kv.z;
-      acc += qs[wave][4 * d4 + 3] * kv.w;
-    }
-    sc = acc * scale;
-  }
-  const float m = lane_max<32>(sc, lane);
-  const float e = valid ? expf(sc - m) : 0.0f;
-  const float l = lane_sum<32>(e, lane);
-  pw[wave][lane] = lane < nold ? e : 0.0f;          // cached positions only
-  const float enew = __shfl(e, jnew < 0 ? 0 : jnew, 64);
-  __syncthreads();
-
-  // o[d] = sum_j e_j v_{t0+j}[d] over the cached positions (8 partial sums),
-  // plus e_new * v_new for the new one (model.cpp:362-371)
-#pragma unroll
-  for (int u = 0; u < VD; ++u) {
-    const int d = u * kWave + lane;
-    float s8[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    if constexpr (kPrefetchV) {
-#pragma unroll
-      for (int j = 0; j < kAttnChunk; ++j) s8[j % 8] += pw[wave][j] * vv[j];
-    } else {
-      const float *vb = vc + size_t(t0) * row + kvh * HD + d;
-      int j = 0;
-      for (; j + 8 <= nold; j += 8) {
-#pragma unroll
-        for (int w8 = 0; w8 < 8; ++w8) s8[w8] += pw[wave][j + w8] * vb[size_t(j + w8) * row];
-      }
-      for (; j < nold; ++j) s8[0] += pw[wave][j] * vb[size_t(j) * row];
-    }
-    float o = ((s8[0] + s8[1]) + (s8[2] + s8[3])) + ((s8[4] + s8[5]) + (s8[6] + s8[7]));
-    if (own) o += enew * vin[d];
-    dst[4 + d] = o;
-  }
-  if (lane == 0) dst[0] = m, dst[1] = l;
 }
 
 // Greedy token of the step: the largest of the head GEMV's per-wave argmax
@@ -283,6 +168,188 @@ std::vector<float> rope_freqs(const lmx_decoder_config &c) {
   return f;
 }
 
+// Attention with the chunk merge inside: one workgroup per (KV head, 64
+// positions), 8 waves.  All 8 waves first load the chunk's 64 cached K and V
+// rows of the KV head into LDS (every row is in bounds: the cache holds whole
+// chunks), so the chunk costs one memory round trip whatever the head
+// dimension; wave w < group then serves query head kvh*group + w: RoPE of q
+// (and of the new key in the chunk holding the position), scores, a partial
+// softmax and the weighted V sum of the chunk (model.cpp:326-372,
+// attention.cpp:23-42), written as (m, l, o[HD]).  The last workgroup of the
+// KV head to finish (a device-scope ticket, the split-K handoff of the GEMV)
+// merges the chunks up to the position in chunk order, x = sum_c e^(m_c - M)
+// o_c / sum_c e^(m_c - M) l_c with M = max_c m_c, and writes the heads'
+// attention output, so the o-projection is a plain GEMV.  Partials and
+// tickets travel as device-scope relaxed atomics (no L2 writeback needed);
+// the last workgroup clears the ticket for the next step.
+template <int HD>
+__global__ __launch_bounds__(512) void attn_kernel(const float *__restrict__ qkv, float *__restrict__ kc,
+                                                   float *__restrict__ vc, const int *__restrict__ pos_p,
+                                                   const float *__restrict__ freq, float pos_div, int n_heads,
+                                                   int n_kv, int group, int max_seq, float scale,
+                                                   float *__restrict__ part, int n_chunks,
+                                                   unsigned *__restrict__ tickets, float *__restrict__ out) {
+  constexpr int VD = HD / kWave;          // value columns per lane
+  constexpr int NT = 512;
+  constexpr int KV4 = kAttnChunk * HD / 4 / NT;   // float4 of K (and of V) per thread
+  static_assert(KV4 >= 1, "chunk rows cover the workgroup");
+  __shared__ float ks[kAttnChunk][HD + 4];   // padded rows: lane j reads row j without bank conflicts
+  __shared__ float vs[kAttnChunk][HD];
+  __shared__ float qs[8][HD];
+  __shared__ float pw[8][kAttnChunk];
+  __shared__ float knew[HD];
+  __shared__ unsigned ticket;
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  const int kvh = blockIdx.x % n_kv, chunk = blockIdx.x / n_kv;
+  const size_t row = size_t(n_kv) * HD;
+  const int t0 = chunk * kAttnChunk;
+  const float *kin = qkv + size_t(n_heads) * HD + kvh * HD;
+  const float *vin = kin + row;
+  const int pos = min(*pos_p, max_seq - 1);
+
+  // ---- the chunk's K and V rows into LDS (loads first, one round trip) ----
+  {
+    float4 kr[KV4], vr[KV4];
+#pragma unroll
+    for (int i = 0; i < KV4; ++i) {
+      const int f = int(threadIdx.x) + i * NT;          // float4 index in the 64 x HD chunk
+      const int r = f / (HD / 4), c4 = f % (HD / 4);
+      kr[i] = *reinterpret_cast<const float4 *>(kc + size_t(t0 + r) * row + kvh * HD + 4 * c4);
+      vr[i] = *reinterpret_cast<const float4 *>(vc + size_t(t0 + r) * row + kvh * HD + 4 * c4);
+    }
+#pragma unroll
+    for (int i = 0; i < KV4; ++i) {
+      const int f = int(threadIdx.x) + i * NT;
+      const int r = f / (HD / 4), c4 = f % (HD / 4);
+      *reinterpret_cast<float4 *>(&ks[r][4 * c4]) = kr[i];
+      *reinterpret_cast<float4 *>(&vs[r][4 * c4]) = vr[i];
+    }
+  }
+  const bool live = t0 <= pos;                      // chunk holds positions of the sequence
+  const bool own = pos / kAttnChunk == chunk;       // the chunk holds the new position
+  const float pf = float(pos) / pos_div;
+  if (live && wave < group) {
+    rope_pair<HD>(qkv + size_t(kvh * group + wave) * HD, qs[wave], freq, pf, lane);
+    if (own && wave == 0) rope_pair<HD>(kin, knew, freq, pf, lane);
+  }
+  __syncthreads();
+
+  if (wave < group) {
+    const int head = kvh * group + wave;
+    float *dst = part + (size_t(head) * n_chunks + chunk) * (HD + 4);   // m, l, -, -, o[HD]
+    float o[VD], m = -INFINITY, l = 0.0f;
+#pragma unroll
+    for (int u = 0; u < VD; ++u) o[u] = 0.0f;
+    if (live) {
+      const int t = t0 + lane;
+      const bool valid = t <= pos;
+      const int n = min(kAttnChunk, pos - t0 + 1);
+      const int jnew = own ? pos - t0 : -1;
+      const int nold = own ? n - 1 : n;
+      float sc = -INFINITY;
+      if (valid) {
+        const float *kv = lane == jnew ? knew : ks[lane];
+        float acc = 0.0f;
+#pragma unroll
+        for (int d4 = 0; d4 < HD / 4; ++d4) {
+          const float4 k4 = *reinterpret_cast<const float4 *>(kv + 4 * d4);
+          const float4 q4 = *reinterpret_cast<const float4 *>(&qs[wave][4 * d4]);
+          acc += q4.x * k4.x;
+          acc += q4.y * k4.y;
+          acc += q4.z * k4.z;
+          acc += q4.w * k4.w;
+        }
+        sc = acc * scale;
+      }
+      m = lane_max<32>(sc, lane);
+      const float e = valid ? expf(sc - m) : 0.0f;
+      l = lane_sum<32>(e, lane);
+      pw[wave][lane] = lane < nold ? e : 0.0f;      // cached positions only
+      const float enew = __shfl(e, jnew < 0 ? 0 : jnew, 64);
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int u = 0; u < VD; ++u) {
+        const int d = u * kWave + lane;
+        float s8[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+        for (int j = 0; j < kAttnChunk; ++j) s8[j % 8] += pw[wave][j] * vs[j][d];
+        o[u] = ((s8[0] + s8[1]) + (s8[2] + s8[3])) + ((s8[4] + s8[5]) + (s8[6] + s8[7]));
+        if (own) o[u] += enew * vin[d];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < VD; ++u)
+      __hip_atomic_store(dst + 4 + u * kWave + lane, o[u], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (lane == 0) {
+      __hip_atomic_store(dst, m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(dst + 1, l, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (own && wave == 0) {   // append the new position to the cache
+      for (int d = lane; d < HD; d += kWave) {
+        kc[size_t(pos) * row + kvh * HD + d] = knew[d];
+        vc[size_t(pos) * row + kvh * HD + d] = vin[d];
+      }
+    }
+  }
+  // ---- ticket: the last workgroup of this KV head merges ----
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0)
+    ticket = __hip_atomic_fetch_add(tickets + kvh, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  if (ticket != unsigned(n_chunks - 1)) return;   // uniform over the workgroup
+  if (wave < group) {
+    const int head = kvh * group + wave;
+    const float *ph = part + size_t(head) * n_chunks * (HD + 4);
+    const int nused = pos / kAttnChunk + 1;        // chunks holding positions
+    // chunk weights: lane c holds chunk c (64 at a time)
+    float M = -INFINITY;
+    for (int c0 = 0; c0 < nused; c0 += kWave) {
+      const int c = c0 + lane;
+      const float mc = c < nused ? __hip_atomic_load(ph + size_t(c) * (HD + 4), __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT) : -INFINITY;
+      M = fmaxf(M, lane_max<32>(mc, lane));
+    }
+    float L = 0.0f, o[VD];
+#pragma unroll
+    for (int u = 0; u < VD; ++u) o[u] = 0.0f;
+    for (int c0 = 0; c0 < nused; c0 += kWave) {
+      const int c = c0 + lane;
+      float wc = 0.0f, lc = 0.0f;
+      if (c < nused) {
+        const float mc = __hip_atomic_load(ph + size_t(c) * (HD + 4), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        lc = __hip_atomic_load(ph + size_t(c) * (HD + 4) + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        wc = expf(mc - M);
+      }
+      L += lane_sum<32>(wc * lc, lane);
+      pw[wave][lane] = wc;
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      const int nb = min(kWave, nused - c0);
+      for (int j0 = 0; j0 < nb; j0 += 8) {   // 8 chunks' loads in flight at a time
+        float v[8][VD];
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj)
+#pragma unroll
+          for (int u = 0; u < VD; ++u)
+            v[jj][u] = j0 + jj < nb ? __hip_atomic_load(ph + size_t(c0 + j0 + jj) * (HD + 4) + 4 + u * kWave + lane,
+                                                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                    : 0.0f;
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj)
+#pragma unroll
+          for (int u = 0; u < VD; ++u) o[u] += (j0 + jj < nb ? pw[wave][j0 + jj] : 0.0f) * v[jj][u];
+      }
+      __builtin_amdgcn_wave_barrier();
+    }
+    const float inv = 1.0f / L;
+#pragma unroll
+    for (int u = 0; u < VD; ++u) out[size_t(head) * HD + u * kWave + lane] = o[u] * inv;
+  }
+  if (threadIdx.x == 0) __hip_atomic_store(tickets + kvh, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 size_t attn_chunks(const lmx_decoder_config &c) { return (c.max_seq + kAttnChunk - 1) / kAttnChunk; }
 
 }  // namespace
@@ -303,6 +370,8 @@ struct lmx_decoder {
   float *hidden = nullptr, *qkv = nullptr, *gate_up = nullptr, *logits = nullptr;
   float *kcache = nullptr, *vcache = nullptr, *freq = nullptr;
   float *attn_part = nullptr;            // [n_heads][chunks][m, l, -, -, o[head_dim]]
+  float *attn_out = nullptr;             // [n_heads * head_dim] merged attention output
+  unsigned *attn_tickets = nullptr;      // [n_kv_heads] chunk tickets (zero between steps)
   unsigned long long *amax = nullptr;    // per-wave argmax keys of the head GEMV
   size_t amax_slots = 0;
   int *tokens = nullptr, *pos = nullptr;
@@ -341,19 +410,6 @@ int gemv(const lmx_weight *w, const float *x, float *y, const float *bias, int x
   return launch_gemv(w->format, a, st);
 }
 
-// o-projection with the attention chunks merged in its activation loader;
-// the hidden state is the residual (bias) and the output.
-int gemv_attn_merge(lmx_decoder *d, const lmx_weight *o, hipStream_t st) {
-  GemvArgs a = weight_args(o);
-  a.x = d->attn_part;
-  a.y = d->hidden;
-  a.bias = d->hidden;
-  a.rotate = rotates(o->format) ? LMX_ROTATE_FWHT256 : LMX_ROTATE_NONE;
-  a.xmode = kXModeAttnMerge;
-  a.achunks = int(attn_chunks(d->cfg));
-  a.ahd_shift = d->cfg.head_dim == 64 ? 6 : 7;
-  return launch_gemv(o->format, a, st);
-}
 
 template <int FMT>
 void launch_embed(const lmx_weight *w, const int *tokens, const int *pos, float *out, hipStream_t st) {
@@ -383,14 +439,15 @@ int attention(lmx_decoder *d, size_t layer, hipStream_t st) {
   const size_t per_layer = size_t(nch) * kAttnChunk * c.n_kv_heads * c.head_dim;
   float *kc = d->kcache + layer * per_layer, *vc = d->vcache + layer * per_layer;
   const float scale = 1.0f / std::sqrt(float(c.head_dim));   // model.cpp:337
-  const dim3 grid(unsigned(c.n_kv_heads * nch)), block(unsigned(group * kWave));
+  const dim3 grid(unsigned(c.n_kv_heads * nch));
   if (c.head_dim == 64)
-    attn_chunk_kernel<64><<<grid, block, 0, st>>>(d->qkv, kc, vc, d->pos, d->freq, d->pos_div, int(c.n_heads),
-                                                  int(c.n_kv_heads), group, int(c.max_seq), scale, d->attn_part, nch);
+    attn_kernel<64><<<grid, dim3(512), 0, st>>>(d->qkv, kc, vc, d->pos, d->freq, d->pos_div, int(c.n_heads),
+                                                int(c.n_kv_heads), group, int(c.max_seq), scale, d->attn_part, nch,
+                                                d->attn_tickets, d->attn_out);
   else
-    attn_chunk_kernel<128><<<grid, block, 0, st>>>(d->qkv, kc, vc, d->pos, d->freq, d->pos_div, int(c.n_heads),
-                                                   int(c.n_kv_heads), group, int(c.max_seq), scale, d->attn_part,
-                                                   nch);
+    attn_kernel<128><<<grid, dim3(512), 0, st>>>(d->qkv, kc, vc, d->pos, d->freq, d->pos_div, int(c.n_heads),
+                                                 int(c.n_kv_heads), group, int(c.max_seq), scale, d->attn_part, nch,
+                                                 d->attn_tickets, d->attn_out);
   return launch_err("attention");
 }
 
@@ -417,7 +474,7 @@ int step(lmx_decoder *d, float *logits_out, hipStream_t st) {
     const lmx_decoder::Layer &L = d->layers[l];
     if ((r = gemv(L.qkv, d->hidden, d->qkv, L.qkv_bias, kXModeRmsNorm, L.in_norm, c.rms_eps, st)) ||
         (r = attention(d, l, st)) ||
-        (r = gemv_attn_merge(d, L.o, st)) ||
+        (r = gemv(L.o, d->attn_out, d->hidden, d->hidden, kXModeNone, nullptr, 0.0f, st)) ||
         (r = gemv(L.gate_up, d->hidden, d->gate_up, nullptr, kXModeRmsNorm, L.post_norm, c.rms_eps, st)) ||
         (r = gemv(L.down, d->gate_up, d->hidden, d->hidden, kXModeSiluMul, nullptr, 0.0f, st)))
       return r;
@@ -498,6 +555,8 @@ int lmx_decoder_create(const lmx_decoder_config *cfg, lmx_decoder **out) {
       (st = d->alloc(reinterpret_cast<void **>(&d->pos), 4)) ||
       (st = d->alloc(reinterpret_cast<void **>(&d->attn_part),
                      c.n_heads * attn_chunks(c) * (c.head_dim + 4) * sizeof(float))) ||
+      (st = d->alloc(reinterpret_cast<void **>(&d->attn_out), c.n_heads * c.head_dim * sizeof(float))) ||
+      (st = d->alloc(reinterpret_cast<void **>(&d->attn_tickets), c.n_kv_heads * sizeof(unsigned))) ||
       (st = upload(d, &d->freq, fr.data(), fr.size()))) {
     delete d;
     return st;

@@ -65,9 +65,6 @@ struct GemvArgs {
   const float *xw;         // kXModeRmsNorm: norm weight [cols]
   float eps;               // kXModeRmsNorm: epsilon
   unsigned long long *amax;  // when set: per-wave argmax keys of y (gemv_argmax_slots of them)
-  // kXModeAttnMerge: x is [heads][chunks][m, l, -, -, o[head_dim]] attention partials
-  int achunks;             // chunks per head in the partials
-  int ahd_shift;           // log2(head_dim)
 };
 
 // Activation transforms applied while the tables are built:
@@ -75,14 +72,10 @@ struct GemvArgs {
 //                   (norm.cpp:18-34), the sum taken over x[0..cols) by every workgroup
 //   kXModeSiluMul:  x'[k] = silu(x[k]) * x[cols + k]  (model.cpp:36,413-416: gate and
 //                   up halves of one fused gate|up output)
-// (both applied by xform4 after the load; the merge below replaces the load)
+// (both applied by xform4 after the load)
 constexpr int kXModeNone = 0;
 constexpr int kXModeRmsNorm = 1;
 constexpr int kXModeSiluMul = 2;
-//   kXModeAttnMerge: x[h*hd + d] = sum_c e^(m_c - M) o_c[d] / sum_c e^(m_c - M) l_c over
-//                   the attention chunks of head h (partials m, l, o[hd]; empty chunks
-//                   m = -inf, l = 0)
-constexpr int kXModeAttnMerge = 3;
 constexpr int kAttnChunk = 64;
 
 // Full-K kernel configurations (waves x k-slices per wave x chunks per slice):

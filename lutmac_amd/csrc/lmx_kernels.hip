@@ -275,37 +275,6 @@ __device__ __forceinline__ void mask_x4(const float4 v, int k0, int cols, int la
   x3 = in ? v.w : 0.0f;
 }
 
-// kXModeAttnMerge load: the lane's 4 activations x[k..k+3] (one head, four
-// consecutive dims) merged from all attention chunks of the head with an
-// online softmax rescale.  Chunk 0 always holds position 0; chunks past the
-// sequence carry (m = -inf, l = 0, o = 0) and weigh 0.  The loads do not
-// depend on each other or on the position, so they overlap.
-__device__ __forceinline__ void load_x4_attn(const GemvArgs &a, int k0, int lane, float &x0, float &x1, float &x2,
-                                             float &x3) {
-  const int k = k0 + 4 * lane;
-  x0 = x1 = x2 = x3 = 0.0f;
-  if (k >= a.cols) return;
-  const int hd = 1 << a.ahd_shift, stride = hd + 4;   // (m, l, -, -, o[hd]): 16-byte aligned rows
-  const int head = k >> a.ahd_shift, d = k & (hd - 1);
-  const float *ph = a.x + size_t(head) * a.achunks * stride;
-  float M = ph[0], L = ph[1];
-  float4 o = *reinterpret_cast<const float4 *>(ph + 4 + d);
-#pragma unroll 8
-  for (int c = 1; c < a.achunks; ++c) {
-    const float *q = ph + size_t(c) * stride;
-    const float m = q[0], l = q[1];
-    const float4 v = *reinterpret_cast<const float4 *>(q + 4 + d);
-    const float Mn = fmaxf(M, m);
-    const float r = expf(M - Mn), w = m == -INFINITY ? 0.0f : expf(m - Mn);
-    L = L * r + w * l;
-    o.x = o.x * r + w * v.x; o.y = o.y * r + w * v.y;
-    o.z = o.z * r + w * v.z; o.w = o.w * r + w * v.w;
-    M = Mn;
-  }
-  const float inv = 1.0f / L;
-  x0 = o.x * inv; x1 = o.y * inv; x2 = o.z * inv; x3 = o.w * inv;
-}
-
 // Second operand of the fused activation transform for the lane's 4
 // activations at k0 + 4*lane: the norm weights (kXModeRmsNorm) or the up
 // half of a gate|up vector (kXModeSiluMul).  Other modes load x[0..3] in
@@ -408,10 +377,7 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_kernel(GemvArgs a, int
 #pragma unroll
   for (int j = 0; j < XJ; ++j) {
     const int c2 = min(wave + j * WAVES, C2 - 1);
-    if (a.xmode == kXModeAttnMerge)
-      load_x4_attn(a, k0 + c2 * kRotChunk, lane, xv[j][0], xv[j][1], xv[j][2], xv[j][3]);
-    else
-      load_x4(a.x, k0 + c2 * kRotChunk, a.cols, lane, xv[j][0], xv[j][1], xv[j][2], xv[j][3]);
+    load_x4(a.x, k0 + c2 * kRotChunk, a.cols, lane, xv[j][0], xv[j][1], xv[j][2], xv[j][3]);
   }
   if (a.xmode == kXModeRmsNorm || a.xmode == kXModeSiluMul) {
 #pragma unroll
@@ -653,14 +619,6 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_fullk_kernel(GemvArgs 
   // Lanes 0-31 / 32-63 hold the first / second 128-chunk of a 256-chunk; a
   // lane's values count (norm, tables) only where the wave owns that chunk,
   // which partitions x exactly, so the norm needs no second read of x.
-  // The attention merge (its own dependent loads) runs after the weight
-  // loads are issued, so the plain path has no branch between its loads; it
-  // replaces the raw x (zero past cols, like the mask applied below).
-  if (a.xmode == kXModeAttnMerge) {
-#pragma unroll
-    for (int j = 0; j < XJ; ++j)
-      load_x4_attn(a, min(c2base + j, C2n - 1) * kRotChunk, lane, xr[j].x, xr[j].y, xr[j].z, xr[j].w);
-  }
   float inv_rms = 1.0f;
   if (a.xmode == kXModeRmsNorm) {
     float ss = 0.0f;
@@ -838,7 +796,7 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_plain_kernel(GemvArgs 
 #pragma unroll
   for (int j = 0; j < XJ; ++j) {
     const int k = min(min(c2base + j, C2n - 1) * kRotChunk + 4 * lane, a.cols - 4);
-    if constexpr (XM != kXModeAttnMerge) xr[j] = *reinterpret_cast<const float4 *>(a.x + k);
+    xr[j] = *reinterpret_cast<const float4 *>(a.x + k);
     // norm weight, or the up half of a gate|up vector
     if constexpr (AUX) xa[j] = *reinterpret_cast<const float4 *>((XM == kXModeRmsNorm ? a.xw : a.x + a.cols) + k);
   }
@@ -865,12 +823,6 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_plain_kernel(GemvArgs 
   }
   __builtin_amdgcn_sched_barrier(0);
 
-  // The attention merge (its own dependent loads) after the weight loads.
-  if constexpr (XM == kXModeAttnMerge) {
-#pragma unroll
-    for (int j = 0; j < XJ; ++j)
-      load_x4_attn(a, min(c2base + j, C2n - 1) * kRotChunk, lane, xr[j].x, xr[j].y, xr[j].z, xr[j].w);
-  }
   // RMSNorm: the waves' 256-chunks partition x, so the sum of squares over
   // them (zero past cols) is the norm's, summed in the same order in every
   // workgroup (norm.cpp:18-34).
@@ -1121,7 +1073,6 @@ static int launch_plain_cfg(const GemvArgs &a, hipStream_t st) {
         switch (a.xmode) {
         case kXModeRmsNorm: return launch_plain_kernel<FMT, false, WAVES, H, CPS, kXModeRmsNorm>(a, st);
         case kXModeSiluMul: return launch_plain_kernel<FMT, false, WAVES, H, CPS, kXModeSiluMul>(a, st);
-        case kXModeAttnMerge: return launch_plain_kernel<FMT, false, WAVES, H, CPS, kXModeAttnMerge>(a, st);
         }
       }
     }
