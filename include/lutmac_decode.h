@@ -64,6 +64,14 @@ typedef struct lmx_decoder lmx_decoder;
 /* Allocates the device state (activations, KV cache, token buffer) on the
  * current device. */
 int lmx_decoder_create(const lmx_decoder_config *cfg, lmx_decoder **out);
+/* A decoder of `batch` (1..64) sequences decoded in lockstep at one shared
+ * position, each with its own KV cache (no counterpart in the reference,
+ * whose Model::forward takes one token; it extends inference.cpp's loop to
+ * several sequences so the linears read their weights once per step for
+ * all of them).  Every token array of the calls below is then [batch][n]
+ * row-major and the logits of lmx_decoder_step [batch][vocab].  batch 1 is
+ * lmx_decoder_create. */
+int lmx_decoder_create_batched(const lmx_decoder_config *cfg, size_t batch, lmx_decoder **out);
 int lmx_decoder_destroy(lmx_decoder *d);
 /* Layer weights (borrowed handles) and norm weights (host, copied);
  * qkv_bias (host, n_heads*hd + 2*n_kv*hd floats) may be NULL. */

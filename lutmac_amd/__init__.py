@@ -38,7 +38,7 @@ EXPORTS = [
     "lmx_host_gemv", "lmx_host_lut_linear", "lmx_host_apply_hadamard_rotation",
     "lmx_host_precompute_luts",
     # include/lutmac_decode.h
-    "lmx_decoder_create", "lmx_decoder_destroy", "lmx_decoder_set_layer", "lmx_decoder_set_head",
+    "lmx_decoder_create", "lmx_decoder_create_batched", "lmx_decoder_destroy", "lmx_decoder_set_layer", "lmx_decoder_set_head",
     "lmx_decoder_reset", "lmx_decoder_step", "lmx_decoder_tokens", "lmx_decoder_generate",
     # include/lutmac_synth.h
     "lmx_quantize_int4", "lmx_synth_int4_normal", "lmx_synth_normal",
@@ -105,6 +105,7 @@ _SIGS = {
     "lmx_model_decoder": ([_p], _p),
     "lmx_model_weight_format": ([_p, _i, _i, ctypes.POINTER(_i)], _i),
     "lmx_decoder_create": ([ctypes.POINTER(DecoderConfigC), ctypes.POINTER(_p)], _i),
+    "lmx_decoder_create_batched": ([ctypes.POINTER(DecoderConfigC), _sz, ctypes.POINTER(_p)], _i),
     "lmx_decoder_destroy": ([_p], _i),
     "lmx_decoder_set_layer": ([_p, _sz, _p, _p, _p, _p, _p, _p, _p], _i),
     "lmx_decoder_set_head": ([_p, _p, _p, _p], _i),

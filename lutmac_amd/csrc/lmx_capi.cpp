@@ -239,6 +239,7 @@ int gemv_batched(lmx_weight *w, GemvArgs a, const float *x, float *y, size_t bat
   *done = 0;
   if (!w->batched || batch < 4 || reinterpret_cast<size_t>(x) % 16 || w->cols % 4) return LMX_OK;
   const size_t splits = w->Kp / kRotChunk;
+  const float *resid = a.resid;   // [batch][rows] residual rows, offset with the vectors
   while (batch - *done >= 4) {
     const size_t left = batch - *done;
     const int nb = left >= 16 ? 16 : left >= 8 ? 8 : 4;
@@ -253,6 +254,7 @@ int gemv_batched(lmx_weight *w, GemvArgs a, const float *x, float *y, size_t bat
     }
     a.x = x + *done * w->cols;
     a.y = y + *done * w->rows;
+    a.resid = resid ? resid + *done * w->rows : nullptr;
     a.cols = int(w->cols);
     a.partials = w->d_bpartials;
     int st = launch_gemv_batch(w->format, a, nb, stream);

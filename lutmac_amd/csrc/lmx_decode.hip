@@ -76,11 +76,13 @@ template <int FMT>
 __global__ __launch_bounds__(256) void embed_kernel(const uint8_t *__restrict__ planes, const float *__restrict__ scales,
                                                     int Npad, int rows, int n_groups, int group_chunks, int cols,
                                                     const int *__restrict__ tokens, const int *__restrict__ pos,
-                                                    float *__restrict__ out) {
+                                                    float *__restrict__ out, int tstride) {
   constexpr int P = EmbFmt<FMT>::P, S = EmbFmt<FMT>::S;
   const int k = blockIdx.x * 256 + threadIdx.x;
   if (k >= cols) return;
-  const int t = min(max(tokens[*pos], 0), rows - 1);
+  // sequence blockIdx.y: its tokens at tokens[y * tstride], its row at out[y * cols]
+  out += size_t(blockIdx.y) * cols;
+  const int t = min(max(tokens[size_t(blockIdx.y) * tstride + *pos], 0), rows - 1);
   const int c = k / kChunk, byte = (k % kChunk) / 8, bit = 7 - k % 8;
   int b[P];
 #pragma unroll
@@ -103,6 +105,69 @@ __device__ __forceinline__ void rope_pair(const float *in, float *out, const flo
     const float a0 = in[d], a1 = in[d + HALF];
     out[d] = a0 * cs - a1 * sn;
     out[d + HALF] = a0 * sn + a1 * cs;
+  }
+}
+
+// Batched decode helpers (one workgroup per sequence row).
+// y[b] = x[b] * inv_rms(x[b]) * w, inv_rms = 1/sqrt(sum x^2 / n + eps)
+// (norm.cpp:18-34).
+__global__ __launch_bounds__(256) void rmsnorm_rows_kernel(const float *__restrict__ x, const float *__restrict__ w,
+                                                           int n, float eps, float *__restrict__ y) {
+  __shared__ float red[4];
+  x += size_t(blockIdx.x) * n;
+  y += size_t(blockIdx.x) * n;
+  float s = 0.0f;
+  for (int k = threadIdx.x; k < n; k += 256) s += x[k] * x[k];
+  s = lane_sum<32>(s, threadIdx.x & (kWave - 1));
+  if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = s;
+  __syncthreads();
+  const float inv = 1.0f / sqrtf(((red[0] + red[1]) + (red[2] + red[3])) / float(n) + eps);
+  for (int k = threadIdx.x; k < n; k += 256) y[k] = x[k] * inv * w[k];
+}
+
+// act[b][k] = silu(gu[b][k]) * gu[b][ffn + k] (model.cpp:36, 413-416).
+__global__ __launch_bounds__(256) void silu_mul_rows_kernel(const float *__restrict__ gu, int ffn,
+                                                            float *__restrict__ act) {
+  const int k = blockIdx.x * 256 + threadIdx.x;
+  if (k >= ffn) return;
+  const float *g = gu + size_t(blockIdx.y) * 2 * ffn;
+  const float a = g[k];
+  act[size_t(blockIdx.y) * ffn + k] = a / (1.0f + expf(-a)) * g[ffn + k];
+}
+
+// Greedy token of every sequence: the first maximum of its logits row
+// (model.cpp:480-490); written unless the next position is forced.  The last
+// workgroup to finish (a ticket) advances the shared position.
+__global__ __launch_bounds__(1024) void argmax_rows_kernel(const float *__restrict__ logits, int vocab,
+                                                           int *__restrict__ tokens, int tstride,
+                                                           int *__restrict__ pos_p, int n_forced, int max_pos,
+                                                           unsigned *__restrict__ ticket_p) {
+  __shared__ unsigned long long best[16];
+  __shared__ unsigned ticket;
+  const float *lg = logits + size_t(blockIdx.x) * vocab;
+  unsigned long long key = 0;
+  for (int i = threadIdx.x; i < vocab; i += 1024) {
+    const float v = lg[i];
+    if (__builtin_isnan(v)) continue;
+    uint32_t u = __float_as_uint(v + 0.0f);
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    const unsigned long long k = (static_cast<unsigned long long>(u) << 32) | (0xFFFFFFFFu - uint32_t(i));
+    key = k > key ? k : key;
+  }
+  key = wave_max_key(key, threadIdx.x & (kWave - 1));
+  if ((threadIdx.x & (kWave - 1)) == 0) best[threadIdx.x / kWave] = key;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < 16; ++w) key = best[w] > key ? best[w] : key;
+    const int idx = key ? int(0xFFFFFFFFu - uint32_t(key)) : 0;
+    const int pos = *pos_p;
+    if (pos + 1 >= n_forced && pos + 1 <= max_pos) tokens[size_t(blockIdx.x) * tstride + pos + 1] = idx;
+    __builtin_amdgcn_s_waitcnt(0);
+    ticket = __hip_atomic_fetch_add(ticket_p, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (ticket == gridDim.x - 1) {   // every workgroup has read the position
+      *pos_p = pos + 1;
+      __hip_atomic_store(ticket_p, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
   }
 }
 
@@ -188,7 +253,8 @@ __global__ __launch_bounds__(512) void attn_kernel(const float *__restrict__ qkv
                                                    const float *__restrict__ freq, float pos_div, int n_heads,
                                                    int n_kv, int group, int max_seq, float scale,
                                                    float *__restrict__ part, int n_chunks,
-                                                   unsigned *__restrict__ tickets, float *__restrict__ out) {
+                                                   unsigned *__restrict__ tickets, float *__restrict__ out,
+                                                   size_t qkv_stride, size_t kv_stride) {
   constexpr int VD = HD / kWave;          // value columns per lane
   constexpr int NT = 512;
   constexpr int KV4 = kAttnChunk * HD / 4 / NT;   // float4 of K (and of V) per thread
@@ -199,6 +265,17 @@ __global__ __launch_bounds__(512) void attn_kernel(const float *__restrict__ qkv
   __shared__ float pw[8][kAttnChunk];
   __shared__ float knew[HD];
   __shared__ unsigned ticket;
+  {
+    // sequence blockIdx.y of a batch: its q|k|v row, KV cache, partials,
+    // tickets and output (the position is shared)
+    const size_t b = blockIdx.y;
+    qkv += b * qkv_stride;
+    kc += b * kv_stride;
+    vc += b * kv_stride;
+    part += b * size_t(n_heads) * n_chunks * (HD + 4);
+    tickets += b * n_kv;
+    out += b * size_t(n_heads) * HD;
+  }
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
   const int kvh = blockIdx.x % n_kv, chunk = blockIdx.x / n_kv;
   const size_t row = size_t(n_kv) * HD;
@@ -360,6 +437,7 @@ using namespace lmx;
 struct lmx_decoder {
   lmx_decoder_config cfg{};
   int device = 0;
+  size_t batch = 1;   // sequences decoded in lockstep (every per-sequence buffer is [batch][...])
   struct Layer {
     const lmx_weight *qkv = nullptr, *o = nullptr, *gate_up = nullptr, *down = nullptr;
     float *in_norm = nullptr, *post_norm = nullptr, *qkv_bias = nullptr;
@@ -372,6 +450,9 @@ struct lmx_decoder {
   float *attn_part = nullptr;            // [n_heads][chunks][m, l, -, -, o[head_dim]]
   float *attn_out = nullptr;             // [n_heads * head_dim] merged attention output
   unsigned *attn_tickets = nullptr;      // [n_kv_heads] chunk tickets (zero between steps)
+  float *normed = nullptr, *act = nullptr;   // batch > 1: RMSNorm output [hidden], SiLU*up [ffn] rows
+  unsigned *argmax_ticket = nullptr;         // batch > 1: argmax_rows_kernel's ticket
+  size_t kv_seq = 0;                         // floats of one sequence's K (or V) cache, all layers
   unsigned long long *amax = nullptr;    // per-wave argmax keys of the head GEMV
   size_t amax_slots = 0;
   int *tokens = nullptr, *pos = nullptr;
@@ -412,21 +493,24 @@ int gemv(const lmx_weight *w, const float *x, float *y, const float *bias, int x
 
 
 template <int FMT>
-void launch_embed(const lmx_weight *w, const int *tokens, const int *pos, float *out, hipStream_t st) {
-  embed_kernel<FMT><<<dim3(unsigned((w->cols + 255) / 256)), dim3(256), 0, st>>>(
+void launch_embed(const lmx_weight *w, const int *tokens, const int *pos, float *out, size_t batch, int tstride,
+                  hipStream_t st) {
+  embed_kernel<FMT><<<dim3(unsigned((w->cols + 255) / 256), unsigned(batch)), dim3(256), 0, st>>>(
       static_cast<const uint8_t *>(w->d_planes), w->d_scales, int(w->Npad), int(w->rows), int(w->n_groups),
-      int(w->group / kChunk), int(w->cols), tokens, pos, out);
+      int(w->group / kChunk), int(w->cols), tokens, pos, out, tstride);
 }
 
-int embed(const lmx_weight *w, const int *tokens, const int *pos, float *out, hipStream_t st) {
+// Embedding rows of `batch` sequences (tokens of sequence b at tokens[b * tstride]).
+int embed(const lmx_weight *w, const int *tokens, const int *pos, float *out, size_t batch, int tstride,
+          hipStream_t st) {
   switch (w->format) {
-  case LMX_FMT_TERNARY: launch_embed<LMX_FMT_TERNARY>(w, tokens, pos, out, st); break;
-  case LMX_FMT_BINARY: launch_embed<LMX_FMT_BINARY>(w, tokens, pos, out, st); break;
-  case LMX_FMT_RRQ2: launch_embed<LMX_FMT_RRQ2>(w, tokens, pos, out, st); break;
-  case LMX_FMT_RRQ3: launch_embed<LMX_FMT_RRQ3>(w, tokens, pos, out, st); break;
-  case LMX_FMT_INT3: launch_embed<LMX_FMT_INT3>(w, tokens, pos, out, st); break;
-  case LMX_FMT_INT4: launch_embed<LMX_FMT_INT4>(w, tokens, pos, out, st); break;
-  case LMX_FMT_INT8: launch_embed<LMX_FMT_INT8>(w, tokens, pos, out, st); break;
+  case LMX_FMT_TERNARY: launch_embed<LMX_FMT_TERNARY>(w, tokens, pos, out, batch, tstride, st); break;
+  case LMX_FMT_BINARY: launch_embed<LMX_FMT_BINARY>(w, tokens, pos, out, batch, tstride, st); break;
+  case LMX_FMT_RRQ2: launch_embed<LMX_FMT_RRQ2>(w, tokens, pos, out, batch, tstride, st); break;
+  case LMX_FMT_RRQ3: launch_embed<LMX_FMT_RRQ3>(w, tokens, pos, out, batch, tstride, st); break;
+  case LMX_FMT_INT3: launch_embed<LMX_FMT_INT3>(w, tokens, pos, out, batch, tstride, st); break;
+  case LMX_FMT_INT4: launch_embed<LMX_FMT_INT4>(w, tokens, pos, out, batch, tstride, st); break;
+  case LMX_FMT_INT8: launch_embed<LMX_FMT_INT8>(w, tokens, pos, out, batch, tstride, st); break;
   default: return fail(LMX_ERR_UNSUPPORTED_FORMAT, "embedding format %d", w->format);
   }
   return launch_err("embed");
@@ -439,15 +523,16 @@ int attention(lmx_decoder *d, size_t layer, hipStream_t st) {
   const size_t per_layer = size_t(nch) * kAttnChunk * c.n_kv_heads * c.head_dim;
   float *kc = d->kcache + layer * per_layer, *vc = d->vcache + layer * per_layer;
   const float scale = 1.0f / std::sqrt(float(c.head_dim));   // model.cpp:337
-  const dim3 grid(unsigned(c.n_kv_heads * nch));
+  const dim3 grid(unsigned(c.n_kv_heads * nch), unsigned(d->batch));
+  const size_t qkv_stride = (c.n_heads + 2 * c.n_kv_heads) * c.head_dim;
   if (c.head_dim == 64)
     attn_kernel<64><<<grid, dim3(512), 0, st>>>(d->qkv, kc, vc, d->pos, d->freq, d->pos_div, int(c.n_heads),
                                                 int(c.n_kv_heads), group, int(c.max_seq), scale, d->attn_part, nch,
-                                                d->attn_tickets, d->attn_out);
+                                                d->attn_tickets, d->attn_out, qkv_stride, d->kv_seq);
   else
     attn_kernel<128><<<grid, dim3(512), 0, st>>>(d->qkv, kc, vc, d->pos, d->freq, d->pos_div, int(c.n_heads),
                                                  int(c.n_kv_heads), group, int(c.max_seq), scale, d->attn_part, nch,
-                                                 d->attn_tickets, d->attn_out);
+                                                 d->attn_tickets, d->attn_out, qkv_stride, d->kv_seq);
   return launch_err("attention");
 }
 
@@ -466,9 +551,70 @@ int upload(lmx_decoder *d, float **dst, const float *src, size_t n) {
   return e == hipSuccess ? LMX_OK : hip_err(e, "hipMemcpy (decoder weights)");
 }
 
-int step(lmx_decoder *d, float *logits_out, hipStream_t st) {
+// y[b] = W x[b] (+ bias) (+ resid[b]) for the decoder's `batch` rows: groups
+// of 16/8/4 through the batched kernel (weights read once per group), the
+// rest one GEMV per row (the residual then rides as that row's bias).
+int gemv_rows(const lmx_decoder *d, const lmx_weight *w, const float *x, float *y, const float *bias,
+              const float *resid, hipStream_t st) {
+  GemvArgs a = weight_args(w);
+  a.rotate = rotates(w->format) ? LMX_ROTATE_FWHT256 : LMX_ROTATE_NONE;
+  a.bias = bias;
+  a.resid = resid;
+  size_t done = 0;
+  int r = gemv_batched(const_cast<lmx_weight *>(w), a, x, y, d->batch, st, &done);
+  if (r) return r;
+  a.resid = nullptr;
+  for (size_t b = done; b < d->batch; ++b) {
+    a.x = x + b * w->cols;
+    a.y = y + b * w->rows;
+    a.partials = w->d_partials;
+    if (resid) a.bias = resid + b * w->rows;   // decoder rows never carry both
+    if ((r = launch_gemv(w->format, a, st))) return r;
+  }
+  return LMX_OK;
+}
+
+int rmsnorm_rows(const lmx_decoder *d, const float *x, const float *wt, float *y, hipStream_t st) {
+  rmsnorm_rows_kernel<<<dim3(unsigned(d->batch)), dim3(256), 0, st>>>(x, wt, int(d->cfg.hidden), d->cfg.rms_eps, y);
+  return launch_err("rmsnorm_rows");
+}
+
+// One token step of `batch` sequences in lockstep: every linear reads its
+// weights once per group of sequences; the norms and SiLU*up run as row
+// kernels (the batched GEMV splits K, so it cannot fuse them), attention and
+// argmax per sequence.
+int step_batched(lmx_decoder *d, float *logits_out, hipStream_t st) {
   const lmx_decoder_config &c = d->cfg;
-  int r = embed(d->embed, d->tokens, d->pos, d->hidden, st);
+  const size_t B = d->batch;
+  int r = embed(d->embed, d->tokens, d->pos, d->hidden, B, int(c.max_seq + 1), st);
+  if (r) return r;
+  for (size_t l = 0; l < c.n_layers; ++l) {
+    const lmx_decoder::Layer &L = d->layers[l];
+    if ((r = rmsnorm_rows(d, d->hidden, L.in_norm, d->normed, st)) ||
+        (r = gemv_rows(d, L.qkv, d->normed, d->qkv, L.qkv_bias, nullptr, st)) ||
+        (r = attention(d, l, st)) ||
+        (r = gemv_rows(d, L.o, d->attn_out, d->hidden, nullptr, d->hidden, st)) ||
+        (r = rmsnorm_rows(d, d->hidden, L.post_norm, d->normed, st)) ||
+        (r = gemv_rows(d, L.gate_up, d->normed, d->gate_up, nullptr, nullptr, st)))
+      return r;
+    silu_mul_rows_kernel<<<dim3(unsigned((c.ffn + 255) / 256), unsigned(B)), dim3(256), 0, st>>>(d->gate_up,
+                                                                                                int(c.ffn), d->act);
+    if ((r = launch_err("silu_mul_rows")) || (r = gemv_rows(d, L.down, d->act, d->hidden, nullptr, d->hidden, st)))
+      return r;
+  }
+  float *lg = logits_out ? logits_out : d->logits;
+  if ((r = rmsnorm_rows(d, d->hidden, d->final_norm, d->normed, st)) ||
+      (r = gemv_rows(d, d->head, d->normed, lg, nullptr, nullptr, st)))
+    return r;
+  argmax_rows_kernel<<<dim3(unsigned(B)), dim3(1024), 0, st>>>(lg, int(c.vocab), d->tokens, int(c.max_seq + 1),
+                                                               d->pos, d->n_forced, int(c.max_seq), d->argmax_ticket);
+  return launch_err("argmax_rows");
+}
+
+int step(lmx_decoder *d, float *logits_out, hipStream_t st) {
+  if (d->batch > 1) return step_batched(d, logits_out, st);
+  const lmx_decoder_config &c = d->cfg;
+  int r = embed(d->embed, d->tokens, d->pos, d->hidden, 1, int(c.max_seq + 1), st);
   if (r) return r;
   for (size_t l = 0; l < c.n_layers; ++l) {
     const lmx_decoder::Layer &L = d->layers[l];
@@ -494,13 +640,15 @@ int ready(const lmx_decoder *d) {
   return LMX_OK;
 }
 
+// tokens: [batch][n], row b the first n tokens of sequence b.
 int set_position(lmx_decoder *d, const int32_t *tokens, size_t n, hipStream_t st) {
   if (n == 0 || n > d->cfg.max_seq) return fail(LMX_ERR_INVALID_ARGUMENT, "%zu tokens for max_seq %zu", n, d->cfg.max_seq);
-  for (size_t i = 0; i < n; ++i)
+  for (size_t i = 0; i < n * d->batch; ++i)
     if (tokens[i] < 0 || size_t(tokens[i]) >= d->cfg.vocab)
       return fail(LMX_ERR_INVALID_ARGUMENT, "token %d at %zu outside the vocabulary", tokens[i], i);
   const int zero = 0;
-  hipError_t e = hipMemcpyAsync(d->tokens, tokens, n * sizeof(int32_t), hipMemcpyHostToDevice, st);
+  hipError_t e = hipMemcpy2DAsync(d->tokens, (d->cfg.max_seq + 1) * sizeof(int32_t), tokens, n * sizeof(int32_t),
+                                  n * sizeof(int32_t), d->batch, hipMemcpyHostToDevice, st);
   if (e == hipSuccess) e = hipMemcpyAsync(d->pos, &zero, sizeof(int), hipMemcpyHostToDevice, st);
   if (e == hipSuccess) e = hipStreamSynchronize(st);
   if (e != hipSuccess) return hip_err(e, "decoder reset");
@@ -514,7 +662,12 @@ int set_position(lmx_decoder *d, const int32_t *tokens, size_t n, hipStream_t st
 extern "C" {
 
 int lmx_decoder_create(const lmx_decoder_config *cfg, lmx_decoder **out) {
+  return lmx_decoder_create_batched(cfg, 1, out);
+}
+
+int lmx_decoder_create_batched(const lmx_decoder_config *cfg, size_t batch, lmx_decoder **out) {
   if (!cfg || !out) return fail(LMX_ERR_INVALID_ARGUMENT, "NULL argument");
+  if (batch == 0 || batch > 64) return fail(LMX_ERR_INVALID_ARGUMENT, "batch %zu outside 1..64", batch);
   *out = nullptr;
   const lmx_decoder_config &c = *cfg;
   if (!c.hidden || !c.n_layers || !c.n_heads || !c.n_kv_heads || !c.ffn || !c.vocab || !c.max_seq)
@@ -539,24 +692,30 @@ int lmx_decoder_create(const lmx_decoder_config *cfg, lmx_decoder **out) {
   if (!d) return fail(LMX_ERR_OUT_OF_MEMORY, "decoder allocation");
   d->cfg = c;
   d->device = dev;
+  d->batch = batch;
   d->layers.resize(c.n_layers);
   d->pos_div = c.rope_mode == LMX_ROPE_REFERENCE ? c.rope_factor : 1.0f;
   const size_t qkv_rows = (c.n_heads + 2 * c.n_kv_heads) * c.head_dim;
   const size_t kv = c.n_layers * attn_chunks(c) * kAttnChunk * c.n_kv_heads * c.head_dim;   // whole chunks
+  d->kv_seq = kv;
+  const size_t B = batch;
   const std::vector<float> fr = rope_freqs(c);
   int st;
-  if ((st = d->alloc(reinterpret_cast<void **>(&d->hidden), c.hidden * 4)) ||
-      (st = d->alloc(reinterpret_cast<void **>(&d->qkv), qkv_rows * 4)) ||
-      (st = d->alloc(reinterpret_cast<void **>(&d->gate_up), 2 * c.ffn * 4)) ||
-      (st = d->alloc(reinterpret_cast<void **>(&d->logits), c.vocab * 4)) ||
-      (st = d->alloc(reinterpret_cast<void **>(&d->kcache), kv * 4)) ||
-      (st = d->alloc(reinterpret_cast<void **>(&d->vcache), kv * 4)) ||
-      (st = d->alloc(reinterpret_cast<void **>(&d->tokens), (c.max_seq + 1) * 4)) ||
+  if ((st = d->alloc(reinterpret_cast<void **>(&d->hidden), B * c.hidden * 4)) ||
+      (st = d->alloc(reinterpret_cast<void **>(&d->qkv), B * qkv_rows * 4)) ||
+      (st = d->alloc(reinterpret_cast<void **>(&d->gate_up), B * 2 * c.ffn * 4)) ||
+      (st = d->alloc(reinterpret_cast<void **>(&d->logits), B * c.vocab * 4)) ||
+      (st = d->alloc(reinterpret_cast<void **>(&d->kcache), B * kv * 4)) ||
+      (st = d->alloc(reinterpret_cast<void **>(&d->vcache), B * kv * 4)) ||
+      (st = d->alloc(reinterpret_cast<void **>(&d->tokens), B * (c.max_seq + 1) * 4)) ||
       (st = d->alloc(reinterpret_cast<void **>(&d->pos), 4)) ||
       (st = d->alloc(reinterpret_cast<void **>(&d->attn_part),
-                     c.n_heads * attn_chunks(c) * (c.head_dim + 4) * sizeof(float))) ||
-      (st = d->alloc(reinterpret_cast<void **>(&d->attn_out), c.n_heads * c.head_dim * sizeof(float))) ||
-      (st = d->alloc(reinterpret_cast<void **>(&d->attn_tickets), c.n_kv_heads * sizeof(unsigned))) ||
+                     B * c.n_heads * attn_chunks(c) * (c.head_dim + 4) * sizeof(float))) ||
+      (st = d->alloc(reinterpret_cast<void **>(&d->attn_out), B * c.n_heads * c.head_dim * sizeof(float))) ||
+      (st = d->alloc(reinterpret_cast<void **>(&d->attn_tickets), B * c.n_kv_heads * sizeof(unsigned))) ||
+      (B > 1 && (st = d->alloc(reinterpret_cast<void **>(&d->normed), B * c.hidden * 4))) ||
+      (B > 1 && (st = d->alloc(reinterpret_cast<void **>(&d->act), B * c.ffn * 4))) ||
+      (B > 1 && (st = d->alloc(reinterpret_cast<void **>(&d->argmax_ticket), sizeof(unsigned)))) ||
       (st = upload(d, &d->freq, fr.data(), fr.size()))) {
     delete d;
     return st;
@@ -638,7 +797,8 @@ int lmx_decoder_tokens(lmx_decoder *d, int32_t *out, size_t n, void *stream) {
   if (!d || !out) return fail(LMX_ERR_INVALID_ARGUMENT, "NULL argument");
   if (n > d->cfg.max_seq + 1) return fail(LMX_ERR_INVALID_ARGUMENT, "n %zu > max_seq + 1", n);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  hipError_t e = hipMemcpyAsync(out, d->tokens, n * sizeof(int32_t), hipMemcpyDeviceToHost, st);
+  hipError_t e = hipMemcpy2DAsync(out, n * sizeof(int32_t), d->tokens, (d->cfg.max_seq + 1) * sizeof(int32_t),
+                                  n * sizeof(int32_t), d->batch, hipMemcpyDeviceToHost, st);
   if (e == hipSuccess) e = hipStreamSynchronize(st);
   return e == hipSuccess ? LMX_OK : hip_err(e, "decoder tokens");
 }
@@ -695,7 +855,8 @@ int lmx_decoder_generate(lmx_decoder *d, const int32_t *prompt, size_t n_prompt,
   if (e == hipSuccess) e = hipEventElapsedTime(&t0, ev[0], ev[1]);
   if (e == hipSuccess) e = hipEventElapsedTime(&t1, ev[1], ev[2]);
   if (e == hipSuccess)
-    e = hipMemcpy(out_tokens, d->tokens, (n_prompt + n_new) * sizeof(int32_t), hipMemcpyDeviceToHost);
+    e = hipMemcpy2D(out_tokens, (n_prompt + n_new) * sizeof(int32_t), d->tokens, (d->cfg.max_seq + 1) * sizeof(int32_t),
+                    (n_prompt + n_new) * sizeof(int32_t), d->batch, hipMemcpyDeviceToHost);
   for (auto &x : ev)
     if (x) (void)hipEventDestroy(x);
   (void)hipGraphExecDestroy(exec);

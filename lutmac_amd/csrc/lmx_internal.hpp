@@ -48,6 +48,7 @@ struct GemvArgs {
   const float *x;          // [cols]
   float *y;                // [rows]
   const float *bias;       // [rows] or null
+  const float *resid;      // batched kernel: [batch][rows] added to y (may alias y), or null
   float *partials;         // [splits][Npad]
   unsigned *counters;      // [row_blocks]
   int rows, Npad, cols, Kp;
@@ -173,4 +174,8 @@ struct lmx_weight {
 namespace lmx {
 // Kernel arguments of a handle (x, y, bias, rotation and transform unset).
 GemvArgs weight_args(const lmx_weight *w);
+// Vectors x[0..batch) in groups of 16/8/4 through the batched kernel (a.bias
+// per row, a.resid per vector row); *done = the vectors it covered (none
+// below 4).  Grows the handle's batched scratch on first use.
+int gemv_batched(lmx_weight *w, GemvArgs a, const float *x, float *y, size_t batch, void *stream, size_t *done);
 }  // namespace lmx

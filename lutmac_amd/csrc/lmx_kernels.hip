@@ -1305,16 +1305,20 @@ __global__ __launch_bounds__(256) void lut_gemv_batch_kernel(GemvArgs a, int row
   for (int n = 0; n < NB; ++n) a.partials[(size_t(n) * splits + split) * a.Npad + row] = acc[n];
 }
 
-// y[n*rows + r] = sum_s partials[n][s][r] (+ bias[r]) in split order.
+// y[n*rows + r] = sum_s partials[n][s][r] (+ bias[r]) (+ resid[n*rows + r])
+// in split order; resid may be y itself (each element is read and written
+// by one thread).
 __global__ __launch_bounds__(64) void batched_reduce_kernel(const float *__restrict__ partials, int splits, int Npad,
                                                             int rows, const float *__restrict__ bias,
-                                                            float *__restrict__ y) {
+                                                            const float *resid, float *y) {
   const int r = blockIdx.x * kWave + threadIdx.x, n = blockIdx.y;
   if (r >= rows) return;
   const float *p = partials + size_t(n) * splits * Npad + r;
   float s = 0.0f;
   for (int k = 0; k < splits; ++k) s += p[size_t(k) * Npad];
-  y[size_t(n) * rows + r] = bias ? s + bias[r] : s;
+  if (bias) s += bias[r];
+  if (resid) s += resid[size_t(n) * rows + r];
+  y[size_t(n) * rows + r] = s;
 }
 
 template <int FMT, int NB>
@@ -1322,7 +1326,7 @@ static int launch_batch_nb(const GemvArgs &a, hipStream_t st) {
   const int row_blocks = (a.Npad + 255) / 256, splits = a.Kp / kRotChunk;
   lut_gemv_batch_kernel<FMT, NB><<<dim3(row_blocks * splits), dim3(256), 0, st>>>(a, row_blocks, splits);
   batched_reduce_kernel<<<dim3((a.rows + kWave - 1) / kWave, NB), dim3(kWave), 0, st>>>(a.partials, splits, a.Npad,
-                                                                                     a.rows, a.bias, a.y);
+                                                                                     a.rows, a.bias, a.resid, a.y);
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? LMX_OK : fail(LMX_ERR_LAUNCH_FAILED, "batched lut_gemv launch: %s", hipGetErrorString(e));
 }

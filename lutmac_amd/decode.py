@@ -132,30 +132,36 @@ class _DecoderOps:
     cfg = None
     _h = None
 
+    batch = 1
+
     def reset(self, tokens):
+        """tokens: [n], or [batch, n] for a batched decoder."""
         t = np.ascontiguousarray(tokens, np.int32)
-        check(lib().lmx_decoder_reset(self._h, _np_ptr(t), t.size))
+        check(lib().lmx_decoder_reset(self._h, _np_ptr(t), t.size // self.batch))
 
     def step(self, logits=None, stream=None):
         """One forward step at the current position; logits (device float32 tensor of
-        vocab entries) receives the step's logits when given."""
+        vocab entries, batch x vocab for a batched decoder) receives the step's logits
+        when given."""
         from . import _dev_ptr
         check(lib().lmx_decoder_step(self._h, _dev_ptr(logits), _stream_ptr(stream)))
         return logits
 
     def tokens(self, n, stream=None):
-        out = np.zeros(n, np.int32)
+        out = np.zeros((self.batch, n), np.int32)
         check(lib().lmx_decoder_tokens(self._h, _np_ptr(out), n, _stream_ptr(stream)))
-        return out
+        return out[0] if self.batch == 1 else out
 
     def generate(self, prompt, n_new, stream=None):
-        """Greedy generation; returns (tokens[n_prompt + n_new], prefill_ms, decode_ms)."""
+        """Greedy generation; prompt [n_prompt] (or [batch, n_prompt]); returns
+        (tokens[n_prompt + n_new] (or [batch, ...]), prefill_ms, decode_ms)."""
         p = np.ascontiguousarray(prompt, np.int32)
-        out = np.zeros(p.size + n_new, np.int32)
+        n_prompt = p.size // self.batch
+        out = np.zeros((self.batch, n_prompt + n_new), np.int32)
         t0, t1 = ctypes.c_float(), ctypes.c_float()
-        check(lib().lmx_decoder_generate(self._h, _np_ptr(p), p.size, n_new, _np_ptr(out),
+        check(lib().lmx_decoder_generate(self._h, _np_ptr(p), n_prompt, n_new, _np_ptr(out),
                                          ctypes.byref(t0), ctypes.byref(t1), _stream_ptr(stream)))
-        return out, t0.value, t1.value
+        return (out[0] if self.batch == 1 else out), t0.value, t1.value
 
     def __del__(self):
         try:
@@ -165,10 +171,12 @@ class _DecoderOps:
 
 
 class Decoder(_DecoderOps):
-    """Device decoder over LUT-GEMV weight handles built from a SyntheticModel."""
+    """Device decoder over LUT-GEMV weight handles built from a SyntheticModel;
+    batch > 1 decodes that many sequences in lockstep."""
 
-    def __init__(self, model):
+    def __init__(self, model, batch=1):
         self.model, self.cfg = model, model.cfg
+        self.batch = batch
         self._h = None
         self.weights = []
         self.head = None
@@ -176,7 +184,7 @@ class Decoder(_DecoderOps):
         c = self.cfg
         h = ctypes.c_void_p()
         cs = c.c_struct()
-        check(lib().lmx_decoder_create(ctypes.byref(cs), ctypes.byref(h)))
+        check(lib().lmx_decoder_create_batched(ctypes.byref(cs), batch, ctypes.byref(h)))
         self._h = h
         for i, L in enumerate(model.layers):
             ws = [Weight.from_planes(FMT_INT4, L[n][0], L[n][1], *shapes[n], model.group)

@@ -175,3 +175,61 @@ def test_lutmac_file_int8_embedding(cuda, tmp_path):
     assert ours.weight_format(-1) == L.FMT_INT8 and ours.weight_format(-2) == L.FMT_INT8
     toks = np.random.default_rng(34).integers(0, cfg.vocab, 10)
     check_against(ours, oracle.RefDecoder.from_file(path, cfg.vocab), toks)
+
+
+# ---- batched decoder: several sequences in lockstep --------------------------
+def batched_check(dec, m, toks, tol=DECODE_TOL):
+    """Teacher-forced logits of every sequence at every step against one oracle
+    decoder per sequence."""
+    B, n = toks.shape
+    dec.reset(toks)
+    lg = torch.empty(B * m.cfg.vocab, dtype=torch.float32, device="cuda")
+    refs = [oracle.OracleDecoder(m) for _ in range(B)]
+    for pos in range(n):
+        dec.step(lg)
+        got = lg.cpu().numpy().reshape(B, m.cfg.vocab)
+        for b in range(B):
+            want = refs[b].step(toks[b, pos], pos)
+            err = rel_max_err(got[b], want)
+            assert err < tol, f"sequence {b} step {pos}: rel err {err:.3e}"
+
+
+# B = 4: one group of the batched GEMV; B = 6: a group of 4 and two rows by the
+# single-vector GEMV; 70 positions cross a 64-position attention chunk.
+@pytest.mark.parametrize("batch", [4, 6])
+def test_batched_decoder_matches_oracle(cuda, batch):
+    cfg = D.small_config(max_seq=128, rope_mode=D.ROPE_LLAMA3, rope_factor=32.0, rope_orig_max_pos=64,
+                         rope_theta=10000.0)
+    m = D.SyntheticModel(cfg, seed=31, group=128, random_norms=True)
+    toks = np.random.default_rng(32).integers(0, cfg.vocab, (batch, 70))
+    batched_check(D.Decoder(m, batch=batch), m, toks)
+
+
+def test_batched_decoder_qwen_style(cuda):
+    cfg = D.small_config(hidden=512, n_heads=12, n_kv_heads=2, head_dim=128, ffn=768, vocab=1500, max_seq=128,
+                         rope_mode=D.ROPE_REFERENCE, rope_factor=1.0, rope_theta=1e6, rms_eps=1e-6,
+                         qkv_bias=True)
+    m = D.SyntheticModel(cfg, seed=33, group=128, random_norms=True)
+    toks = np.random.default_rng(34).integers(0, cfg.vocab, (4, 70))
+    batched_check(D.Decoder(m, batch=4), m, toks)
+
+
+def test_batched_generate_graph_equals_eager_and_oracle(cuda):
+    cfg = D.small_config(max_seq=96)
+    m = D.SyntheticModel(cfg, seed=35, group=128, random_norms=True)
+    B, n_prompt, n_new = 4, 8, 72
+    dec = D.Decoder(m, batch=B)
+    prompt = np.random.default_rng(36).integers(0, cfg.vocab, (B, n_prompt))
+    out, t_pre, t_dec = dec.generate(prompt, n_new)
+    assert out.shape == (B, n_prompt + n_new) and np.array_equal(out[:, :n_prompt], prompt)
+    assert t_pre > 0 and t_dec > 0
+    dec.reset(prompt)
+    for _ in range(n_prompt + n_new - 1):
+        dec.step()
+    assert np.array_equal(dec.tokens(n_prompt + n_new), out)
+    for b in range(B):   # every generated token is the oracle's argmax for its sequence
+        o = oracle.OracleDecoder(m)
+        for pos in range(n_prompt + n_new - 1):
+            lg = o.step(out[b, pos], pos)
+            if pos + 1 >= n_prompt:
+                assert lg[out[b, pos + 1]] >= lg.max() - DECODE_TOL * np.linalg.norm(lg)
