@@ -193,34 +193,44 @@ def decode_bench(n_prompt, n_new, seed=2024):
             "setup_s": round(setup_s, 1)}
 
 
-def qwen_decode_bench(context, n_new, seed=2025):
-    """BASELINE config 5 at batch 1: greedy decode of a random-init
-    Qwen-2.5-1.5B architecture (QKV bias, GQA 12/2, head_dim 128, tied
-    151936 x 1536 4-bit head) with a KV context of `context` positions: a
-    seeded prompt of context - n_new tokens prefilled token by token, then
-    n_new generated tokens, each attending over ~context positions."""
+def qwen_decode_bench(context, n_new, batches=(1, 4, 16), seed=2025):
+    """greedy decode of a random-init Qwen-2.5-1.5B
+    architecture (QKV bias, GQA 12/2, head_dim 128, tied 151936 x 1536 4-bit
+    head) with a KV context of `context` positions, at each batch size: B
+    seeded prompts of context - n_new tokens prefilled in lockstep, then n_new
+    generated tokens per sequence, each step attending over ~context
+    positions.  Per batch: step time, tokens/s per sequence and in aggregate,
+    and the HBM bytes a step reads (weights once, every sequence's KV)."""
     from lutmac_amd import decode as D
     from dataclasses import replace
     cfg = replace(D.QWEN_2_5_1_5B, max_seq=context)
     t0 = time.perf_counter()
     model = D.SyntheticModel(cfg, seed=seed, group=128)
-    dec = D.Decoder(model)
     setup_s = time.perf_counter() - t0
-    prompt = np.random.default_rng(seed + 1).integers(0, cfg.vocab, context - n_new)
-    out, pre_ms, dec_ms = dec.generate(prompt, n_new)
-    tok_s = (n_new - 1) / (dec_ms / 1e3)
-    B = decode_weight_bytes(cfg, 128)
-    kv = 2 * cfg.n_layers * cfg.kv_dim * 4 * (context - n_new / 2)
-    dec.close()
-    return {"metric": "Qwen-2.5-1.5B-arch decode tokens/s bs=1", "tokens_per_s": round(tok_s, 1),
-            "ms_per_token": round(dec_ms / (n_new - 1), 4), "kv_context": context,
+    W = decode_weight_bytes(cfg, 128)
+    kv_seq = 2 * cfg.n_layers * cfg.kv_dim * 4 * (context - n_new / 2)
+    per_batch = {}
+    for B in batches:
+        dec = D.Decoder(model, batch=B)
+        prompt = np.random.default_rng(seed + 1).integers(0, cfg.vocab, (B, context - n_new))
+        out, pre_ms, dec_ms = dec.generate(prompt if B > 1 else prompt[0], n_new)
+        dec.close()
+        step_ms = dec_ms / (n_new - 1)
+        per_batch[str(B)] = {"ms_per_step": round(step_ms, 4),
+                             "tokens_per_s_per_sequence": round(1e3 / step_ms, 1),
+                             "tokens_per_s_aggregate": round(B * 1e3 / step_ms, 1),
+                             "prefill_ms": round(pre_ms, 1),
+                             "step_bytes": int(W + B * kv_seq),
+                             "achieved_GB_s": round((W + B * kv_seq) / step_ms / 1e6, 1)}
+    return {"metric": "Qwen-2.5-1.5B-arch decode tokens/s bs=1/4/16, KV context " + str(context),
+            "tokens_per_s": per_batch[str(batches[0])]["tokens_per_s_per_sequence"],
+            "ms_per_token": per_batch[str(batches[0])]["ms_per_step"], "kv_context": context,
             "prefill_tokens": context - n_new, "n_new": n_new,
-            "weight_bytes_per_token": B, "kv_bytes_per_token_mean": int(kv),
-            "achieved_GB_s": round((B + kv) * tok_s / 1e9, 1),
-            "frac_of_peak": round((B + kv) * tok_s / 1e9 / HBM_PEAK_GBPS, 4),
+            "weight_bytes_per_step": W, "kv_bytes_per_sequence_step_mean": int(kv_seq),
+            "per_batch": per_batch,
             "config": {"workload": "Qwen-2.5-1.5B architecture, random-init N(0,0.02) weights, 4-bit per-128-group "
-                                   "linears, QKV bias, tied 4-bit embedding/head, greedy, batch 1 (BASELINE config 5; "
-                                   "batch 4/16 in batched_qwen_linears)",
+                                   "linears, QKV bias, tied 4-bit embedding/head, greedy, sequences in lockstep "
+                                   "(BASELINE config 5)",
                        "layers": cfg.n_layers, "hidden": cfg.hidden, "heads": cfg.n_heads,
                        "kv_heads": cfg.n_kv_heads, "head_dim": cfg.head_dim, "ffn": cfg.ffn, "vocab": cfg.vocab},
             "setup_s": round(setup_s, 1)}
@@ -381,8 +391,9 @@ def main():
     qwen = None
     if not args.no_decode and not args.no_qwen_decode:
         qwen = qwen_decode_bench(args.qwen_context, args.qwen_tokens)
-        print(f"# qwen decode (KV {qwen['kv_context']}): {qwen['tokens_per_s']} tokens/s "
-              f"({qwen['ms_per_token']} ms/token)", file=sys.stderr, flush=True)
+        print(f"# qwen decode (KV {qwen['kv_context']}): " + ", ".join(
+            f"bs {b}: {v['tokens_per_s_aggregate']} tokens/s ({v['ms_per_step']} ms/step)"
+            for b, v in qwen["per_batch"].items()), file=sys.stderr, flush=True)
     batched = None if args.no_batched else batched_bench(torch, L)
     if batched is not None:
         print("# batched linears per step: " + ", ".join(
