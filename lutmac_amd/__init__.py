@@ -126,6 +126,14 @@ def lib():
     if _LIB is None:
         if not os.path.exists(LIB_PATH):
             raise RuntimeError(f"{LIB_PATH} is missing: build it with `python -m lutmac_amd.build`")
+        # torch's wheel carries its own HIP runtime; loading torch first makes
+        # the library bind to that same runtime, so torch streams and device
+        # pointers are valid in both (a library loaded first pulls in the
+        # system runtime, and torch then finds no GPU).
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         L = ctypes.CDLL(LIB_PATH)
         for name, (args, res) in _SIGS.items():
             f = getattr(L, name)

@@ -57,13 +57,15 @@ int choose_waves() {
   return (env == 1 || env == 2 || env == 4) ? env : 4;
 }
 
-// k-slice per workgroup: 512 when the padded K allows it and the grid still
-// has at least 4 workgroups per CU, else 256.  LMX_KSLICE overrides.
+// k-slice per workgroup: 512 when K is above 4096, the padded K allows it
+// and the grid still has at least 4 workgroups per CU, else 256 (measured on
+// MI355X: the LM heads, K 1536 and 2048, run 3-4 % faster at 256).
+// LMX_KSLICE overrides.
 int choose_kslice(size_t Npad, size_t Kp, int waves) {
   const int env = env_int("LMX_KSLICE", 0);
   if ((env == 256 || env == 512) && Kp % size_t(env) == 0) return env;
   const size_t row_blocks = (Npad + kWave * waves - 1) / (kWave * waves);
-  if (Kp % 512 == 0 && row_blocks * (Kp / 512) >= 1024) return 512;
+  if (Kp > 4096 && Kp % 512 == 0 && row_blocks * (Kp / 512) >= 1024) return 512;
   return 256;
 }
 
@@ -90,14 +92,15 @@ int choose_fullk(int fmt, size_t Npad, size_t Kp, int kfamily) {
   auto workgroups = [&](int cfg) { return Npad / size_t(kWave / fullk_shape(cfg).h); };
   // Measured on MI355X (4-bit, decode shapes):
   //  * K <= 2048: 4 waves x 16 rows per workgroup wins from N = 256 up to
-  //    ~16k rows (latency-bound small GEMVs want many small workgroups); up
-  //    to ~32k rows 8 waves x 32 rows; beyond that (LM heads) every
-  //    workgroup rebuilding the tables costs more than the split-K handoff.
+  //    ~8k rows (latency-bound small GEMVs want many small workgroups); up
+  //    to ~32k rows 8 waves x 32 rows (16384 x 2048: 6.7 against 7.5 us);
+  //    beyond that (LM heads) every workgroup rebuilding the tables costs
+  //    more than the split-K handoff.
   //  * larger K: the configuration with the most workgroups that still
   //    leaves at most one per CU (each holds up to 160 KB of tables);
   //    split-K when none does.
   if (Kc <= 16) {
-    if (fits(kFullK_4x4x1) && workgroups(kFullK_4x4x1) <= 1024) return kFullK_4x4x1;
+    if (fits(kFullK_4x4x1) && workgroups(kFullK_4x4x1) <= 512) return kFullK_4x4x1;
     if (fits(kFullK_8x2x1) && workgroups(kFullK_8x2x1) <= 1024) return kFullK_8x2x1;
     return kFullK_None;
   }

@@ -94,20 +94,6 @@ __global__ __launch_bounds__(256) void embed_kernel(const uint8_t *__restrict__ 
   out[k] = weight_value<FMT>(b, s);
 }
 
-// RoPE of one head vector: pairs (d, d + HD/2) rotated by pf * freq[d]
-// (embedding.cpp:36-75 pairs the halves the same way).
-template <int HD>
-__device__ __forceinline__ void rope_pair(const float *in, float *out, const float *freq, float pf, int lane) {
-  constexpr int HALF = HD / 2;
-  for (int d = lane; d < HALF; d += kWave) {
-    float sn, cs;
-    sincosf(pf * freq[d], &sn, &cs);
-    const float a0 = in[d], a1 = in[d + HALF];
-    out[d] = a0 * cs - a1 * sn;
-    out[d + HALF] = a0 * sn + a1 * cs;
-  }
-}
-
 // Batched decode helpers (one workgroup per sequence row).
 // y[b] = x[b] * inv_rms(x[b]) * w, inv_rms = 1/sqrt(sum x^2 / n + eps)
 // (norm.cpp:18-34).
@@ -284,30 +270,69 @@ __global__ __launch_bounds__(512) void attn_kernel(const float *__restrict__ qkv
   const float *vin = kin + row;
   const int pos = min(*pos_p, max_seq - 1);
 
-  // ---- the chunk's K and V rows into LDS (loads first, one round trip) ----
-  {
-    float4 kr[KV4], vr[KV4];
+  // ---- every global operand requested before the first wait (one round
+  // trip): the chunk's K and V rows, the query head's q, the new key and
+  // value, and the RoPE frequencies (all waves load them; in bounds) ----
+  constexpr int HALF = HD / 2;
+  constexpr int RP = (HALF + kWave - 1) / kWave;   // rotation pairs per lane
+  float4 kr[KV4], vr[KV4];
 #pragma unroll
-    for (int i = 0; i < KV4; ++i) {
-      const int f = int(threadIdx.x) + i * NT;          // float4 index in the 64 x HD chunk
-      const int r = f / (HD / 4), c4 = f % (HD / 4);
-      kr[i] = *reinterpret_cast<const float4 *>(kc + size_t(t0 + r) * row + kvh * HD + 4 * c4);
-      vr[i] = *reinterpret_cast<const float4 *>(vc + size_t(t0 + r) * row + kvh * HD + 4 * c4);
-    }
+  for (int i = 0; i < KV4; ++i) {
+    const int f = int(threadIdx.x) + i * NT;          // float4 index in the 64 x HD chunk
+    const int r = f / (HD / 4), c4 = f % (HD / 4);
+    kr[i] = *reinterpret_cast<const float4 *>(kc + size_t(t0 + r) * row + kvh * HD + 4 * c4);
+    vr[i] = *reinterpret_cast<const float4 *>(vc + size_t(t0 + r) * row + kvh * HD + 4 * c4);
+  }
+  const float *qin = qkv + size_t(kvh * group + (wave < group ? wave : 0)) * HD;
+  float qa[RP], qb[RP], ka[RP], kb[RP], fr[RP], vn[VD];
 #pragma unroll
-    for (int i = 0; i < KV4; ++i) {
-      const int f = int(threadIdx.x) + i * NT;
-      const int r = f / (HD / 4), c4 = f % (HD / 4);
-      *reinterpret_cast<float4 *>(&ks[r][4 * c4]) = kr[i];
-      *reinterpret_cast<float4 *>(&vs[r][4 * c4]) = vr[i];
-    }
+  for (int i = 0; i < RP; ++i) {
+    const int d = min(lane + i * kWave, HALF - 1);
+    fr[i] = freq[d];
+    qa[i] = qin[d];
+    qb[i] = qin[d + HALF];
+    ka[i] = kin[d];
+    kb[i] = kin[d + HALF];
+  }
+#pragma unroll
+  for (int u = 0; u < VD; ++u) vn[u] = vin[u * kWave + lane];
+  // One wait for all of them: without a use of every loaded value here the
+  // compiler issues the small loads after the K/V waits (a second round trip).
+#pragma unroll
+  for (int i = 0; i < KV4; ++i)
+    asm volatile("" ::"v"(kr[i].x), "v"(kr[i].y), "v"(kr[i].z), "v"(kr[i].w), "v"(vr[i].x), "v"(vr[i].y),
+                 "v"(vr[i].z), "v"(vr[i].w));
+#pragma unroll
+  for (int i = 0; i < RP; ++i) asm volatile("" ::"v"(fr[i]), "v"(qa[i]), "v"(qb[i]), "v"(ka[i]), "v"(kb[i]));
+#pragma unroll
+  for (int u = 0; u < VD; ++u) asm volatile("" ::"v"(vn[u]));
+#pragma unroll
+  for (int i = 0; i < KV4; ++i) {
+    const int f = int(threadIdx.x) + i * NT;
+    const int r = f / (HD / 4), c4 = f % (HD / 4);
+    *reinterpret_cast<float4 *>(&ks[r][4 * c4]) = kr[i];
+    *reinterpret_cast<float4 *>(&vs[r][4 * c4]) = vr[i];
   }
   const bool live = t0 <= pos;                      // chunk holds positions of the sequence
   const bool own = pos / kAttnChunk == chunk;       // the chunk holds the new position
   const float pf = float(pos) / pos_div;
-  if (live && wave < group) {
-    rope_pair<HD>(qkv + size_t(kvh * group + wave) * HD, qs[wave], freq, pf, lane);
-    if (own && wave == 0) rope_pair<HD>(kin, knew, freq, pf, lane);
+  // RoPE: pairs (d, d + HD/2) rotated by pf * freq[d] (embedding.cpp:36-75),
+  // computed by every lane so that no load sinks into a branch
+#pragma unroll
+  for (int i = 0; i < RP; ++i) {
+    const int d = lane + i * kWave;
+    float sn, cs;
+    sincosf(pf * fr[i], &sn, &cs);
+    const float q0 = qa[i] * cs - qb[i] * sn, q1 = qa[i] * sn + qb[i] * cs;
+    const float k0 = ka[i] * cs - kb[i] * sn, k1 = ka[i] * sn + kb[i] * cs;
+    if (live && wave < group && d < HALF) {
+      qs[wave][d] = q0;
+      qs[wave][d + HALF] = q1;
+      if (own && wave == 0) {
+        knew[d] = k0;
+        knew[d + HALF] = k1;
+      }
+    }
   }
   __syncthreads();
 
@@ -352,7 +377,7 @@ __global__ __launch_bounds__(512) void attn_kernel(const float *__restrict__ qkv
 #pragma unroll
         for (int j = 0; j < kAttnChunk; ++j) s8[j % 8] += pw[wave][j] * vs[j][d];
         o[u] = ((s8[0] + s8[1]) + (s8[2] + s8[3])) + ((s8[4] + s8[5]) + (s8[6] + s8[7]));
-        if (own) o[u] += enew * vin[d];
+        if (own) o[u] += enew * vn[u];
       }
     }
 #pragma unroll
@@ -363,9 +388,11 @@ __global__ __launch_bounds__(512) void attn_kernel(const float *__restrict__ qkv
       __hip_atomic_store(dst + 1, l, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     if (own && wave == 0) {   // append the new position to the cache
-      for (int d = lane; d < HD; d += kWave) {
+#pragma unroll
+      for (int u = 0; u < VD; ++u) {
+        const int d = u * kWave + lane;
         kc[size_t(pos) * row + kvh * HD + d] = knew[d];
-        vc[size_t(pos) * row + kvh * HD + d] = vin[d];
+        vc[size_t(pos) * row + kvh * HD + d] = vn[u];
       }
     }
   }
@@ -380,45 +407,53 @@ __global__ __launch_bounds__(512) void attn_kernel(const float *__restrict__ qkv
     const int head = kvh * group + wave;
     const float *ph = part + size_t(head) * n_chunks * (HD + 4);
     const int nused = pos / kAttnChunk + 1;        // chunks holding positions
-    // chunk weights: lane c holds chunk c (64 at a time)
-    float M = -INFINITY;
-    for (int c0 = 0; c0 < nused; c0 += kWave) {
-      const int c = c0 + lane;
-      const float mc = c < nused ? __hip_atomic_load(ph + size_t(c) * (HD + 4), __ATOMIC_RELAXED,
-                                                     __HIP_MEMORY_SCOPE_AGENT) : -INFINITY;
-      M = fmaxf(M, lane_max<32>(mc, lane));
-    }
-    float L = 0.0f, o[VD];
+    // Lane c loads chunk c's (m, l) and, in the same round trip, the o rows of
+    // the pass's first 8 chunks; later groups of 8 (past 512 positions)
+    // follow.  Passes of 64 chunks rescale a running maximum.
+    float M = -INFINITY, L = 0.0f, o[VD];
 #pragma unroll
     for (int u = 0; u < VD; ++u) o[u] = 0.0f;
     for (int c0 = 0; c0 < nused; c0 += kWave) {
       const int c = c0 + lane;
-      float wc = 0.0f, lc = 0.0f;
-      if (c < nused) {
-        const float mc = __hip_atomic_load(ph + size_t(c) * (HD + 4), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        lc = __hip_atomic_load(ph + size_t(c) * (HD + 4) + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        wc = expf(mc - M);
-      }
-      L += lane_sum<32>(wc * lc, lane);
-      pw[wave][lane] = wc;
-      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-      __builtin_amdgcn_wave_barrier();
       const int nb = min(kWave, nused - c0);
-      for (int j0 = 0; j0 < nb; j0 += 8) {   // 8 chunks' loads in flight at a time
-        float v[8][VD];
-#pragma unroll
-        for (int jj = 0; jj < 8; ++jj)
-#pragma unroll
-          for (int u = 0; u < VD; ++u)
-            v[jj][u] = j0 + jj < nb ? __hip_atomic_load(ph + size_t(c0 + j0 + jj) * (HD + 4) + 4 + u * kWave + lane,
-                                                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                                    : 0.0f;
-#pragma unroll
-        for (int jj = 0; jj < 8; ++jj)
-#pragma unroll
-          for (int u = 0; u < VD; ++u) o[u] += (j0 + jj < nb ? pw[wave][j0 + jj] : 0.0f) * v[jj][u];
+      float mc = -INFINITY, lc = 0.0f;
+      if (c < nused) {
+        mc = __hip_atomic_load(ph + size_t(c) * (HD + 4), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        lc = __hip_atomic_load(ph + size_t(c) * (HD + 4) + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
-      __builtin_amdgcn_wave_barrier();
+      float v[8][VD];
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj)
+#pragma unroll
+        for (int u = 0; u < VD; ++u)
+          v[jj][u] = jj < nb ? __hip_atomic_load(ph + size_t(c0 + jj) * (HD + 4) + 4 + u * kWave + lane,
+                                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                             : 0.0f;
+      const float Mn = fmaxf(M, lane_max<32>(mc, lane));   // finite: chunk 0 holds position 0
+      const float rs = expf(M - Mn);                        // 0 on the first pass
+      L *= rs;
+#pragma unroll
+      for (int u = 0; u < VD; ++u) o[u] *= rs;
+      M = Mn;
+      const float wc = c < nused ? expf(mc - M) : 0.0f;
+      L += lane_sum<32>(wc * lc, lane);
+      for (int j0 = 0; j0 < nb; j0 += 8) {
+        if (j0 > 0) {
+#pragma unroll
+          for (int jj = 0; jj < 8; ++jj)
+#pragma unroll
+            for (int u = 0; u < VD; ++u)
+              v[jj][u] = j0 + jj < nb ? __hip_atomic_load(ph + size_t(c0 + j0 + jj) * (HD + 4) + 4 + u * kWave + lane,
+                                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                      : 0.0f;
+        }
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) {
+          const float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wc), j0 + jj));
+#pragma unroll
+          for (int u = 0; u < VD; ++u) o[u] += w * v[jj][u];
+        }
+      }
     }
     const float inv = 1.0f / L;
 #pragma unroll
