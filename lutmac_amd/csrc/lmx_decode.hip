@@ -219,6 +219,56 @@ std::vector<float> rope_freqs(const lmx_decoder_config &c) {
   return f;
 }
 
+// One pass of the attention chunk merge over chunks c0 .. c0 + nb - 1 (nb <=
+// 64): lane c loads chunk c0 + c's (m, l) and, in the same round trip, the o
+// rows of the first MB chunks; later groups of MB follow.  Rescales the
+// running (M, L, o) to the pass's new maximum and adds the pass's chunks
+// weighted by e^(m_c - M) (each weight read from its lane).
+template <int HD, int MB>
+__device__ __forceinline__ void merge_pass(const float *ph, int c0, int nb, int lane, float &M, float &L,
+                                           float (&o)[HD / kWave]) {
+  constexpr int VD = HD / kWave;
+  const int c = c0 + lane;
+  float mc = -INFINITY, lc = 0.0f;
+  if (lane < nb) {
+    mc = __hip_atomic_load(ph + size_t(c) * (HD + 4), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    lc = __hip_atomic_load(ph + size_t(c) * (HD + 4) + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  float v[MB][VD];
+#pragma unroll
+  for (int jj = 0; jj < MB; ++jj)
+#pragma unroll
+    for (int u = 0; u < VD; ++u)
+      v[jj][u] = jj < nb ? __hip_atomic_load(ph + size_t(c0 + jj) * (HD + 4) + 4 + u * kWave + lane,
+                                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                         : 0.0f;
+  const float Mn = fmaxf(M, lane_max<32>(mc, lane));   // finite: chunk 0 holds position 0
+  const float rs = expf(M - Mn);                        // 0 on the first pass
+  L *= rs;
+#pragma unroll
+  for (int u = 0; u < VD; ++u) o[u] *= rs;
+  M = Mn;
+  const float wc = lane < nb ? expf(mc - M) : 0.0f;
+  L += lane_sum<32>(wc * lc, lane);
+  for (int j0 = 0; j0 < nb; j0 += MB) {
+    if (j0 > 0) {
+#pragma unroll
+      for (int jj = 0; jj < MB; ++jj)
+#pragma unroll
+        for (int u = 0; u < VD; ++u)
+          v[jj][u] = j0 + jj < nb ? __hip_atomic_load(ph + size_t(c0 + j0 + jj) * (HD + 4) + 4 + u * kWave + lane,
+                                                      __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                  : 0.0f;
+    }
+#pragma unroll
+    for (int jj = 0; jj < MB; ++jj) {
+      const float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wc), j0 + jj));
+#pragma unroll
+      for (int u = 0; u < VD; ++u) o[u] += w * v[jj][u];
+    }
+  }
+}
+
 // Attention with the chunk merge inside: one workgroup per (KV head, 64
 // positions), 8 waves.  All 8 waves first load the chunk's 64 cached K and V
 // rows of the KV head into LDS (every row is in bounds: the cache holds whole
@@ -407,53 +457,18 @@ __global__ __launch_bounds__(512) void attn_kernel(const float *__restrict__ qkv
     const int head = kvh * group + wave;
     const float *ph = part + size_t(head) * n_chunks * (HD + 4);
     const int nused = pos / kAttnChunk + 1;        // chunks holding positions
-    // Lane c loads chunk c's (m, l) and, in the same round trip, the o rows of
-    // the pass's first 8 chunks; later groups of 8 (past 512 positions)
-    // follow.  Passes of 64 chunks rescale a running maximum.
+    // Passes of 64 chunks (lane c holds chunk c0 + c) rescale a running
+    // maximum; the batch of o rows loaded with the weights is sized to the
+    // chunks in use (8 or 32).
     float M = -INFINITY, L = 0.0f, o[VD];
 #pragma unroll
     for (int u = 0; u < VD; ++u) o[u] = 0.0f;
     for (int c0 = 0; c0 < nused; c0 += kWave) {
-      const int c = c0 + lane;
       const int nb = min(kWave, nused - c0);
-      float mc = -INFINITY, lc = 0.0f;
-      if (c < nused) {
-        mc = __hip_atomic_load(ph + size_t(c) * (HD + 4), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        lc = __hip_atomic_load(ph + size_t(c) * (HD + 4) + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-      float v[8][VD];
-#pragma unroll
-      for (int jj = 0; jj < 8; ++jj)
-#pragma unroll
-        for (int u = 0; u < VD; ++u)
-          v[jj][u] = jj < nb ? __hip_atomic_load(ph + size_t(c0 + jj) * (HD + 4) + 4 + u * kWave + lane,
-                                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                             : 0.0f;
-      const float Mn = fmaxf(M, lane_max<32>(mc, lane));   // finite: chunk 0 holds position 0
-      const float rs = expf(M - Mn);                        // 0 on the first pass
-      L *= rs;
-#pragma unroll
-      for (int u = 0; u < VD; ++u) o[u] *= rs;
-      M = Mn;
-      const float wc = c < nused ? expf(mc - M) : 0.0f;
-      L += lane_sum<32>(wc * lc, lane);
-      for (int j0 = 0; j0 < nb; j0 += 8) {
-        if (j0 > 0) {
-#pragma unroll
-          for (int jj = 0; jj < 8; ++jj)
-#pragma unroll
-            for (int u = 0; u < VD; ++u)
-              v[jj][u] = j0 + jj < nb ? __hip_atomic_load(ph + size_t(c0 + j0 + jj) * (HD + 4) + 4 + u * kWave + lane,
-                                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                                      : 0.0f;
-        }
-#pragma unroll
-        for (int jj = 0; jj < 8; ++jj) {
-          const float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wc), j0 + jj));
-#pragma unroll
-          for (int u = 0; u < VD; ++u) o[u] += w * v[jj][u];
-        }
-      }
+      if (nb <= 8)
+        merge_pass<HD, 8>(ph, c0, nb, lane, M, L, o);
+      else
+        merge_pass<HD, 32>(ph, c0, nb, lane, M, L, o);
     }
     const float inv = 1.0f / L;
 #pragma unroll

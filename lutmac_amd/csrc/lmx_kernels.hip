@@ -485,19 +485,20 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_kernel(GemvArgs a, int
   const int r = rb * ROWS + threadIdx.x;
   float out = 0.0f;
   if (r < a.rows) {
-    // Sum the partials in split order; loads go out 8 at a time so their
-    // latencies overlap.
+    // Sum the partials in split order; loads go out 32 at a time so their
+    // latencies overlap (one round trip up to 32 splits, K = 8192 at
+    // 256-wide slices).
     float s = 0.0f;
     const float *pr = a.partials + r;
-    for (int k0s = 0; k0s < splits; k0s += 8) {
-      float v[8];
+    for (int k0s = 0; k0s < splits; k0s += 32) {
+      float v[32];
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
+      for (int j = 0; j < 32; ++j)
         v[j] = k0s + j < splits
                    ? __hip_atomic_load(pr + size_t(k0s + j) * a.Npad, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
                    : 0.0f;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) s += v[j];
+      for (int j = 0; j < 32; ++j) s += v[j];
     }
     out = a.bias ? s + a.bias[r] : s;
     a.y[r] = out;
@@ -1315,7 +1316,13 @@ __global__ __launch_bounds__(64) void batched_reduce_kernel(const float *__restr
   if (r >= rows) return;
   const float *p = partials + size_t(n) * splits * Npad + r;
   float s = 0.0f;
-  for (int k = 0; k < splits; ++k) s += p[size_t(k) * Npad];
+  for (int k0 = 0; k0 < splits; k0 += 32) {   // 32 loads in flight, summed in split order
+    float v[32];
+#pragma unroll
+    for (int j = 0; j < 32; ++j) v[j] = k0 + j < splits ? p[size_t(k0 + j) * Npad] : 0.0f;
+#pragma unroll
+    for (int j = 0; j < 32; ++j) s += v[j];
+  }
   if (bias) s += bias[r];
   if (resid) s += resid[size_t(n) * rows + r];
   y[size_t(n) * rows + r] = s;

@@ -61,6 +61,19 @@ def test_decoder_matches_oracle_qwen_style(cuda):
     check_against(D.Decoder(m), oracle.OracleDecoder(m), toks)
 
 
+def test_decoder_long_ffn(cuda):
+    # FFN 8960 (Qwen-2.5-1.5B's width): the down projection's K = 8960 fits
+    # no full-K configuration and runs split-K (35 slices) with SiLU*up fused,
+    # gate|up (17920 rows) the 8 x 32 small-K configuration
+    cfg = D.small_config(hidden=256, ffn=8960, vocab=1000, rope_mode=D.ROPE_REFERENCE, rope_factor=1.0,
+                         rope_theta=1e6)
+    m = D.SyntheticModel(cfg, seed=31, group=128, random_norms=True)
+    dec = D.Decoder(m)
+    assert [w.kernel_config()[0] for w in dec.weights[:4]] == [6, 6, 3, 0]   # qkv, o, gate|up, down
+    toks = np.random.default_rng(32).integers(0, cfg.vocab, 12)
+    check_against(dec, oracle.OracleDecoder(m), toks)
+
+
 @pytest.mark.parametrize("head_dim,n_heads,n_kv", [(64, 8, 2), (128, 12, 2)])
 def test_decoder_multi_chunk_context(cuda, head_dim, n_heads, n_kv):
     # 150 positions span three 64-position attention chunks (a fourth, empty,
