@@ -1188,12 +1188,17 @@ size_t gemv_argmax_slots(const GemvArgs &a) {
 // ---------------------------------------------------------------------------
 // Batched GEMV: y_b = W x_b for NB activation vectors with the weights read
 // once (replaces lut_linear's per-row loop, lut_gemm_scalar.cpp:76-79).  A
-// workgroup owns 256 rows (4 waves, one row per lane) and a k-slice of 256;
-// the tables of the NB vectors sit interleaved per group in LDS, table
-// (chunk c, group g, vector b) at ((c*32 + g)*NB + b)*64 bytes, so one v_perm
-// address serves all NB vectors and the vector picks the ds_read immediate.
-// Partials [NB][splits][Npad] go through batched_reduce_kernel.
-template <int NB>
+// workgroup owns 256 rows and a k-slice of 256 with 4 * NB/VG waves: wave w
+// serves row group w % 4 (one row per lane) for vectors (w / 4)*VG ..
+// (w / 4)*VG + VG - 1, so the LDS lookups of many vectors have enough waves
+// to hide their latency (the weight words of a row group are read by NB/VG
+// waves: one HBM read, the rest cache hits).  The tables of a vector group
+// sit interleaved per group in LDS, table (chunk c, vector group v, group g,
+// vector b of the group) at (((c*NB/VG + v)*32 + g)*VG + b)*64 bytes, so
+// every group block starts 256-byte aligned, one v_perm address serves a
+// wave's VG vectors and the vector picks the ds_read immediate.  Partials
+// [NB][splits][Npad] go through batched_reduce_kernel.
+template <int VG>
 __device__ __forceinline__ void word_lookups_batch(uint32_t v, int i, uint32_t cbase, float *out) {
   const uint32_t hi = (v >> 2) & 0x3C3C3C3Cu, lo = (v << 2) & 0x3C3C3C3Cu;
   uint32_t ad[8];
@@ -1203,33 +1208,41 @@ __device__ __forceinline__ void word_lookups_batch(uint32_t v, int i, uint32_t c
     ad[2 * b + 1] = __builtin_amdgcn_perm(cbase, lo, 0x0C060500u | b);
   }
 #pragma unroll
-  for (int n = 0; n < NB; ++n) {
+  for (int n = 0; n < VG; ++n) {
     float t[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) t[j] = lds_load(ad[j] + ((8 * i + j) * NB + n) * 64);
+    for (int j = 0; j < 8; ++j) t[j] = lds_load(ad[j] + ((8 * i + j) * VG + n) * 64);
     out[n] += ((t[0] + t[1]) + (t[2] + t[3])) + ((t[4] + t[5]) + (t[6] + t[7]));
   }
 }
 
-template <int FMT, int NB>
-__global__ __launch_bounds__(256) void lut_gemv_batch_kernel(GemvArgs a, int row_blocks, int splits) {
+template <int NB, int VG>
+constexpr int batch_waves() { return 4 * (NB / VG); }
+
+template <int FMT, int NB, int VG>
+__global__ __launch_bounds__((kWave * batch_waves<NB, VG>())) void lut_gemv_batch_kernel(GemvArgs a, int row_blocks,
+                                                                                      int splits) {
   constexpr int P = Fmt<FMT>::P, NA = Fmt<FMT>::NA, S = Fmt<FMT>::S;
   constexpr int CH = kRotChunk / kChunk;   // 2 chunks of 128 per slice
+  constexpr int NW = batch_waves<NB, VG>();
+  constexpr int NVG = NB / VG;
+  static_assert(NB % VG == 0 && NW <= 16, "whole vector groups, at most 1024 threads");
   __shared__ __attribute__((aligned(256))) float tables[CH * 32 * NB * 16];
   __shared__ float xsum[NB][CH];
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  const int rg = wave & 3, vg = wave >> 2;
   const int rb = blockIdx.x % row_blocks, split = blockIdx.x / row_blocks;
   const int k0 = split * kRotChunk;
-  const int row = rb * 256 + wave * kWave + lane;
-  const bool active = rb * 256 + wave * kWave < a.Npad;
+  const int row = rb * 256 + rg * kWave + lane;
+  const bool active = rb * 256 + rg * kWave < a.Npad;
   const int lr = min(row, a.Npad - 1);
 
-  // activations: wave w builds the tables of vectors w, w+4, ...
-  constexpr int XV = (NB + 3) / 4;
+  // activations: wave w builds the tables of vectors w, w + NW, ...
+  constexpr int XV = (NB + NW - 1) / NW;
   float xv[XV][4];
 #pragma unroll
   for (int j = 0; j < XV; ++j) {
-    const int n = min(wave + 4 * j, NB - 1);
+    const int n = min(wave + NW * j, NB - 1);
     load_x4(a.x + size_t(n) * a.cols, k0, a.cols, lane, xv[j][0], xv[j][1], xv[j][2], xv[j][3]);
   }
   __builtin_amdgcn_sched_barrier(0);
@@ -1242,7 +1255,11 @@ __global__ __launch_bounds__(256) void lut_gemv_batch_kernel(GemvArgs a, int row
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
 #pragma unroll
-      for (int p = 0; p < P; ++p) w[c][p] = __builtin_nontemporal_load(pl + (size_t(c0 + c) * P + p) * Npad + lr);
+      for (int p = 0; p < P; ++p) {
+        const u32x4 *src = pl + (size_t(c0 + c) * P + p) * Npad + lr;
+        // one wave per row group streams; the others re-read through the caches
+        w[c][p] = NW == 4 ? __builtin_nontemporal_load(src) : *src;
+      }
       const int g = (c0 + c) / a.group_chunks;
 #pragma unroll
       for (int t = 0; t < S; ++t) sc[c][t] = a.scales[(size_t(t) * a.n_groups + g) * Npad + lr];
@@ -1250,14 +1267,14 @@ __global__ __launch_bounds__(256) void lut_gemv_batch_kernel(GemvArgs a, int row
   }
 #pragma unroll
   for (int j = 0; j < XV; ++j) {
-    const int n = wave + 4 * j;
+    const int n = wave + NW * j;
     if (n >= NB) break;   // wave-uniform
     float x0 = xv[j][0], x1 = xv[j][1], x2 = xv[j][2], x3 = xv[j][3];
     if (a.rotate == LMX_ROTATE_FWHT256) fwht256_regs(x0, x1, x2, x3, lane);
     float t[16];
     group_table(x0, x1, x2, x3, t);
     const int c = lane >> 5, g = lane & 31;
-    float4 *dst = reinterpret_cast<float4 *>(tables + ((c * 32 + g) * NB + n) * 16);
+    float4 *dst = reinterpret_cast<float4 *>(tables + (((c * NVG + n / VG) * 32 + g) * VG + n % VG) * 16);
     dst[0] = make_float4(t[0], t[1], t[2], t[3]);
     dst[1] = make_float4(t[4], t[5], t[6], t[7]);
     dst[2] = make_float4(t[8], t[9], t[10], t[11]);
@@ -1271,18 +1288,19 @@ __global__ __launch_bounds__(256) void lut_gemv_batch_kernel(GemvArgs a, int row
   __syncthreads();
   if (!active) return;   // whole wavefronts; no barrier follows
 
-  float acc[NB];
+  const int n0 = vg * VG;   // this wave's first vector
+  float acc[VG];
 #pragma unroll
-  for (int n = 0; n < NB; ++n) acc[n] = 0.0f;
-  const uint32_t tbase = lds_addr(tables);
+  for (int n = 0; n < VG; ++n) acc[n] = 0.0f;
+  const uint32_t tbase = lds_addr(tables) + uint32_t(vg) * (32 * VG * 64);   // 256-byte aligned
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
-    float A[NA][NB];
+    float A[NA][VG];
 #pragma unroll
     for (int q = 0; q < NA; ++q)
 #pragma unroll
-      for (int n = 0; n < NB; ++n) A[q][n] = 0.0f;
-    const uint32_t cbase = tbase + c * 32 * NB * 64;
+      for (int n = 0; n < VG; ++n) A[q][n] = 0.0f;
+    const uint32_t cbase = tbase + c * (NVG * 32 * VG * 64);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       uint32_t wi[P], v[NA];
@@ -1290,20 +1308,20 @@ __global__ __launch_bounds__(256) void lut_gemv_batch_kernel(GemvArgs a, int row
       for (int p = 0; p < P; ++p) wi[p] = w[c][p][i];
       lookup_words<FMT>(wi, v);
 #pragma unroll
-      for (int q = 0; q < NA; ++q) word_lookups_batch<NB>(v[q], i, cbase, A[q]);
+      for (int q = 0; q < NA; ++q) word_lookups_batch<VG>(v[q], i, cbase, A[q]);
     }
 #pragma unroll
-    for (int n = 0; n < NB; ++n) {
+    for (int n = 0; n < VG; ++n) {
       float An[NA];
 #pragma unroll
       for (int q = 0; q < NA; ++q) An[q] = A[q][n];
       float xs = 0.0f;
-      if constexpr (Fmt<FMT>::XS) xs = xsum[n][c];
+      if constexpr (Fmt<FMT>::XS) xs = xsum[n0 + n][c];
       acc[n] = finish_chunk<FMT>(An, xs, sc[c], acc[n]);
     }
   }
 #pragma unroll
-  for (int n = 0; n < NB; ++n) a.partials[(size_t(n) * splits + split) * a.Npad + row] = acc[n];
+  for (int n = 0; n < VG; ++n) a.partials[(size_t(n0 + n) * splits + split) * a.Npad + row] = acc[n];
 }
 
 // y[n*rows + r] = sum_s partials[n][s][r] (+ bias[r]) (+ resid[n*rows + r])
@@ -1331,7 +1349,9 @@ __global__ __launch_bounds__(64) void batched_reduce_kernel(const float *__restr
 template <int FMT, int NB>
 static int launch_batch_nb(const GemvArgs &a, hipStream_t st) {
   const int row_blocks = (a.Npad + 255) / 256, splits = a.Kp / kRotChunk;
-  lut_gemv_batch_kernel<FMT, NB><<<dim3(row_blocks * splits), dim3(256), 0, st>>>(a, row_blocks, splits);
+  constexpr int VG = NB >= 4 ? NB / 4 : 1;   // vectors per wave: 16 waves from 4 vectors up
+  lut_gemv_batch_kernel<FMT, NB, VG>
+      <<<dim3(row_blocks * splits), dim3(kWave * batch_waves<NB, VG>()), 0, st>>>(a, row_blocks, splits);
   batched_reduce_kernel<<<dim3((a.rows + kWave - 1) / kWave, NB), dim3(kWave), 0, st>>>(a.partials, splits, a.Npad,
                                                                                      a.rows, a.bias, a.resid, a.y);
   hipError_t e = hipGetLastError();
