@@ -1,9 +1,10 @@
 // lmx_decode.hip -- device-resident batch-1 decoder forward (lutmac_decode.h).
 //
 // A token step is Model::forward(token, pos) + greedy Model::sample
-// (src/model.cpp:47-453, 455-490) with every op on the GPU:
-//   embed_kernel           row `token` of the tied table, dequantized from the
-//                          tile layout (model.cpp:58-85)
+// (src/model.cpp:47-453, 455-490) with every op on the GPU; it starts from
+// the embedding of the token at the current position in the hidden state
+// (embed_kernel at reset: row `token` of the tied table, dequantized from
+// the tile layout, model.cpp:58-85):
 //   per layer:
 //     GEMV qkv             RMSNorm(input_norm) fused into the table prologue,
 //                          q|k|v rows in one weight, + bias (model.cpp:296-323)
@@ -20,7 +21,10 @@
 //   GEMV head              RMSNorm(final_norm) fused, tied table (model.cpp:433-447),
 //                          each wave's first maximum folded into a 64-bit key
 //                          by the GEMV's epilogue (model.cpp:480-490)
-//   argmax_finish_kernel   maximum of the keys -> next token, position + 1
+//   finish_embed_kernel    maximum of the keys -> next token, position + 1,
+//                          and the next token's embedding into the hidden state
+// (Batches of sequences start each step with embed_kernel and finish with
+// argmax_rows_kernel, see step_batched.)
 // The position and the token sequence live in device memory, so the same
 // captured step replays for every position.
 #include <hip/hip_runtime.h>
@@ -157,24 +161,55 @@ __global__ __launch_bounds__(1024) void argmax_rows_kernel(const float *__restri
   }
 }
 
-// Greedy token of the step: the largest of the head GEMV's per-wave argmax
-// keys (the encoding keeps the first maximum, model.cpp:480-490); written
-// unless the next position is forced; then the position advances.
-__global__ __launch_bounds__(1024) void argmax_finish_kernel(const unsigned long long *__restrict__ slots, int n_slots,
-                                                             int *__restrict__ tokens, int *__restrict__ pos_p,
-                                                             int n_forced, int max_pos) {
+// Greedy finish of a step fused with the next step's embedding: the token
+// (the largest of the head GEMV's per-wave argmax keys; the encoding keeps
+// the first maximum, model.cpp:480-490) is written unless the next position
+// is forced, the position advances, and the embedding row of the next token
+// (forced or chosen) becomes the hidden state the next step starts from
+// (embed_kernel's dequantisation).
+template <int FMT>
+__global__ __launch_bounds__(1024) void finish_embed_kernel(const unsigned long long *__restrict__ slots, int n_slots,
+                                                            int *__restrict__ tokens, int *__restrict__ pos_p,
+                                                            int n_forced, int max_pos,
+                                                            const uint8_t *__restrict__ planes,
+                                                            const float *__restrict__ scales, int Npad, int rows,
+                                                            int n_groups, int group_chunks, int cols,
+                                                            float *__restrict__ out) {
+  constexpr int P = EmbFmt<FMT>::P, S = EmbFmt<FMT>::S;
   __shared__ unsigned long long best[16];
+  __shared__ int next;
   unsigned long long key = 0;
   for (int i = threadIdx.x; i < n_slots; i += 1024) key = slots[i] > key ? slots[i] : key;
   key = wave_max_key(key, threadIdx.x & (kWave - 1));
   if ((threadIdx.x & (kWave - 1)) == 0) best[threadIdx.x / kWave] = key;
   __syncthreads();
-  if (threadIdx.x != 0) return;
-  for (int w = 1; w < 16; ++w) key = best[w] > key ? best[w] : key;
-  const int idx = key ? int(0xFFFFFFFFu - uint32_t(key)) : 0;   // no finite maximum: index 0
-  const int pos = *pos_p;
-  if (pos + 1 >= n_forced && pos + 1 <= max_pos) tokens[pos + 1] = idx;
-  *pos_p = pos + 1;
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < 16; ++w) key = best[w] > key ? best[w] : key;
+    const int idx = key ? int(0xFFFFFFFFu - uint32_t(key)) : 0;   // no finite maximum: index 0
+    const int pos = *pos_p;
+    int t = idx;
+    if (pos + 1 <= max_pos) {
+      if (pos + 1 >= n_forced)
+        tokens[pos + 1] = idx;
+      else
+        t = tokens[pos + 1];   // the prompt's token
+    }
+    *pos_p = pos + 1;
+    next = t;
+  }
+  __syncthreads();
+  const int t = min(max(next, 0), rows - 1);
+  for (int k = threadIdx.x; k < cols; k += 1024) {
+    const int c = k / kChunk, byte = (k % kChunk) / 8, bit = 7 - k % 8;
+    int b[P];
+#pragma unroll
+    for (int p = 0; p < P; ++p) b[p] = (planes[((size_t(c) * P + p) * Npad + t) * 16 + byte] >> bit) & 1;
+    const int g = c / group_chunks;
+    float sc[S];
+#pragma unroll
+    for (int i = 0; i < S; ++i) sc[i] = scales[(size_t(i) * n_groups + g) * Npad + t];
+    out[k] = weight_value<FMT>(b, sc);
+  }
 }
 
 int hip_err(hipError_t e, const char *what) {
@@ -566,6 +601,30 @@ int embed(const lmx_weight *w, const int *tokens, const int *pos, float *out, si
   return launch_err("embed");
 }
 
+template <int FMT>
+void launch_finish_embed(const lmx_decoder *d, hipStream_t st) {
+  const lmx_weight *w = d->embed;
+  finish_embed_kernel<FMT><<<dim3(1), dim3(1024), 0, st>>>(
+      d->amax, int(d->amax_slots), d->tokens, d->pos, d->n_forced, int(d->cfg.max_seq),
+      static_cast<const uint8_t *>(w->d_planes), w->d_scales, int(w->Npad), int(w->rows), int(w->n_groups),
+      int(w->group / kChunk), int(w->cols), d->hidden);
+}
+
+// Greedy finish of a batch-1 step and the embedding of the next token.
+int finish_embed(const lmx_decoder *d, hipStream_t st) {
+  switch (d->embed->format) {
+  case LMX_FMT_TERNARY: launch_finish_embed<LMX_FMT_TERNARY>(d, st); break;
+  case LMX_FMT_BINARY: launch_finish_embed<LMX_FMT_BINARY>(d, st); break;
+  case LMX_FMT_RRQ2: launch_finish_embed<LMX_FMT_RRQ2>(d, st); break;
+  case LMX_FMT_RRQ3: launch_finish_embed<LMX_FMT_RRQ3>(d, st); break;
+  case LMX_FMT_INT3: launch_finish_embed<LMX_FMT_INT3>(d, st); break;
+  case LMX_FMT_INT4: launch_finish_embed<LMX_FMT_INT4>(d, st); break;
+  case LMX_FMT_INT8: launch_finish_embed<LMX_FMT_INT8>(d, st); break;
+  default: return fail(LMX_ERR_UNSUPPORTED_FORMAT, "embedding format %d", d->embed->format);
+  }
+  return launch_err("finish_embed");
+}
+
 int attention(lmx_decoder *d, size_t layer, hipStream_t st) {
   const lmx_decoder_config &c = d->cfg;
   const int group = int(c.n_heads / c.n_kv_heads);
@@ -661,11 +720,14 @@ int step_batched(lmx_decoder *d, float *logits_out, hipStream_t st) {
   return launch_err("argmax_rows");
 }
 
+// One token step of one sequence.  The hidden state already holds the
+// embedding of the token at the current position (set_position, then each
+// step's finish_embed), so the step ends with the greedy finish and the next
+// token's embedding in one kernel.
 int step(lmx_decoder *d, float *logits_out, hipStream_t st) {
   if (d->batch > 1) return step_batched(d, logits_out, st);
   const lmx_decoder_config &c = d->cfg;
-  int r = embed(d->embed, d->tokens, d->pos, d->hidden, 1, int(c.max_seq + 1), st);
-  if (r) return r;
+  int r = LMX_OK;
   for (size_t l = 0; l < c.n_layers; ++l) {
     const lmx_decoder::Layer &L = d->layers[l];
     if ((r = gemv(L.qkv, d->hidden, d->qkv, L.qkv_bias, kXModeRmsNorm, L.in_norm, c.rms_eps, st)) ||
@@ -677,9 +739,7 @@ int step(lmx_decoder *d, float *logits_out, hipStream_t st) {
   }
   float *lg = logits_out ? logits_out : d->logits;
   if ((r = gemv(d->head, d->hidden, lg, nullptr, kXModeRmsNorm, d->final_norm, c.rms_eps, st, d->amax))) return r;
-  argmax_finish_kernel<<<dim3(1), dim3(1024), 0, st>>>(d->amax, int(d->amax_slots), d->tokens, d->pos, d->n_forced,
-                                                       int(c.max_seq));
-  return launch_err("argmax");
+  return finish_embed(d, st);
 }
 
 int ready(const lmx_decoder *d) {
@@ -700,7 +760,12 @@ int set_position(lmx_decoder *d, const int32_t *tokens, size_t n, hipStream_t st
   hipError_t e = hipMemcpy2DAsync(d->tokens, (d->cfg.max_seq + 1) * sizeof(int32_t), tokens, n * sizeof(int32_t),
                                   n * sizeof(int32_t), d->batch, hipMemcpyHostToDevice, st);
   if (e == hipSuccess) e = hipMemcpyAsync(d->pos, &zero, sizeof(int), hipMemcpyHostToDevice, st);
-  if (e == hipSuccess) e = hipStreamSynchronize(st);
+  if (e != hipSuccess) return hip_err(e, "decoder reset");
+  if (d->batch == 1) {   // a batch-1 step starts from the embedding of the token at its position
+    const int r = embed(d->embed, d->tokens, d->pos, d->hidden, 1, int(d->cfg.max_seq + 1), st);
+    if (r) return r;
+  }
+  e = hipStreamSynchronize(st);
   if (e != hipSuccess) return hip_err(e, "decoder reset");
   d->n_forced = int(n);
   d->host_pos = 0;
