@@ -47,18 +47,35 @@ FORMATS = {"int4": 6, "ternary": 1, "binary": 2, "rrq2": 3, "rrq3": 4, "int8": 7
 ROTATE_IN_KERNEL = {"ternary", "binary", "rrq2", "rrq3", "int4_rot"}
 
 
-def gemv_bench(L, synth, torch, fmt, n, steps, warmup, graph=True, rotate_in_kernel=True):
-    """Time `steps` GEMVs of an n x n weight of format fmt; returns a dict.
+class Flush:
+    """Streams 1 GiB through HBM (read + write) between timed replays, so the
+    first GEMVs of a replay find none of their weights in the 256 MB MALL."""
+
+    def __init__(self, torch):
+        self.buf = torch.empty(2**28, dtype=torch.float32, device="cuda")
+
+    def __call__(self):
+        self.buf.add_(1.0)
+
+
+def gemv_bench(L, synth, torch, fmt, n, steps, warmup, graph=True, rotate_in_kernel=True, cols=None,
+               group=None, outliers=False, seed=None, flush=None, replays=7):
+    """Time `steps` GEMVs of an n x cols weight of format fmt; returns a dict.
     rotate_in_kernel: FWHT-256 of x fused into the kernel (flags), else x is
     rotated once on the device before the timed region and the kernel runs
-    without rotation."""
-    group = 0 if fmt == L.FMT_TERNARY else 128
-    planes, scales, g = synth.make_weights(fmt, n, n, seed=1000 + fmt, group=group)
-    B = synth.algorithmic_bytes(fmt, n, n, group=g)
+    without rotation.  The `steps` GEMVs are captured in one HIP graph over
+    >= 512 MiB of weight copies; the graph is replayed once untimed and then
+    `replays` times, each after a 1 GiB HBM flush, each timed with HIP events
+    on the launch stream; us_per_gemv is the median replay / steps."""
+    cols = n if cols is None else cols
+    if group is None:
+        group = 0 if fmt == L.FMT_TERNARY else 128
+    planes, scales, g = synth.make_weights(fmt, n, cols, seed=(1000 + fmt) if seed is None else seed, group=group)
+    B = synth.algorithmic_bytes(fmt, n, cols, group=g)
     copies = max(2, -(-ROTATE_BYTES // B))
-    ws = [L.Weight.from_planes(fmt, planes, scales, n, n, g) for _ in range(copies)]
+    ws = [L.Weight.from_planes(fmt, planes, scales, n, cols, g) for _ in range(copies)]
     del planes
-    x = torch.from_numpy(synth.make_activations(n, seed=5)).cuda()
+    x = torch.from_numpy(synth.make_activations(cols, seed=5, outliers=outliers)).cuda()
     if rotate_in_kernel:
         flags = L.ROTATE_FWHT256
     else:
@@ -67,18 +84,20 @@ def gemv_bench(L, synth, torch, fmt, n, steps, warmup, graph=True, rotate_in_ker
         torch.cuda.synchronize()
     y = torch.empty(n, dtype=torch.float32, device="cuda")
     stream = torch.cuda.current_stream()
+    flush = flush or Flush(torch)
     for i in range(warmup):
         ws[i % copies].gemv(x, y, flags=flags, stream=stream)
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     # (a) one launch per GEMV on the stream
+    flush()
     start.record(stream)
     for i in range(steps):
         ws[i % copies].gemv(x, y, flags=flags, stream=stream)
     end.record(stream)
     torch.cuda.synchronize()
     ms_stream = start.elapsed_time(end) / steps
-    ms_graph = None
+    ms_graph, reps = None, []
     if graph:
         # (b) the same `steps` launches captured once in a HIP graph and
         # replayed: what a decode loop captured per token sees.
@@ -91,24 +110,75 @@ def gemv_bench(L, synth, torch, fmt, n, steps, warmup, graph=True, rotate_in_ker
         stream.wait_stream(side)
         cg.replay()                     # untimed: uploads the graph
         torch.cuda.synchronize()
-        start.record(stream)
-        cg.replay()
-        end.record(stream)
-        torch.cuda.synchronize()
-        ms_graph = start.elapsed_time(end) / steps
+        for _ in range(replays):
+            flush()
+            torch.cuda.synchronize()
+            start.record(stream)
+            cg.replay()
+            end.record(stream)
+            torch.cuda.synchronize()
+            reps.append(start.elapsed_time(end) / steps)
+        ms_graph = float(np.median(reps))
         del cg
     ms = ms_graph if ms_graph is not None else ms_stream
     gbps = B / (ms * 1e-3) / 1e9
-    out = {"format": L.FORMAT_NAMES[fmt], "rows": n, "cols": n, "group": g,
+    out = {"format": L.FORMAT_NAMES[fmt], "rows": n, "cols": cols, "group": g,
            "rotation": "FWHT-256 in the kernel" if rotate_in_kernel else "input pre-rotated (FWHT-256), kernel unrotated",
            "kernel_plan": dict(zip(("fullk", "kslice", "staged"), ws[0].kernel_config())),
            "algorithmic_bytes": B, "us_per_gemv": round(ms * 1e3, 3), "GB_per_s": round(gbps, 1),
            "launch": "hip_graph" if ms_graph is not None else "stream",
+           "replays_us_per_gemv": [round(r * 1e3, 3) for r in reps],
            "us_per_gemv_stream_launch": round(ms_stream * 1e3, 3),
            "frac_of_peak": round(gbps / HBM_PEAK_GBPS, 4), "weight_copies": copies,
            "rotated_MiB": round(copies * B / 2**20, 1)}
+    if outliers:
+        out["activations"] = "N(0,1), ceil(0.5% of K) channels x20"
     for w in ws:
         w.close()
+    return out
+
+
+def config_rows(L, synth, torch, steps, warmup, flush):
+    """BASELINE configs 1 and 2 at their own shapes: 4-bit 2048 x 2048 with
+    per-128 scales, unrotated (config 1), and the ternary Llama-3.2-1B
+    projections with a per-row absmean scale and FWHT-256-rotated outlier
+    activations (config 2), each timed like the 8192^2 sweep."""
+    rows = {"config1_int4_2048x2048": gemv_bench(L, synth, torch, L.FMT_INT4, 2048, steps, warmup,
+                                                 rotate_in_kernel=False, group=128, seed=1, flush=flush)}
+    rows["config1_int4_2048x2048"]["rotation"] = "none (the reference's int4 operator does not rotate)"
+    for name, (n, k) in synth.LLAMA_TERNARY_SHAPES.items():
+        if name in ("o_proj", "v_proj", "up_proj"):
+            continue            # same shapes as q/k/gate
+        key = "config2_ternary_" + {"q_proj": "q_o", "k_proj": "k_v", "gate_proj": "gate_up",
+                                    "down_proj": "down"}[name] + f"_{n}x{k}"
+        rows[key] = gemv_bench(L, synth, torch, L.FMT_TERNARY, n, steps, warmup, cols=k, group=0,
+                               outliers=True, seed=2, flush=flush)
+    return rows
+
+
+def copy_bandwidth(torch, nbytes=2**30, reps=20):
+    """Achievable HBM bandwidth yardsticks on this GPU: a device-to-device
+    copy of 1 GiB (torch's copy kernel, bytes read + written per second) and
+    a read-only reduction of the same buffer (torch's sum)."""
+    a = torch.empty(nbytes // 4, dtype=torch.float32, device="cuda").fill_(1.0)
+    b = torch.empty_like(a)
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    out = {}
+    for name, fn, moved in (("copy", lambda: b.copy_(a), 2 * nbytes), ("read", lambda: a.sum(), nbytes)):
+        fn()
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(reps):
+            s.record()
+            fn()
+            e.record()
+            torch.cuda.synchronize()
+            ts.append(s.elapsed_time(e))
+        ms = float(np.median(ts))
+        out[name] = {"GB_per_s": round(moved / (ms * 1e-3) / 1e9, 1), "bytes": moved, "ms": round(ms, 4)}
+    out["note"] = ("achievable-bandwidth yardstick: median of %d launches on a 1 GiB buffer; copy counts bytes "
+                   "read + written" % reps)
+    del a, b
     return out
 
 

@@ -144,8 +144,8 @@ int lmx_weight_read_tiles(const lmx_weight *w, uint8_t *tiles, size_t bytes);
  * the rotation selected by flags.  x holds `cols` floats per batch row (the
  * kernel zero-extends to the padded width).  With batch >= 4 (x 16-byte
  * aligned, cols % 4 == 0) groups of 16/8/4 rows share one pass over the
- * weights; the handle's scratch for that grows on the first such call, so
- * make one before capturing a graph.  Replaces the raw per-format
+ * weights, through scratch allocated with the handle (no call allocates,
+ * so calls can be captured into a HIP graph).  Replaces the raw per-format
  * dispatchers lut_gemv / lut_gemv_binary / int2_gemv / int3_gemv /
  * int4_gemv / int8_gemv (lut_gemm.hpp:172-408). */
 int lmx_gemv(const lmx_weight *w, const float *x, float *y, size_t batch,

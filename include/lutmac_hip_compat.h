@@ -4,10 +4,15 @@
  * The extern "C" functions keep the argument meaning of the reference's
  * scalar kernels: host activations in, host outputs overwritten, weights as
  * the reference's AoS block arrays (BitPlaneBlock / BinaryBlock / Int2Block /
- * Int3Block / Int4Block / Int8Block).  Each returns an lmx_status; the block
- * array is repacked and uploaded on first use and cached by
- * (pointer, count, M, K, format), so it must not change afterwards -- the
- * reference treats loaded weights as immutable too.
+ * Int3Block / Int4Block / Int8Block).  Each returns an lmx_status.  The
+ * reference reads the blocks on every call; here a block array is repacked
+ * and uploaded on first use and cached by (pointer, count, M, K, format),
+ * guarded by a fingerprint of its count and of up to 256 whole blocks spread
+ * over the array, rechecked on every call: a mismatch re-uploads.  Call
+ * lmx_host_forget(blocks) before freeing an array or rewriting part of it
+ * (a change the sample cannot see), so no later call reuses stale device
+ * weights.  Calls from several threads are safe; calls that share one
+ * weight are serialised on it.
  *
  * The C++ section maps the reference's names onto them (namespace
  * lutmac_hip); on a failing status it prints lmx_last_error() and aborts, the
@@ -39,6 +44,13 @@ int lmx_host_gemv(int format, const void *blocks, size_t num_blocks,
 int lmx_host_lut_linear(int format, const void *blocks, size_t num_blocks,
                         const float *bias, const float *input, float *output,
                         size_t M, size_t K, size_t batch_size);
+
+/* Drops the cached device weights of the block array at `blocks` (all
+ * shapes and formats), and every cached weight.  No reference counterpart:
+ * the reference reads its blocks per call, so it has no copy to invalidate;
+ * these tie the device copy's lifetime to the caller's PackedTensor. */
+int lmx_host_forget(const void *blocks);
+int lmx_host_cache_clear(void);
 
 /* apply_hadamard_rotation (transform.hpp:19, transform_simd.cpp:101-110):
  * in place, whole 256-chunks only. */

@@ -31,7 +31,8 @@ extern "C" {
 typedef struct lmx_model lmx_model;
 
 /* Loads `path` onto the current device.  max_seq: KV-cache capacity (0 =
- * the file's max_position_embeddings, or 2048 when absent). */
+ * 2048, the capacity the reference's load_model gives its cache: it never
+ * reads the file's max_position_embeddings back, types.hpp:558). */
 int lmx_model_load(const char *path, size_t max_seq, lmx_model **out);
 int lmx_model_destroy(lmx_model *m);
 /* The decoder config derived from the file, and the decoder itself (owned

@@ -36,7 +36,7 @@ EXPORTS = [
     "lmx_precompute_luts", "lmx_extract_indices",
     # include/lutmac_hip_compat.h
     "lmx_host_gemv", "lmx_host_lut_linear", "lmx_host_apply_hadamard_rotation",
-    "lmx_host_precompute_luts",
+    "lmx_host_precompute_luts", "lmx_host_forget", "lmx_host_cache_clear",
     # include/lutmac_decode.h
     "lmx_decoder_create", "lmx_decoder_create_batched", "lmx_decoder_destroy", "lmx_decoder_set_layer", "lmx_decoder_set_head",
     "lmx_decoder_reset", "lmx_decoder_step", "lmx_decoder_tokens", "lmx_decoder_generate",
@@ -96,6 +96,8 @@ _SIGS = {
     "lmx_host_gemv": ([_i, _p, _sz, _p, _p, _sz, _sz], _i),
     "lmx_host_lut_linear": ([_i, _p, _sz, _p, _p, _p, _sz, _sz, _sz], _i),
     "lmx_host_apply_hadamard_rotation": ([_p, _sz], _i),
+    "lmx_host_forget": ([_p], _i),
+    "lmx_host_cache_clear": ([], _i),
     "lmx_quantize_int4": ([_p, _sz, _sz, _sz, _p, _p], _i),
     "lmx_synth_int4_normal": ([ctypes.c_uint64, ctypes.c_uint64, _sz, _sz, ctypes.c_float, _sz, _p, _p], _i),
     "lmx_synth_normal": ([ctypes.c_uint64, ctypes.c_uint64, _sz, _sz, ctypes.c_float, _p], _i),
@@ -361,6 +363,15 @@ def host_lut_linear(fmt, blocks, x, M, K, bias=None, batch=1):
     nb = M * ((K + 255) // 256)
     check(lib().lmx_host_lut_linear(fmt, _np_ptr(blocks), nb, _np_ptr(b), _np_ptr(x), _np_ptr(y), M, K, batch))
     return y
+
+
+def host_forget(blocks):
+    """Drop the cached device copy of a host block array (lmx_host_forget)."""
+    check(lib().lmx_host_forget(_np_ptr(blocks)))
+
+
+def host_cache_clear():
+    check(lib().lmx_host_cache_clear())
 
 
 def host_apply_hadamard_rotation(x):

@@ -195,6 +195,16 @@ int upload(int fmt, size_t rows, size_t cols, size_t group, const uint8_t *plane
     free_weight(w);
     return hip_fail(e, "hipMalloc (weight)");
   }
+  // Batched partials for the largest vector group (16), allocated with the
+  // handle so that no GEMV call allocates (graph capture stays possible).
+  if (w->batched) {
+    const size_t n = 16 * max_splits * w->Npad;
+    if ((e = hipMalloc(reinterpret_cast<void **>(&w->d_bpartials), n * sizeof(float))) != hipSuccess) {
+      free_weight(w);
+      return hip_fail(e, "hipMalloc (batched partials)");
+    }
+    w->bpartials_cap = n;
+  }
   if ((e = hipMemcpy(w->d_planes, tiles.data(), w->tile_bytes, hipMemcpyHostToDevice)) != hipSuccess ||
       (e = hipMemcpy(w->d_scales, sc.data(), w->scale_bytes, hipMemcpyHostToDevice)) != hipSuccess ||
       (e = hipMemset(w->d_counters, 0, row_blocks * sizeof(unsigned))) != hipSuccess ||
@@ -235,10 +245,10 @@ int stage_if_needed(const lmx_weight *w, GemvArgs &a, void *stream) {
 // Batched vectors in groups of 16/8/4 through the batched kernel (weights
 // read once per group; below 4 vectors one GEMV per vector is faster);
 // returns the number of vectors done.  Needs x
-// 16-byte aligned with cols % 4 == 0 (every vector then is).  The handle's
-// batched partials grow on first use (an allocation: make the first batched
-// call before capturing a graph).
-int gemv_batched(lmx_weight *w, GemvArgs a, const float *x, float *y, size_t batch, void *stream, size_t *done) {
+// 16-byte aligned with cols % 4 == 0 (every vector then is).  Uses the
+// handle's batched partials, allocated with the handle.
+int gemv_batched(const lmx_weight *w, GemvArgs a, const float *x, float *y, size_t batch, void *stream,
+                 size_t *done) {
   *done = 0;
   if (!w->batched || batch < 4 || reinterpret_cast<size_t>(x) % 16 || w->cols % 4) return LMX_OK;
   const size_t splits = w->Kp / kRotChunk;
@@ -246,15 +256,8 @@ int gemv_batched(lmx_weight *w, GemvArgs a, const float *x, float *y, size_t bat
   while (batch - *done >= 4) {
     const size_t left = batch - *done;
     const int nb = left >= 16 ? 16 : left >= 8 ? 8 : 4;
-    const size_t need = size_t(nb) * splits * w->Npad;
-    if (need > w->bpartials_cap) {
-      if (w->d_bpartials) (void)hipFree(w->d_bpartials);
-      w->d_bpartials = nullptr;
-      w->bpartials_cap = 0;
-      hipError_t e = hipMalloc(reinterpret_cast<void **>(&w->d_bpartials), 16 * splits * w->Npad * sizeof(float));
-      if (e != hipSuccess) return hip_fail(e, "hipMalloc (batched partials)");
-      w->bpartials_cap = 16 * splits * w->Npad;
-    }
+    if (size_t(nb) * splits * w->Npad > w->bpartials_cap)
+      return fail(LMX_ERR_INVALID_ARGUMENT, "batched partials of %zu floats hold no group of %d", w->bpartials_cap, nb);
     a.x = x + *done * w->cols;
     a.y = y + *done * w->rows;
     a.resid = resid ? resid + *done * w->rows : nullptr;
@@ -482,7 +485,7 @@ int lmx_gemv(const lmx_weight *w, const float *x, float *y, size_t batch, unsign
   size_t b0 = 0;
   if (flags != LMX_ROTATE_FWHT_FULL) {
     a.rotate = flags == LMX_ROTATE_FWHT256 ? LMX_ROTATE_FWHT256 : LMX_ROTATE_NONE;
-    if ((st = gemv_batched(const_cast<lmx_weight *>(w), a, x, y, batch, stream, &b0))) return st;
+    if ((st = gemv_batched(w, a, x, y, batch, stream, &b0))) return st;
   }
   for (size_t b = b0; b < batch; ++b) {
     a.x = x + b * w->cols;
@@ -514,7 +517,7 @@ int lmx_linear(const lmx_weight *w, const float *bias, const float *x, float *y,
   a.bias = bias;
   a.rotate = rotate ? LMX_ROTATE_FWHT256 : LMX_ROTATE_NONE;
   size_t b0 = 0;
-  if ((st = gemv_batched(const_cast<lmx_weight *>(w), a, x, y, batch, stream, &b0))) return st;
+  if ((st = gemv_batched(w, a, x, y, batch, stream, &b0))) return st;
   for (size_t b = b0; b < batch; ++b) {
     a.x = x + b * w->cols;
     a.y = y + b * w->rows;

@@ -29,7 +29,9 @@
 // captured step replays for every position.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <vector>
 
@@ -318,6 +320,11 @@ __device__ __forceinline__ void merge_pass(const float *ph, int c0, int nb, int 
 // attention output, so the o-projection is a plain GEMV.  Partials and
 // tickets travel as device-scope relaxed atomics (no L2 writeback needed);
 // the last workgroup clears the ticket for the next step.
+// Cost follows the position, not the cache capacity (the reference loops
+// to pos only, model.cpp:344-372): chunks below spec_chunks load their rows
+// speculatively, before the position is known; later chunks read the
+// position first and, when it lies before them, load nothing and only take
+// their ticket (the merge reads chunks up to the position only).
 template <int HD>
 __global__ __launch_bounds__(512) void attn_kernel(const float *__restrict__ qkv, float *__restrict__ kc,
                                                    float *__restrict__ vc, const int *__restrict__ pos_p,
@@ -325,7 +332,7 @@ __global__ __launch_bounds__(512) void attn_kernel(const float *__restrict__ qkv
                                                    int n_kv, int group, int max_seq, float scale,
                                                    float *__restrict__ part, int n_chunks,
                                                    unsigned *__restrict__ tickets, float *__restrict__ out,
-                                                   size_t qkv_stride, size_t kv_stride) {
+                                                   size_t qkv_stride, size_t kv_stride, int spec_chunks) {
   constexpr int VD = HD / kWave;          // value columns per lane
   constexpr int NT = 512;
   constexpr int KV4 = kAttnChunk * HD / 4 / NT;   // float4 of K (and of V) per thread
@@ -354,6 +361,13 @@ __global__ __launch_bounds__(512) void attn_kernel(const float *__restrict__ qkv
   const float *kin = qkv + size_t(n_heads) * HD + kvh * HD;
   const float *vin = kin + row;
   const int pos = min(*pos_p, max_seq - 1);
+  // Past the speculative window a chunk learns the position first (an
+  // atomic load: never hoisted above this uniform branch, so the window's
+  // chunks issue their loads without waiting for it).
+  bool skip = false;
+  if (chunk >= spec_chunks)
+    skip = t0 > min(__hip_atomic_load(pos_p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), max_seq - 1);
+  if (!skip) {   // uniform over the workgroup
 
   // ---- every global operand requested before the first wait (one round
   // trip): the chunk's K and V rows, the query head's q, the new key and
@@ -481,6 +495,7 @@ __global__ __launch_bounds__(512) void attn_kernel(const float *__restrict__ qkv
       }
     }
   }
+  }   // !skip
   // ---- ticket: the last workgroup of this KV head merges ----
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
@@ -544,6 +559,10 @@ struct lmx_decoder {
   int n_forced = 0;
   size_t host_pos = 0;
   float pos_div = 1.0f;
+  // Attention chunks that load their K/V rows before the position is known
+  // (LMX_ATTN_SPEC overrides; later chunks wait for the position and load
+  // only when they hold positions).
+  int spec_chunks = 8;
   std::vector<void *> allocs;
   hipStream_t stream = nullptr;   // capture/replay stream of lmx_decoder_generate
 
@@ -629,6 +648,7 @@ int attention(lmx_decoder *d, size_t layer, hipStream_t st) {
   const lmx_decoder_config &c = d->cfg;
   const int group = int(c.n_heads / c.n_kv_heads);
   const int nch = int(attn_chunks(c));
+  const int spec = min(nch, d->spec_chunks);
   const size_t per_layer = size_t(nch) * kAttnChunk * c.n_kv_heads * c.head_dim;
   float *kc = d->kcache + layer * per_layer, *vc = d->vcache + layer * per_layer;
   const float scale = 1.0f / std::sqrt(float(c.head_dim));   // model.cpp:337
@@ -637,11 +657,11 @@ int attention(lmx_decoder *d, size_t layer, hipStream_t st) {
   if (c.head_dim == 64)
     attn_kernel<64><<<grid, dim3(512), 0, st>>>(d->qkv, kc, vc, d->pos, d->freq, d->pos_div, int(c.n_heads),
                                                 int(c.n_kv_heads), group, int(c.max_seq), scale, d->attn_part, nch,
-                                                d->attn_tickets, d->attn_out, qkv_stride, d->kv_seq);
+                                                d->attn_tickets, d->attn_out, qkv_stride, d->kv_seq, spec);
   else
     attn_kernel<128><<<grid, dim3(512), 0, st>>>(d->qkv, kc, vc, d->pos, d->freq, d->pos_div, int(c.n_heads),
                                                  int(c.n_kv_heads), group, int(c.max_seq), scale, d->attn_part, nch,
-                                                 d->attn_tickets, d->attn_out, qkv_stride, d->kv_seq);
+                                                 d->attn_tickets, d->attn_out, qkv_stride, d->kv_seq, spec);
   return launch_err("attention");
 }
 
@@ -670,7 +690,7 @@ int gemv_rows(const lmx_decoder *d, const lmx_weight *w, const float *x, float *
   a.bias = bias;
   a.resid = resid;
   size_t done = 0;
-  int r = gemv_batched(const_cast<lmx_weight *>(w), a, x, y, d->batch, st, &done);
+  int r = gemv_batched(w, a, x, y, d->batch, st, &done);
   if (r) return r;
   a.resid = nullptr;
   for (size_t b = done; b < d->batch; ++b) {
@@ -810,6 +830,7 @@ int lmx_decoder_create_batched(const lmx_decoder_config *cfg, size_t batch, lmx_
   d->batch = batch;
   d->layers.resize(c.n_layers);
   d->pos_div = c.rope_mode == LMX_ROPE_REFERENCE ? c.rope_factor : 1.0f;
+  if (const char *sp = std::getenv("LMX_ATTN_SPEC")) d->spec_chunks = std::max(1, std::atoi(sp));
   const size_t qkv_rows = (c.n_heads + 2 * c.n_kv_heads) * c.head_dim;
   const size_t kv = c.n_layers * attn_chunks(c) * kAttnChunk * c.n_kv_heads * c.head_dim;   // whole chunks
   d->kv_seq = kv;

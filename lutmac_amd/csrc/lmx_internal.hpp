@@ -167,7 +167,7 @@ struct lmx_weight {
   unsigned *d_counters = nullptr;
   float *d_xrot = nullptr;  // staging for LMX_ROTATE_FWHT_FULL (cols floats)
   bool batched = true;           // batch >= 2 through the batched kernel (LMX_BATCHED=0: one GEMV per vector)
-  float *d_bpartials = nullptr;  // batched partials, grown on the first batched call
+  float *d_bpartials = nullptr;  // batched partials [16][Kp/256][Npad], allocated with the handle
   size_t bpartials_cap = 0;      // floats
 };
 
@@ -176,6 +176,7 @@ namespace lmx {
 GemvArgs weight_args(const lmx_weight *w);
 // Vectors x[0..batch) in groups of 16/8/4 through the batched kernel (a.bias
 // per row, a.resid per vector row); *done = the vectors it covered (none
-// below 4).  Grows the handle's batched scratch on first use.
-int gemv_batched(lmx_weight *w, GemvArgs a, const float *x, float *y, size_t batch, void *stream, size_t *done);
+// below 4).
+int gemv_batched(const lmx_weight *w, GemvArgs a, const float *x, float *y, size_t batch, void *stream,
+                 size_t *done);
 }  // namespace lmx

@@ -297,8 +297,10 @@ int lmx_model_load(const char *path, size_t max_seq, lmx_model **out) {
   c.rope_mode = LMX_ROPE_REFERENCE;
   c.rope_factor = float(num_or(*config, "rope_scaling_factor", 1.0));
   if (!(c.rope_factor > 0.0f)) c.rope_factor = 1.0f;                  // format.cpp:331-332
-  c.max_seq = max_seq ? max_seq : size_t(num_or(*config, "max_position_embeddings", 2048));
-  if (c.max_seq == 0) c.max_seq = 2048;
+  // KV capacity: the reference never reads max_position_embeddings back
+  // (format.cpp:321-342), so its cache holds the default 2048 positions
+  // (types.hpp:558, model.hpp:117); a file's 131072 would mean a multi-GB cache.
+  c.max_seq = max_seq ? max_seq : 2048;
   if (!c.vocab || !c.hidden || !c.n_layers || !c.n_heads || !c.n_kv_heads)
     return fail(LMX_ERR_INVALID_ARGUMENT, "incomplete model config in %s", path);
 

@@ -3,11 +3,28 @@
 // implemented over the device C ABI.
 //
 // Every function takes and returns HOST memory exactly like the reference's
-// scalar kernels: activations in, outputs overwritten.  The reference's
-// weights are immutable after load, so the first call with a given block
-// array repacks and uploads it once; later calls reuse the device handle
-// (keyed by block pointer, count, shape and format).  Activations/outputs go
-// through per-thread device staging buffers on a per-thread stream.
+// scalar kernels: activations in, outputs overwritten.  The reference reads
+// its block array on every call (lut_gemm_scalar.cpp:68-180); uploading it
+// per call would cost a PCIe copy of the whole matrix, so the first call with
+// a given block array repacks and uploads it once and later calls reuse the
+// device handle, keyed by (block pointer, count, shape, format) and guarded
+// by a fingerprint of the blocks' contents:
+//   * the fingerprint hashes the count and up to kSampleBlocks whole blocks
+//     spread evenly over the array (first and last included), rechecked on
+//     every call; a mismatch (a freed array whose address now holds another
+//     tensor, or rewritten weights) re-uploads, so no call computes with
+//     weights the caller no longer holds;
+//   * lmx_host_forget(blocks) drops the handles of an array the caller is
+//     about to free or rewrite in part (changes the sample cannot see), and
+//     lmx_host_cache_clear() drops every handle and frees its device memory.
+// A handle's GEMV uses the handle's scratch (split-K partials, tickets), so
+// each cache entry has a mutex that a call holds from the launch through its
+// stream synchronisation: threads sharing one weight are serialised on it,
+// threads on different weights run concurrently (the reference's lut_linear
+// is reentrant per thread, lut_gemm_scalar.cpp:85).  Entries are reference
+// counted, so a replaced or forgotten entry stays alive until its last user
+// returns.  Activations/outputs go through per-thread device staging buffers
+// on a per-thread stream.
 //
 // The reference functions return void and have no error channel; these
 // entry points return an lmx_status, and the C++ wrappers in
@@ -17,6 +34,7 @@
 
 #include <cstring>
 #include <map>
+#include <memory>
 #include <mutex>
 #include <tuple>
 #include <vector>
@@ -28,12 +46,36 @@ namespace {
 
 using Key = std::tuple<const void *, size_t, size_t, size_t, int>;
 
+constexpr size_t kSampleBlocks = 256;
+
+// FNV-1a over the block count and up to kSampleBlocks whole blocks.
+uint64_t fingerprint(const void *blocks, size_t num_blocks, size_t block_bytes) {
+  uint64_t h = 1469598103934665603ull;
+  auto mix = [&h](const uint8_t *p, size_t n) {
+    for (size_t i = 0; i < n; ++i) h = (h ^ p[i]) * 1099511628211ull;
+  };
+  mix(reinterpret_cast<const uint8_t *>(&num_blocks), sizeof num_blocks);
+  const uint8_t *b = static_cast<const uint8_t *>(blocks);
+  const size_t n = num_blocks < kSampleBlocks ? num_blocks : kSampleBlocks;
+  for (size_t i = 0; i < n; ++i) {
+    const size_t j = n > 1 ? i * (num_blocks - 1) / (n - 1) : 0;
+    mix(b + j * block_bytes, block_bytes);
+  }
+  return h;
+}
+
+struct Entry {
+  lmx_weight *w = nullptr;
+  uint64_t print = 0;
+  std::mutex mu;   // held by a call from launch to stream synchronisation
+  ~Entry() {
+    if (w) lmx_weight_destroy(w);
+  }
+};
+
 struct WeightCache {
   std::mutex mu;
-  std::map<Key, lmx_weight *> handles;
-  ~WeightCache() {
-    for (auto &kv : handles) lmx_weight_destroy(kv.second);
-  }
+  std::map<Key, std::shared_ptr<Entry>> handles;
 };
 
 WeightCache &cache() {
@@ -41,20 +83,29 @@ WeightCache &cache() {
   return c;
 }
 
-int get_weight(int fmt, const void *blocks, size_t num_blocks, size_t M, size_t K, lmx_weight **out) {
-  WeightCache &c = cache();
-  std::lock_guard<std::mutex> lock(c.mu);
-  const Key key{blocks, num_blocks, M, K, fmt};
-  auto it = c.handles.find(key);
-  if (it != c.handles.end()) {
-    *out = it->second;
-    return LMX_OK;
-  }
-  lmx_weight *w = nullptr;
-  int st = lmx_weight_from_blocks(fmt, blocks, num_blocks, M, K, &w);
+// The entry for this block array with its contents uploaded; re-uploads when
+// the fingerprint no longer matches.
+int get_weight(int fmt, const void *blocks, size_t num_blocks, size_t M, size_t K, std::shared_ptr<Entry> *out) {
+  size_t bb = 0;
+  int st = lmx_block_bytes(fmt, &bb);
   if (st) return st;
-  c.handles.emplace(key, w);
-  *out = w;
+  const uint64_t fp = fingerprint(blocks, num_blocks, bb);
+  WeightCache &c = cache();
+  const Key key{blocks, num_blocks, M, K, fmt};
+  {
+    std::lock_guard<std::mutex> lock(c.mu);
+    auto it = c.handles.find(key);
+    if (it != c.handles.end() && it->second->print == fp) {
+      *out = it->second;
+      return LMX_OK;
+    }
+  }
+  auto e = std::make_shared<Entry>();
+  if ((st = lmx_weight_from_blocks(fmt, blocks, num_blocks, M, K, &e->w))) return st;
+  e->print = fp;
+  std::lock_guard<std::mutex> lock(c.mu);
+  c.handles[key] = e;   // a replaced entry lives on while a call still holds it
+  *out = e;
   return LMX_OK;
 }
 
@@ -108,12 +159,14 @@ int host_run(int fmt, const void *blocks, size_t num_blocks, const float *bias, 
              size_t M, size_t K, size_t batch, bool linear) {
   if (!blocks || !input || !output) return lmx::fail(LMX_ERR_INVALID_ARGUMENT, "NULL pointer");
   if (M == 0 || K == 0 || batch == 0) return LMX_OK;
-  lmx_weight *w = nullptr;
-  int st = get_weight(fmt, blocks, num_blocks, M, K, &w);
+  std::shared_ptr<Entry> ent;
+  int st = get_weight(fmt, blocks, num_blocks, M, K, &ent);
   if (st) return st;
   if ((st = stage_stream()) || (st = ensure(&g_stage.d_in, &g_stage.n_in, K * batch)) ||
       (st = ensure(&g_stage.d_out, &g_stage.n_out, M * batch)))
     return st;
+  std::lock_guard<std::mutex> use(ent->mu);   // the handle's scratch is this call's until the sync
+  const lmx_weight *w = ent->w;
   const float *d_bias = nullptr;
   if (bias) {
     if ((st = ensure(&g_stage.d_bias, &g_stage.n_bias, M)) || (st = h2d(g_stage.d_bias, bias, M))) return st;
@@ -138,6 +191,21 @@ int lmx_host_gemv(int format, const void *blocks, size_t num_blocks, const float
 int lmx_host_lut_linear(int format, const void *blocks, size_t num_blocks, const float *bias, const float *input,
                         float *output, size_t M, size_t K, size_t batch_size) {
   return host_run(format, blocks, num_blocks, bias, input, output, M, K, batch_size, true);
+}
+
+int lmx_host_forget(const void *blocks) {
+  WeightCache &c = cache();
+  std::lock_guard<std::mutex> lock(c.mu);
+  for (auto it = c.handles.begin(); it != c.handles.end();)
+    it = std::get<0>(it->first) == blocks ? c.handles.erase(it) : std::next(it);
+  return LMX_OK;
+}
+
+int lmx_host_cache_clear(void) {
+  WeightCache &c = cache();
+  std::lock_guard<std::mutex> lock(c.mu);
+  c.handles.clear();
+  return LMX_OK;
 }
 
 int lmx_host_apply_hadamard_rotation(float *data, size_t n) {

@@ -450,8 +450,10 @@ void orc_planes_gemv(int fmt, const uint8_t *planes, const float *scales,
                      size_t M, size_t Kp, size_t G, const float *x, float *y) {
   int S = orc_format_stages(fmt);
   size_t ng = Kp / G;
-  int v[8];
+  /* rows are independent: spread over threads, each row's sum unchanged */
+#pragma omp parallel for schedule(static)
   for (size_t r = 0; r < M; ++r) {
+    int v[8];
     float acc = 0.0f;
     for (int st = 0; st < S; ++st) {
       const float *sc = scales + ((size_t)st * M + r) * ng;
@@ -528,8 +530,8 @@ int orc_decode_step(const orc_model *m, int token, size_t pos, float *logits) {
   if (pos >= m->max_seq || token < 0 || (size_t)token >= m->vocab) return -1;
   float *hs = malloc(h * 4), *nrm = malloc(h * 4), *qkv = malloc((qd + 2 * kvd) * 4);
   float *att = malloc(qd * 4), *tmp = malloc(h * 4), *gu = malloc(2 * ffn * 4);
-  float *inter = malloc(ffn * 4), *w = malloc((pos + 1) * 4);
-  if (!hs || !nrm || !qkv || !att || !tmp || !gu || !inter || !w) return -2;
+  float *inter = malloc(ffn * 4), *wall = malloc(nh * (pos + 1) * 4);
+  if (!hs || !nrm || !qkv || !att || !tmp || !gu || !inter || !wall) return -2;
 
   /* embedding row (model.cpp:58-85, per-group scales of the tied table) */
   {
@@ -557,7 +559,10 @@ int orc_decode_step(const orc_model *m, int token, size_t pos, float *logits) {
     memcpy(kc + pos * kvd, qkv + qd, kvd * 4);
     memcpy(vc + pos * kvd, qkv + qd + kvd, kvd * 4);
     memset(att, 0, qd * 4);
+    /* heads are independent (own score row w[hh], own output slice) */
+#pragma omp parallel for schedule(static)
     for (size_t hh = 0; hh < nh; ++hh) { /* model.cpp:341-372 */
+      float *w = wall + hh * (pos + 1);
       size_t kvh = hh / group;
       const float *q = qkv + hh * hd;
       for (size_t t = 0; t <= pos; ++t) {
@@ -587,6 +592,6 @@ int orc_decode_step(const orc_model *m, int token, size_t pos, float *logits) {
   }
   rms_norm(hs, m->final_norm, nrm, h, m->rms_eps);
   linear(&m->head, nrm, logits);
-  free(hs); free(nrm); free(qkv); free(att); free(tmp); free(gu); free(inter); free(w);
+  free(hs); free(nrm); free(qkv); free(att); free(tmp); free(gu); free(inter); free(wall);
   return 0;
 }

@@ -110,3 +110,67 @@ def test_cpp_dropins_compile_and_run(cuda):
     print(r.stdout)
     assert r.returncode == 0, r.stdout + r.stderr
     assert "0 failure(s)" in r.stdout
+
+
+def random_int4_blocks(M, K, seed):
+    """M * ceil(K/256) Int4Blocks (types.hpp:174-202): random nibbles, scale |N(0,1)|*0.02."""
+    rng = np.random.default_rng(seed)
+    nb = M * ((K + 255) // 256)
+    blk = rng.integers(0, 256, (nb, 132), dtype=np.uint8)
+    blk[:, 128:] = (np.abs(rng.standard_normal(nb)) * 0.02).astype(np.float32).view(np.uint8).reshape(nb, 4)
+    return blk.reshape(-1)
+
+
+def test_weight_cache_sees_rewritten_blocks(cuda):
+    # one host buffer, new contents in place (a freed PackedTensor's address
+    # reused by another tensor of the same shape): the new weights are used
+    M, K = 64, 512
+    buf = random_int4_blocks(M, K, 1)
+    x = np.random.default_rng(2).standard_normal(K).astype(np.float32)
+    y1 = L.host_gemv(6, buf, x, M, K)
+    assert rel_max_err(y1, oracle.block_gemv(6, buf, x, M, K)) < TOL
+    buf[:] = random_int4_blocks(M, K, 3)
+    y2 = L.host_gemv(6, buf, x, M, K)
+    assert rel_max_err(y2, oracle.block_gemv(6, buf, x, M, K)) < TOL
+    assert not np.array_equal(y1, y2)
+
+
+def test_weight_cache_forget(cuda):
+    # more blocks than the fingerprint samples: a change to one unsampled block
+    # is the caller's to announce with lmx_host_forget
+    M, K = 512, 1024
+    buf = random_int4_blocks(M, K, 4)
+    x = np.random.default_rng(5).standard_normal(K).astype(np.float32)
+    L.host_gemv(6, buf, x, M, K)
+    blk = buf.reshape(-1, 132)
+    blk[777, :128] ^= 0x5A   # row 194
+    L.host_forget(buf)
+    y = L.host_gemv(6, buf, x, M, K)
+    assert rel_max_err(y, oracle.block_gemv(6, buf, x, M, K)) < TOL
+    L.host_cache_clear()
+    assert rel_max_err(L.host_gemv(6, buf, x, M, K), y) == 0.0
+
+
+def test_weight_cache_threads(cuda):
+    # two threads on one cached weight (serialised on its scratch) and a third
+    # on another weight: every result equals the single-threaded one
+    import threading
+    M, K = 1024, 2048   # split-K / full-K scratch in use
+    bufs = [random_int4_blocks(M, K, 6), random_int4_blocks(M, K, 7)]
+    xs = [np.random.default_rng(10 + i).standard_normal(K).astype(np.float32) for i in range(6)]
+    want = {(b, i): L.host_gemv(6, bufs[b], xs[i], M, K) for b in range(2) for i in range(6)}
+    bad = []
+
+    def run(b, seed):
+        order = np.random.default_rng(seed).integers(0, 6, 40)
+        for i in order:
+            y = L.host_gemv(6, bufs[b], xs[i], M, K)
+            if not np.array_equal(y, want[(b, int(i))]):
+                bad.append((b, int(i)))
+
+    ts = [threading.Thread(target=run, args=(b, s)) for b, s in [(0, 1), (0, 2), (1, 3)]]
+    for t in ts:
+        t.start()
+    for t in ts:
+        t.join()
+    assert not bad, bad[:5]

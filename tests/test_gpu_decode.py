@@ -246,3 +246,81 @@ def test_batched_generate_graph_equals_eager_and_oracle(cuda):
             lg = o.step(out[b, pos], pos)
             if pos + 1 >= n_prompt:
                 assert lg[out[b, pos + 1]] >= lg.max() - DECODE_TOL * np.linalg.norm(lg)
+
+
+# ---- BASELINE config 5 code paths: long KV context, batch 16, full Qwen ------
+def check_positions(dec, ref, tokens, check_from, tol=DECODE_TOL):
+    """Teacher-forced run over all of `tokens`; logits compared from position
+    `check_from` on (earlier steps only fill both KV caches)."""
+    dec.reset(tokens)
+    lg = torch.empty(dec.cfg.vocab, dtype=torch.float32, device="cuda")
+    for pos, t in enumerate(tokens):
+        want = ref.step(t, pos)
+        if pos < check_from:
+            dec.step()
+            continue
+        dec.step(lg)
+        err = rel_max_err(lg.cpu().numpy(), want)
+        assert err < tol, f"step {pos}: rel err {err:.3e}"
+
+
+def qwen_small(**kw):
+    # Qwen-2.5 attention geometry (head_dim 128, 12 query / 2 KV heads, QKV bias)
+    base = dict(hidden=256, n_layers=1, n_heads=12, n_kv_heads=2, head_dim=128, ffn=512, vocab=512,
+                rope_mode=D.ROPE_REFERENCE, rope_factor=1.0, rope_theta=1e6, rms_eps=1e-6, qkv_bias=True)
+    base.update(kw)
+    return D.small_config(**base)
+
+
+@pytest.mark.parametrize("spec", [8, 1])
+def test_decoder_past_512_positions(cuda, monkeypatch, spec):
+    # 600 positions = 10 attention chunks: the merge takes its 32-chunk batch
+    # (merge_pass<128, 32>), and chunks past the speculative window (LMX_ATTN_SPEC)
+    # wait for the position and skip their loads while they lie past it.
+    monkeypatch.setenv("LMX_ATTN_SPEC", str(spec))
+    cfg = qwen_small(max_seq=640)
+    m = D.SyntheticModel(cfg, seed=51, group=128, random_norms=True)
+    toks = np.random.default_rng(52).integers(0, cfg.vocab, 600)
+    check_positions(D.Decoder(m), oracle.OracleDecoder(m), toks, check_from=0)
+
+
+def test_decoder_past_4096_positions(cuda):
+    # 4112 positions = 65 chunks: two passes of the merge (64 chunks, then 1)
+    cfg = qwen_small(n_heads=4, n_kv_heads=2, vocab=256, max_seq=4160)
+    m = D.SyntheticModel(cfg, seed=53, group=128, random_norms=True)
+    toks = np.random.default_rng(54).integers(0, cfg.vocab, 4112)
+    check_positions(D.Decoder(m), oracle.OracleDecoder(m), toks, check_from=4030)
+
+
+def test_batched_decoder_batch16_past_512(cuda):
+    # batch 16 = one full group of the batched GEMV, with the attention of every
+    # sequence past 512 positions (32-chunk merge)
+    cfg = qwen_small(max_seq=576)
+    m = D.SyntheticModel(cfg, seed=55, group=128, random_norms=True)
+    B, n = 16, 530
+    toks = np.random.default_rng(56).integers(0, cfg.vocab, (B, n))
+    dec = D.Decoder(m, batch=B)
+    dec.reset(toks)
+    lg = torch.empty(B * cfg.vocab, dtype=torch.float32, device="cuda")
+    refs = [oracle.OracleDecoder(m) for _ in range(B)]
+    for pos in range(n):
+        dec.step(lg)
+        if pos % 8 and pos < n - 4:   # every sequence's KV cache is filled; logits checked on a subset
+            for b in range(B):
+                refs[b].step(toks[b, pos], pos)
+            continue
+        got = lg.cpu().numpy().reshape(B, cfg.vocab)
+        for b in range(B):
+            err = rel_max_err(got[b], refs[b].step(toks[b, pos], pos))
+            assert err < DECODE_TOL, f"sequence {b} step {pos}: rel err {err:.3e}"
+
+
+def test_qwen_1_5b_architecture_steps(cuda):
+    # BASELINE config 5's model at full size: 28 layers, hidden 1536, QKV bias,
+    # GQA 12/2 with head_dim 128, FFN 8960 (down projection split-K at K = 8960),
+    # tied 151936 x 1536 head (split-K at K = 1536)
+    cfg = D.QWEN_2_5_1_5B
+    m = D.SyntheticModel(cfg, seed=57, group=128)
+    toks = np.random.default_rng(58).integers(0, cfg.vocab, 2)
+    print("qwen model built", flush=True)
+    check_against(D.Decoder(m), oracle.OracleDecoder(m), toks)
