@@ -9,15 +9,23 @@ other formats of the sweep are reported beside it, ternary and the 1-2 bit
 formats with the FWHT fused into the kernel as lut_linear applies it, and
 int4 with the rotation fused in as "int4_rot".  Weights
 rotate over >= 512 MiB of distinct device copies so neither the 256 MB MALL
-nor the L2 holds them between launches.  The timed region is bracketed by
-torch.cuda.synchronize() and HIP events recorded on the stream the kernels
-are launched on; value = algorithmic bytes per GEMV / average time per GEMV.
-The K timed GEMVs are captured in one HIP graph and replayed (the launch
-path of a captured decode step); the per-launch stream time is reported
-beside it (--no-graph times only that).
+nor the L2 holds them between launches.  The K timed GEMVs are captured in
+one HIP graph (the launch path of a captured decode step), replayed once
+untimed and then --replays times, each replay after a 1 GiB HBM flush and
+bracketed by torch.cuda.synchronize() and HIP events recorded on the stream
+the graph is launched on; value = algorithmic bytes per GEMV / (median
+replay time / K).  The per-launch stream time is reported beside it
+(--no-graph times only that).  BASELINE configs 1 and 2 are timed the same
+way at their own shapes ("configs"), and a 1 GiB device copy and read give
+the achievable-bandwidth yardstick ("achievable_bandwidth").
+
+The reference's own lut_linear (built from its sources, oracle/_ref) is
+timed on the host for int4, ternary (1 thread each) and binary (its
+ThreadPool), with the CPU model and core counts ("cpu_baselines").
 
 Beside it, the metric's second half: batch-1 greedy decode tokens/s of a
-random-init Llama-3.2-1B architecture in "decode".
+random-init Llama-3.2-1B architecture in "decode", and
+the Qwen-2.5-1.5B architecture at batch 1/4/16 (config 5) in "qwen_decode".
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--formats int4,ternary,...]
 """
@@ -156,65 +164,135 @@ def config_rows(L, synth, torch, steps, warmup, flush):
     return rows
 
 
-def copy_bandwidth(torch, nbytes=2**30, reps=20):
-    """Achievable HBM bandwidth yardsticks on this GPU: a device-to-device
-    copy of 1 GiB (torch's copy kernel, bytes read + written per second) and
-    a read-only reduction of the same buffer (torch's sum)."""
-    a = torch.empty(nbytes // 4, dtype=torch.float32, device="cuda").fill_(1.0)
-    b = torch.empty_like(a)
-    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+def achievable_bandwidth(torch, L, sizes, steps, flush, replays=7):
+    """The achievable-bandwidth yardstick at each GEMV size: a plain streaming
+    read of the same number of bytes (lmx_hbm_read_probe), timed exactly like
+    the GEMVs (steps launches over >= 512 MiB of distinct buffers in one HIP
+    graph, replayed after a flush, median), plus a 1 GiB read and torch's
+    1 GiB device copy for scale."""
     out = {}
-    for name, fn, moved in (("copy", lambda: b.copy_(a), 2 * nbytes), ("read", lambda: a.sum(), nbytes)):
-        fn()
+    sink = torch.zeros(4, dtype=torch.int32, device="cuda")
+    stream = torch.cuda.current_stream()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    for name, nbytes in sizes.items():
+        nbytes = nbytes // 16 * 16
+        copies = max(2, -(-ROTATE_BYTES // nbytes))
+        bufs = [torch.ones(nbytes // 4, dtype=torch.float32, device="cuda") for _ in range(copies)]
+        n = steps if nbytes < 2**28 else 3
+        cg = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream()
+        side.wait_stream(stream)
+        with torch.cuda.graph(cg, stream=side):
+            for i in range(n):
+                L.hbm_read_probe(bufs[i % copies], sink)
+        stream.wait_stream(side)
+        cg.replay()
         torch.cuda.synchronize()
         ts = []
-        for _ in range(reps):
-            s.record()
-            fn()
-            e.record()
+        for _ in range(replays):
+            flush()
             torch.cuda.synchronize()
-            ts.append(s.elapsed_time(e))
+            s.record(stream)
+            cg.replay()
+            e.record(stream)
+            torch.cuda.synchronize()
+            ts.append(s.elapsed_time(e) / n)
         ms = float(np.median(ts))
-        out[name] = {"GB_per_s": round(moved / (ms * 1e-3) / 1e9, 1), "bytes": moved, "ms": round(ms, 4)}
-    out["note"] = ("achievable-bandwidth yardstick: median of %d launches on a 1 GiB buffer; copy counts bytes "
-                   "read + written" % reps)
+        out[name] = {"bytes": nbytes, "us_per_read": round(ms * 1e3, 3),
+                     "GB_per_s": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                     "frac_of_peak": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}
+        del cg, bufs
+    a = torch.empty(2**28, dtype=torch.float32, device="cuda").fill_(1.0)
+    b = torch.empty_like(a)
+    b.copy_(a)
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(replays):
+        s.record()
+        b.copy_(a)
+        e.record()
+        torch.cuda.synchronize()
+        ts.append(s.elapsed_time(e))
+    ms = float(np.median(ts))
+    out["torch_copy_1GiB"] = {"bytes_moved": 2 * 2**30, "GB_per_s": round(2 * 2**30 / (ms * 1e-3) / 1e9, 1)}
+    out["note"] = ("plain streaming read of the same bytes (no arithmetic), timed like the GEMVs: what the "
+                   "memory system delivers per launch at that size; frac_of_achievable in the sweep = GEMV "
+                   "GB/s / this")
     del a, b
     return out
 
 
-def cpu_baseline(n, budget_s=10.0):
-    """The reference's own int4_gemv (oracle/_ref, scalar, 1 thread) on the
-    same n x n 4-bit GEMV, in its native 256-weight blocks, for ~budget_s."""
+def host_cpu():
+    """CPU model and core counts of the host the CPU baselines run on."""
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except AttributeError:
+        affinity = os.cpu_count()
+    return {"model": model, "nproc": affinity, "hardware_concurrency": os.cpu_count()}
+
+
+# Reference CPU operators timed beside the GPU: (format, block bytes, threads).
+# The reference's x86 lut_linear runs int4 and ternary single-threaded and
+# binary on its ThreadPool of hardware_concurrency threads
+# (lut_gemm_scalar.cpp:186-222, 7-61, 228-259; thread_pool.hpp:15-16).
+CPU_FORMATS = {"int4": (6, "1"), "ternary": (1, "1"), "binary": (2, "pool")}
+
+
+def cpu_baselines(n, budget_s=8.0):
+    """The reference's own lut_linear (oracle/_ref/libref.so, built from its
+    sources with its flags) on the n x n GEMV of each format in CPU_FORMATS, in
+    its native 256-weight blocks (ternary with the row scale in every block,
+    binary and int4 with per-256 scales), repeated for ~budget_s each; the
+    C restatement (oracle, 1 thread) where the reference build is absent."""
     import oracle
+    import lutmac_amd as L
     from lutmac_amd import synth
-    rng = np.random.default_rng(7)
-    bpr = n // 256
-    nb = n * bpr
-    blocks = np.empty((nb, 132), np.uint8)
-    blocks[:, :128] = rng.integers(0, 256, (nb, 128), dtype=np.uint8)
-    blocks[:, 128:] = (np.abs(rng.standard_normal(nb)) * 0.02).astype(np.float32).view(np.uint8).reshape(nb, 4)
-    blocks = blocks.ravel()
-    x = synth.make_activations(n, seed=5)
-    y = np.zeros(n, np.float32)
     R = oracle.ref()
-    kind = "reference" if R is not None else "port"
-    reps, t0 = 0, time.perf_counter()
-    while True:
-        if R is not None:
-            R.ref_gemv(6, oracle._ptr(blocks), nb, oracle._ptr(x), oracle._ptr(y), n, n)
-        else:
-            oracle.lib().orc_int4_gemv(oracle._ptr(blocks), oracle._ptr(x), oracle._ptr(y), n, n)
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= budget_s:
-            break
-    t = el / reps
-    B = synth.algorithmic_bytes(6, n, n, group=256)
-    return {"value": round(B / t / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": kind,
-            "sample": (f"{'oracle/_ref int4_gemv (reference lut_gemm_scalar.cpp:186-222)' if R else 'oracle int4 port'}"
-                       f" {n}x{n} batch 1, native 256-weight blocks, {reps} GEMVs in {el:.1f} s"
-                       f" ({t * 1e3:.1f} ms each), 1 thread"),
-            "ms_per_gemv": round(t * 1e3, 2)}
+    cpu = host_cpu()
+    out = {}
+    x = synth.make_activations(n, seed=5)
+    for name, (fmt, threads) in CPU_FORMATS.items():
+        planes, scales, _ = synth.make_weights(fmt, n, n, seed=3000 + fmt, group=256 if fmt != 1 else 0)
+        if fmt == 1:   # one row scale, replicated into every block
+            scales = np.repeat(scales.reshape(1, n, 1), n // 256, axis=2)
+        blocks = L.planes_to_blocks(fmt, planes, scales, n, n)
+        del planes
+        nb = n * (n // 256)
+        y = np.zeros(n, np.float32)
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            if R is not None:
+                R.ref_lut_linear(fmt, oracle._ptr(blocks), nb, None, oracle._ptr(x), oracle._ptr(y), n, n, 1)
+            else:
+                oracle.lut_linear(fmt, blocks, x, n, n)
+            reps += 1
+            el = time.perf_counter() - t0
+            if el >= budget_s:
+                break
+        t = el / reps
+        B = synth.algorithmic_bytes(fmt, n, n, group=256)
+        cores = (cpu["hardware_concurrency"] if threads == "pool" else 1) if R is not None else 1
+        out[name] = {"value": round(B / t / 1e9, 4), "unit": "GB/s", "cores": cores,
+                     "kind": "reference" if R is not None else "port",
+                     "ms_per_gemv": round(t * 1e3, 2),
+                     "sample": (f"{'oracle/_ref lut_linear (reference lut_gemm_scalar.cpp:68-180)' if R else 'oracle port'}"
+                                f" {L.FORMAT_NAMES[fmt]} {n}x{n} batch 1, native 256-weight blocks, {reps} GEMVs in "
+                                f"{el:.1f} s ({t * 1e3:.1f} ms each), "
+                                + ("1 thread" if cores == 1 else
+                                   f"the reference ThreadPool of {cores} threads on {cpu['nproc']} usable CPUs"))}
+    for v in out.values():
+        v["cpu"] = cpu["model"]
+        v["nproc"] = cpu["nproc"]
+    return out
 
 
 def decode_weight_bytes(cfg, group):
@@ -416,7 +494,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--size", type=int, default=8192)
     ap.add_argument("--formats", default="int4,ternary,binary,rrq2,rrq3,int8,int4_rot")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-seconds", type=float, default=8.0, help="CPU baseline budget per format")
+    ap.add_argument("--replays", type=int, default=7, help="timed graph replays (median reported)")
+    ap.add_argument("--no-configs", action="store_true", help="skip the BASELINE config 1/2 shape rows")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true", help="skip the 1B-architecture decode")
     ap.add_argument("--no-batched", action="store_true", help="skip the Qwen-shape batch 1/4/16 sweep")
@@ -445,14 +525,35 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs a GPU"
 
     names = [f for f in args.formats.split(",") if f]
+    flush = Flush(torch)
     sweep = {}
     for name in names:
         r = gemv_bench(L, synth, torch, FORMATS[name], args.size, args.steps, args.warmup,
-                       graph=not args.no_graph, rotate_in_kernel=name in ROTATE_IN_KERNEL)
+                       graph=not args.no_graph, rotate_in_kernel=name in ROTATE_IN_KERNEL, flush=flush,
+                       replays=args.replays)
         sweep[name] = r
         print(f"# {name}: {r['us_per_gemv']} us/GEMV, {r['GB_per_s']} GB/s "
               f"({100 * r['frac_of_peak']:.1f}% of peak)", file=sys.stderr, flush=True)
     head = sweep.get("int4") or sweep[names[0]]
+    configs = None
+    if not args.no_configs:
+        configs = config_rows(L, synth, torch, args.steps, args.warmup, flush)
+        for k, r in configs.items():
+            print(f"# {k}: {r['us_per_gemv']} us/GEMV, {r['GB_per_s']} GB/s "
+                  f"({100 * r['frac_of_peak']:.1f}% of peak)", file=sys.stderr, flush=True)
+    read_sizes = {f"{k}_{args.size}": v["algorithmic_bytes"] for k, v in sweep.items()}
+    if configs:
+        read_sizes.update({k: v["algorithmic_bytes"] for k, v in configs.items()})
+    read_sizes["1GiB"] = 2**30
+    achievable = achievable_bandwidth(torch, L, read_sizes, args.steps, flush, replays=args.replays)
+    for k, r in list(sweep.items()) + list((configs or {}).items()):
+        key = f"{k}_{args.size}" if k in sweep else k
+        r["read_probe_us"] = achievable[key]["us_per_read"]
+        r["frac_of_achievable"] = round(r["GB_per_s"] / achievable[key]["GB_per_s"], 4)
+    print("# achievable (plain read of the same bytes): " + ", ".join(
+        f"{k} {v['us_per_read']} us ({v['GB_per_s']} GB/s)" for k, v in achievable.items() if "us_per_read" in v),
+        file=sys.stderr, flush=True)
+    del flush
     decode = None
     if not args.no_decode:
         decode = decode_bench(args.decode_prompt, args.decode_tokens)
@@ -469,7 +570,11 @@ def main():
         print("# batched linears per step: " + ", ".join(
             f"bs {b}: {v['linears_us_per_step']} us" for b, v in batched["per_batch"].items()),
             file=sys.stderr, flush=True)
-    cpu = None if args.no_cpu else cpu_baseline(args.size, args.cpu_seconds)
+    cpus = None if args.no_cpu else cpu_baselines(args.size, args.cpu_seconds)
+    cpu = None if cpus is None else cpus["int4" if head["format"] == "int4" else head["format"]]
+    if cpus is not None:
+        print("# cpu: " + ", ".join(f"{k} {v['ms_per_gemv']} ms/GEMV ({v['cores']} threads)"
+                                    for k, v in cpus.items()), file=sys.stderr, flush=True)
     if decode is not None and not args.no_cpu:
         decode["cpu_baseline"] = cpu_decode_baseline(args.cpu_decode_seconds)
     line = {
@@ -492,8 +597,13 @@ def main():
                    "rotated_MiB": head["rotated_MiB"]},
         "roofline": {"bound": "hbm", "achieved": head["GB_per_s"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": head["frac_of_peak"],
-                     "traffic": load_traffic(f"{head['format']}_{args.size}")},
+                     "traffic": load_traffic(f"{head['format']}_{args.size}"),
+                     "achievable_read_GB_s": round(head["GB_per_s"] / head["frac_of_achievable"], 1),
+                     "frac_of_achievable": head["frac_of_achievable"]},
         "cpu_baseline": cpu,
+        "cpu_baselines": cpus,
+        "achievable_bandwidth": achievable,
+        "configs": configs,
         "decode": decode,
         "qwen_decode": qwen,
         "batched_qwen_linears": batched,

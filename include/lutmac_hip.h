@@ -169,6 +169,16 @@ int lmx_extract_indices(const uint8_t *sign_plane, const uint8_t *zero_plane,
                         size_t n_groups, uint8_t *pos_idx, uint8_t *neg_idx,
                         void *stream);
 
+/* ---- measurement -------------------------------------------------------*/
+/* Achievable-bandwidth yardstick: one plain streaming read of `bytes` device
+ * bytes at `buf` (16-byte aligned, a multiple of 16), asynchronous on
+ * `stream`; `sink` is a device word it may write.  Timing it beside a GEMV
+ * of the same bytes gives the GEMV's fraction of what the memory system
+ * delivers at that size.  No reference counterpart (the reference has no
+ * device and no roofline). */
+int lmx_hbm_read_probe(const void *buf, size_t bytes, unsigned *sink,
+                       void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -33,7 +33,7 @@ EXPORTS = [
     "lmx_tile_bytes", "lmx_tile_planes", "lmx_untile_planes",
     "lmx_weight_create", "lmx_weight_from_blocks", "lmx_weight_destroy", "lmx_weight_info",
     "lmx_weight_kernel_config", "lmx_weight_read_tiles", "lmx_gemv", "lmx_linear", "lmx_fwht256",
-    "lmx_precompute_luts", "lmx_extract_indices",
+    "lmx_precompute_luts", "lmx_extract_indices", "lmx_hbm_read_probe",
     # include/lutmac_hip_compat.h
     "lmx_host_gemv", "lmx_host_lut_linear", "lmx_host_apply_hadamard_rotation",
     "lmx_host_precompute_luts", "lmx_host_forget", "lmx_host_cache_clear",
@@ -97,6 +97,7 @@ _SIGS = {
     "lmx_host_lut_linear": ([_i, _p, _sz, _p, _p, _p, _sz, _sz, _sz], _i),
     "lmx_host_apply_hadamard_rotation": ([_p, _sz], _i),
     "lmx_host_forget": ([_p], _i),
+    "lmx_hbm_read_probe": ([_p, _sz, _p, _p], _i),
     "lmx_host_cache_clear": ([], _i),
     "lmx_quantize_int4": ([_p, _sz, _sz, _sz, _p, _p], _i),
     "lmx_synth_int4_normal": ([ctypes.c_uint64, ctypes.c_uint64, _sz, _sz, ctypes.c_float, _sz, _p, _p], _i),
@@ -322,6 +323,13 @@ def fwht256(x, stream=None):
     """In-place blockwise FWHT-256 of a device tensor."""
     check(lib().lmx_fwht256(_dev_ptr(x), x.numel(), _stream_ptr(stream)))
     return x
+
+
+def hbm_read_probe(buf, sink, stream=None):
+    """One plain streaming read of a device tensor (the achievable-bandwidth
+    yardstick, lmx_hbm_read_probe); sink: a device int32 tensor."""
+    check(lib().lmx_hbm_read_probe(_dev_ptr(buf), buf.numel() * buf.element_size(), _dev_ptr(sink),
+                                   _stream_ptr(stream)))
 
 
 def precompute_luts(x, rotate=False, stream=None):
