@@ -116,6 +116,13 @@ int lmx_tile_planes(int format, const uint8_t *planes, size_t rows,
 /* Inverse of lmx_tile_planes. */
 int lmx_untile_planes(int format, const uint8_t *tiles, size_t rows,
                       size_t cols, uint8_t *planes);
+/* Canonical scales [S][rows][ceil(cols/group)] (group as in lmx_planes_desc)
+ * -> the device scale layout [S][n_groups][Npad] fp32 (n_groups = Kp/group,
+ * or 1 per row; padded rows and groups 0).  With out == NULL only *bytes is
+ * set to the layout's size; otherwise *bytes must equal it.  No reference
+ * counterpart (the reference keeps one scale inside each block). */
+int lmx_tile_scales(int format, const float *scales, size_t rows, size_t cols,
+                    size_t group, float *out, size_t *bytes);
 
 /* ---- weights ------------------------------------------------------------*/
 /* Repack + upload canonical planes (BASELINE synthetic formats). */
@@ -168,6 +175,25 @@ int lmx_precompute_luts(const float *x, size_t n, unsigned flags, float *luts,
 int lmx_extract_indices(const uint8_t *sign_plane, const uint8_t *zero_plane,
                         size_t n_groups, uint8_t *pos_idx, uint8_t *neg_idx,
                         void *stream);
+
+/* The GEMV of lmx_gemv without a weight handle, for callers that cannot
+ * allocate: code under HIP graph capture, serving loops with a fixed memory
+ * budget.  No counterpart in the reference.  Weights are the caller's DEVICE
+ * buffers: tiles in the lmx_tile_planes layout (16-byte aligned), scales in
+ * the lmx_tile_scales layout; format, rows, cols, group, x, y, batch, flags
+ * and stream mean what they mean for lmx_gemv, with the same kernel plan, so
+ * y is bit-identical to lmx_gemv's (batches run one vector at a time).  It
+ * allocates nothing: the split-K partials, ticket counters and the staging
+ * copy of x live in an 8 MiB device array that each GPU holds until the
+ * process ends; shapes needing more (counters Npad/64*4 B + staging Kp*4 B +
+ * split-K partials (Kp/kslice)*Npad*4 B) return LMX_ERR_INVALID_ARGUMENT.
+ * The first call on a device looks the array up and zeroes it (a kernel on
+ * `stream`): make it outside graph capture.  Calls on one GPU share the
+ * array: calls that overlap in time on one GPU race, so order them. */
+int lmx_gemv_tiles_noalloc(int format, const void *tiles, const float *scales,
+                           size_t rows, size_t cols, size_t group,
+                           const float *x, float *y, size_t batch,
+                           unsigned flags, void *stream);
 
 /* ---- measurement -------------------------------------------------------*/
 /* Achievable-bandwidth yardstick: one plain streaming read of `bytes` device

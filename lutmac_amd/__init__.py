@@ -30,7 +30,7 @@ OK, ERR_INVALID_ARGUMENT, ERR_UNSUPPORTED_FORMAT, ERR_NO_DEVICE, ERR_OUT_OF_MEMO
 EXPORTS = [
     "lmx_status_string", "lmx_last_error", "lmx_device_count", "lmx_version",
     "lmx_format_info", "lmx_block_bytes", "lmx_blocks_to_planes", "lmx_planes_to_blocks",
-    "lmx_tile_bytes", "lmx_tile_planes", "lmx_untile_planes",
+    "lmx_tile_bytes", "lmx_tile_planes", "lmx_untile_planes", "lmx_tile_scales", "lmx_gemv_tiles_noalloc",
     "lmx_weight_create", "lmx_weight_from_blocks", "lmx_weight_destroy", "lmx_weight_info",
     "lmx_weight_kernel_config", "lmx_weight_read_tiles", "lmx_gemv", "lmx_linear", "lmx_fwht256",
     "lmx_precompute_luts", "lmx_extract_indices", "lmx_hbm_read_probe",
@@ -98,6 +98,8 @@ _SIGS = {
     "lmx_host_apply_hadamard_rotation": ([_p, _sz], _i),
     "lmx_host_forget": ([_p], _i),
     "lmx_hbm_read_probe": ([_p, _sz, _p, _p], _i),
+    "lmx_tile_scales": ([_i, _p, _sz, _sz, _sz, _p, ctypes.POINTER(_sz)], _i),
+    "lmx_gemv_tiles_noalloc": ([_i, _p, _p, _sz, _sz, _sz, _p, _p, _sz, _u, _p], _i),
     "lmx_host_cache_clear": ([], _i),
     "lmx_quantize_int4": ([_p, _sz, _sz, _sz, _p, _p], _i),
     "lmx_synth_int4_normal": ([ctypes.c_uint64, ctypes.c_uint64, _sz, _sz, ctypes.c_float, _sz, _p, _p], _i),
@@ -193,6 +195,24 @@ def planes_to_blocks(fmt, planes, scales, rows, cols):
     check(lib().lmx_planes_to_blocks(fmt, _np_ptr(planes), _np_ptr(scales), rows, cols,
                                      _np_ptr(out), nb))
     return out
+
+
+def tile_scales(fmt, scales, rows, cols, group):
+    """Canonical scales [S, rows, groups] -> the device scale layout (lmx_tile_scales)."""
+    n = ctypes.c_size_t()
+    check(lib().lmx_tile_scales(fmt, None, rows, cols, group, None, ctypes.byref(n)))
+    out = np.zeros(n.value // 4, np.float32)
+    sc = np.ascontiguousarray(scales, np.float32)
+    check(lib().lmx_tile_scales(fmt, _np_ptr(sc), rows, cols, group, _np_ptr(out), ctypes.byref(n)))
+    return out
+
+
+def gemv_tiles_noalloc(fmt, tiles, scales, rows, cols, group, x, y, batch=1, flags=ROTATE_NONE, stream=None):
+    """lmx_gemv_tiles_noalloc on device tensors (tiles uint8, scales fp32 in the
+    device layouts, x [batch*cols], y [batch*rows])."""
+    check(lib().lmx_gemv_tiles_noalloc(fmt, _dev_ptr(tiles), _dev_ptr(scales), rows, cols, group, _dev_ptr(x),
+                                       _dev_ptr(y), batch, flags, _stream_ptr(stream)))
+    return y
 
 
 def tile_bytes(fmt, rows, cols):

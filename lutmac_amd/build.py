@@ -26,6 +26,7 @@ DEVICE = ["-x", "hip", f"--offload-arch={ARCH}",
 SOURCES = [
     ("lmx_kernels.hip", True),
     ("lmx_probe.hip", True),
+    ("lmx_noalloc.hip", True),
     ("lmx_decode.hip", True),
     ("lmx_capi.cpp", False),
     ("lmx_repack.cpp", False),

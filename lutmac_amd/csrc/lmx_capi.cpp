@@ -4,6 +4,7 @@
 // thread-local message.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -126,6 +127,34 @@ int choose_reduce() {
   return (env == kReduceTwoPass || env == kReduceFenceAll) ? env : kReduceTicket;
 }
 
+}  // namespace
+
+void plan_weight(lmx_weight *w, int fmt, size_t rows, size_t cols, size_t group) {
+  FormatInfo fi;
+  format_info(fmt, &fi);
+  w->format = fmt;
+  w->rows = rows;
+  w->cols = cols;
+  w->Npad = round_up(rows, kWave);
+  w->Kp = round_up(cols, kRotChunk);
+  w->group = group ? group : w->Kp;
+  w->n_groups = (w->Kp + w->group - 1) / w->group;
+  w->tile_bytes = (w->Kp / kChunk) * fi.planes * w->Npad * 16;
+  w->scale_bytes = size_t(fi.stages) * w->n_groups * w->Npad * sizeof(float);
+  w->waves = choose_waves();
+  w->kslice = choose_kslice(w->Npad, w->Kp, w->waves);
+  w->reduce = choose_reduce();
+  {
+    const int fam = env_int("LMX_KERNEL", kKernelAuto);
+    w->kfamily = (fam == kKernelGeneric || fam == kKernelLean) ? fam : kKernelAuto;
+  }
+  w->fullk = choose_fullk(fmt, w->Npad, w->Kp, w->kfamily);
+  w->staged = choose_staged();
+  w->batched = env_int("LMX_BATCHED", 1) != 0;
+}
+
+namespace {
+
 void free_weight(lmx_weight *w) {
   if (!w) return;
   if (w->d_planes) (void)hipFree(w->d_planes);
@@ -148,26 +177,8 @@ int upload(int fmt, size_t rows, size_t cols, size_t group, const uint8_t *plane
   if (st) return st;
   lmx_weight *w = new (std::nothrow) lmx_weight;
   if (!w) return fail(LMX_ERR_OUT_OF_MEMORY, "host allocation failed");
-  w->format = fmt;
+  plan_weight(w, fmt, rows, cols, group);
   w->device = dev;
-  w->rows = rows;
-  w->cols = cols;
-  w->Npad = round_up(rows, kWave);
-  w->Kp = round_up(cols, kRotChunk);
-  w->group = group ? group : w->Kp;
-  w->n_groups = (w->Kp + w->group - 1) / w->group;
-  w->tile_bytes = (w->Kp / kChunk) * fi.planes * w->Npad * 16;
-  w->scale_bytes = size_t(fi.stages) * w->n_groups * w->Npad * sizeof(float);
-  w->waves = choose_waves();
-  w->kslice = choose_kslice(w->Npad, w->Kp, w->waves);
-  w->reduce = choose_reduce();
-  {
-    const int fam = env_int("LMX_KERNEL", kKernelAuto);
-    w->kfamily = (fam == kKernelGeneric || fam == kKernelLean) ? fam : kKernelAuto;
-  }
-  w->fullk = choose_fullk(fmt, w->Npad, w->Kp, w->kfamily);
-  w->staged = choose_staged();
-  w->batched = env_int("LMX_BATCHED", 1) != 0;
 
   std::vector<uint8_t> tiles;
   std::vector<float> sc;
@@ -395,6 +406,33 @@ int lmx_untile_planes(int format, const uint8_t *tiles, size_t rows, size_t cols
   return LMX_OK;
 }
 
+int lmx_tile_scales(int format, const float *scales, size_t rows, size_t cols, size_t group, float *out,
+                    size_t *bytes) {
+  FormatInfo fi;
+  if (!format_info(format, &fi)) return fail(LMX_ERR_UNSUPPORTED_FORMAT, "unknown format %d", format);
+  if (!bytes) return fail(LMX_ERR_INVALID_ARGUMENT, "bytes is NULL");
+  if (rows == 0 || cols == 0 || cols % 8)
+    return fail(LMX_ERR_INVALID_ARGUMENT, "rows/cols must be > 0 and cols a multiple of 8");
+  if (group >= round_up(cols, kRotChunk)) group = 0;
+  if (group && group % kChunk)
+    return fail(LMX_ERR_INVALID_ARGUMENT, "group %zu must be a multiple of 128 (or 0 = per row)", group);
+  lmx_weight w;
+  plan_weight(&w, format, rows, cols, group);
+  if (!out) {
+    *bytes = w.scale_bytes;
+    return LMX_OK;
+  }
+  if (!scales) return fail(LMX_ERR_INVALID_ARGUMENT, "scales is NULL");
+  if (*bytes != w.scale_bytes) return fail(LMX_ERR_INVALID_ARGUMENT, "bytes %zu != %zu", *bytes, w.scale_bytes);
+  const size_t ng_src = group ? (cols + group - 1) / group : 1;
+  std::fill(out, out + w.scale_bytes / sizeof(float), 0.0f);
+  for (int s = 0; s < fi.stages; ++s)
+    for (size_t r = 0; r < rows; ++r)
+      for (size_t g = 0; g < ng_src && g < w.n_groups; ++g)
+        out[(size_t(s) * w.n_groups + g) * w.Npad + r] = scales[(size_t(s) * rows + r) * ng_src + g];
+  return LMX_OK;
+}
+
 int lmx_weight_create(const lmx_planes_desc *d, lmx_weight **out) {
   if (!d || !out) return fail(LMX_ERR_INVALID_ARGUMENT, "desc or out is NULL");
   *out = nullptr;
@@ -472,6 +510,14 @@ int lmx_weight_read_tiles(const lmx_weight *w, uint8_t *tiles, size_t bytes) {
 int lmx_gemv(const lmx_weight *w, const float *x, float *y, size_t batch, unsigned flags, void *stream) {
   int st = check_weight(w);
   if (st) return st;
+  return gemv_impl(w, x, y, batch, flags, stream);
+}
+
+}  // extern "C"
+
+namespace lmx {
+int gemv_impl(const lmx_weight *w, const float *x, float *y, size_t batch, unsigned flags, void *stream) {
+  int st;
   if (!x || !y) return fail(LMX_ERR_INVALID_ARGUMENT, "x or y is NULL");
   if (reinterpret_cast<size_t>(x) % 4 || reinterpret_cast<size_t>(y) % 4)
     return fail(LMX_ERR_INVALID_ARGUMENT, "x and y must be 4-byte aligned");
@@ -505,6 +551,9 @@ int lmx_gemv(const lmx_weight *w, const float *x, float *y, size_t batch, unsign
   }
   return LMX_OK;
 }
+}  // namespace lmx
+
+extern "C" {
 
 int lmx_linear(const lmx_weight *w, const float *bias, const float *x, float *y, size_t batch, void *stream) {
   int st = check_weight(w);

@@ -172,6 +172,12 @@ struct lmx_weight {
 };
 
 namespace lmx {
+// Fills a handle's shape, layout sizes and kernel plan for (fmt, rows, cols,
+// group) as lmx_weight_create does; allocates nothing, sets no pointers.
+void plan_weight(lmx_weight *w, int fmt, size_t rows, size_t cols, size_t group);
+// lmx_gemv after its handle check: y = W x for `batch` vectors with the
+// handle's pointers (planes, scales, partials, counters, staging).
+int gemv_impl(const lmx_weight *w, const float *x, float *y, size_t batch, unsigned flags, void *stream);
 // Kernel arguments of a handle (x, y, bias, rotation and transform unset).
 GemvArgs weight_args(const lmx_weight *w);
 // Vectors x[0..batch) in groups of 16/8/4 through the batched kernel (a.bias

@@ -1,0 +1,105 @@
+// lmx_noalloc.hip -- lmx_gemv_tiles_noalloc: the GEMV of lmx_gemv for a
+// caller that cannot allocate (code under HIP graph capture, serving loops
+// with a fixed memory budget).  The weights are the caller's own device
+// buffers in the device tile layout (lmx_tile_planes / lmx_tile_scales), x
+// and y are the caller's; every buffer the kernels need beyond those -- the
+// split-K ticket counters, the staging copy of x and the split-K partial
+// sums -- lives in `scratch`, a file-scope device array of kScratchBytes
+// that each GPU holds for the life of the process.  Nothing here calls
+// hipMalloc, hipFree or any allocating routine.
+//
+// Scratch layout (byte offsets, each region 256-byte aligned):
+//   [0, C)        ticket counters, one per 64-row block   C = Npad/64 * 4
+//   [C, C+X)      staging copy of x (unaligned x, length-K FWHT)   X = Kp * 4
+//   [C+X, ...)    split-K partials [Kp/kslice][Npad] fp32 (split-K plans only)
+// The counters must read zero when a call starts: the first call on a
+// device zeroes the whole array with a fill kernel, and every split-K
+// launch leaves each counter it used at zero again (its last workgroup
+// resets it).  Calls on one GPU share the array, so calls that overlap in
+// time on one GPU (two streams, two threads) race; order them.
+#include <hip/hip_runtime.h>
+
+#include <mutex>
+
+#include "lmx_internal.hpp"
+
+constexpr size_t kScratchBytes = size_t(8) << 20;   // 8 MiB per GPU
+
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace lmx {
+namespace {
+
+constexpr int kMaxDevices = 64;
+
+__global__ __launch_bounds__(256) void zero_scratch_kernel(uint32_t *p, size_t n) {
+  for (size_t i = size_t(blockIdx.x) * 256 + threadIdx.x; i < n; i += size_t(gridDim.x) * 256) p[i] = 0u;
+}
+
+std::mutex g_mu;
+void *g_ptr[kMaxDevices] = {};   // each device's address of `scratch`, set once
+
+// The device address of this device's `scratch` (never the host-side name),
+// set up on the first call on the device.
+int scratch_ptr(int dev, void *stream, unsigned char **out) {
+  if (dev < 0 || dev >= kMaxDevices) return fail(LMX_ERR_NO_DEVICE, "device %d outside 0..%d", dev, kMaxDevices - 1);
+  std::lock_guard<std::mutex> lock(g_mu);
+  if (!g_ptr[dev]) {
+    void *p = nullptr;
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(LMX_ERR_HIP, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+    zero_scratch_kernel<<<dim3(1024), dim3(256), 0, static_cast<hipStream_t>(stream)>>>(static_cast<uint32_t *>(p),
+                                                                                      kScratchBytes / 4);
+    e = hipGetLastError();
+    if (e != hipSuccess) return fail(LMX_ERR_LAUNCH_FAILED, "scratch zero fill: %s", hipGetErrorString(e));
+    g_ptr[dev] = p;
+  }
+  *out = static_cast<unsigned char *>(g_ptr[dev]);
+  return LMX_OK;
+}
+
+}  // namespace
+}  // namespace lmx
+
+extern "C" int lmx_gemv_tiles_noalloc(int format, const void *tiles, const float *scales, size_t rows, size_t cols,
+                                      size_t group, const float *x, float *y, size_t batch, unsigned flags,
+                                      void *stream) {
+  using namespace lmx;
+  FormatInfo fi;
+  if (!format_info(format, &fi)) return fail(LMX_ERR_UNSUPPORTED_FORMAT, "unknown format %d", format);
+  if (!tiles || !scales) return fail(LMX_ERR_INVALID_ARGUMENT, "tiles or scales is NULL");
+  if (rows == 0 || cols == 0 || cols % 8)
+    return fail(LMX_ERR_INVALID_ARGUMENT, "rows/cols must be > 0 and cols a multiple of 8");
+  if (rows > (1u << 30) || cols > (1u << 28))
+    return fail(LMX_ERR_INVALID_ARGUMENT, "shape %zu x %zu too large", rows, cols);
+  if (group >= round_up(cols, kRotChunk)) group = 0;
+  if (group && group % kChunk)
+    return fail(LMX_ERR_INVALID_ARGUMENT, "group %zu must be a multiple of 128 (or 0 = per row)", group);
+  if (reinterpret_cast<size_t>(tiles) % 16 || reinterpret_cast<size_t>(scales) % 4)
+    return fail(LMX_ERR_INVALID_ARGUMENT, "tiles must be 16-byte and scales 4-byte aligned");
+  lmx_weight w;   // the plan lmx_weight_create would choose, over the caller's buffers
+  plan_weight(&w, format, rows, cols, group);
+  w.batched = false;   // one vector at a time: the batched kernel's partials would not fit
+  const size_t counters = round_up(w.Npad / kWave * sizeof(unsigned), 256);
+  const size_t staging = round_up(w.Kp * sizeof(float), 256);
+  const size_t partials = w.fullk ? 0 : (w.Kp / size_t(w.kslice)) * w.Npad * sizeof(float);
+  if (counters + staging + partials > kScratchBytes)
+    return fail(LMX_ERR_INVALID_ARGUMENT,
+                "%zu x %zu needs %zu B of scratch (ticket counters, x staging, split-K partials); "
+                "lmx_gemv_tiles_noalloc holds %zu B per GPU: use a weight handle (lmx_gemv)",
+                rows, cols, counters + staging + partials, kScratchBytes);
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(LMX_ERR_NO_DEVICE, "hipGetDevice: %s", hipGetErrorString(e));
+  unsigned char *base = nullptr;
+  int st = scratch_ptr(dev, stream, &base);
+  if (st) return st;
+  w.device = dev;
+  w.d_planes = const_cast<void *>(tiles);
+  w.d_scales = const_cast<float *>(scales);
+  w.d_counters = reinterpret_cast<unsigned *>(base);
+  w.d_xrot = reinterpret_cast<float *>(base + counters);
+  w.d_partials = reinterpret_cast<float *>(base + counters + staging);
+  return gemv_impl(&w, x, y, batch, flags, stream);
+}

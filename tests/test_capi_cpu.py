@@ -141,3 +141,18 @@ def test_no_device_is_reported():
     h = ctypes.c_void_p()
     assert lib.lmx_weight_create(ctypes.byref(d), ctypes.byref(h)) == L.ERR_NO_DEVICE
     assert not h.value
+
+
+@pytest.mark.parametrize("fmt,rows,cols,group", [(6, 70, 640, 128), (1, 65, 512, 0), (3, 3, 1000, 256),
+                                                 (4, 64, 384, 128)])
+def test_tile_scales_layout(fmt, rows, cols, group):
+    # canonical [S][rows][groups] -> device [S][Kp/group][Npad], zero padded
+    S = L.STAGES[fmt]
+    ng = 1 if group == 0 else -(-cols // group)
+    sc = np.random.default_rng(fmt).standard_normal((S, rows, ng)).astype(np.float32)
+    out = L.tile_scales(fmt, sc, rows, cols, group)
+    Npad, Kp = -(-rows // 64) * 64, -(-cols // 256) * 256
+    ngd = 1 if group == 0 else Kp // group
+    want = np.zeros((S, ngd, Npad), np.float32)
+    want[:, :ng, :rows] = sc.transpose(0, 2, 1)
+    assert np.array_equal(out, want.ravel())
