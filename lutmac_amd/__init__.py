@@ -41,7 +41,7 @@ EXPORTS = [
     "lmx_decoder_create", "lmx_decoder_create_batched", "lmx_decoder_destroy", "lmx_decoder_set_layer", "lmx_decoder_set_head",
     "lmx_decoder_reset", "lmx_decoder_step", "lmx_decoder_tokens", "lmx_decoder_generate",
     # include/lutmac_synth.h
-    "lmx_quantize_int4", "lmx_synth_int4_normal", "lmx_synth_normal",
+    "lmx_quantize_int4", "lmx_quantize", "lmx_synth_int4_normal", "lmx_synth_normal",
     # include/lutmac_model.h
     "lmx_model_load", "lmx_model_destroy", "lmx_model_config", "lmx_model_decoder", "lmx_model_weight_format",
 ]
@@ -102,6 +102,7 @@ _SIGS = {
     "lmx_gemv_tiles_noalloc": ([_i, _p, _p, _sz, _sz, _sz, _p, _p, _sz, _u, _p], _i),
     "lmx_host_cache_clear": ([], _i),
     "lmx_quantize_int4": ([_p, _sz, _sz, _sz, _p, _p], _i),
+    "lmx_quantize": ([_i, _p, _sz, _sz, _sz, _u, _p, _p], _i),
     "lmx_synth_int4_normal": ([ctypes.c_uint64, ctypes.c_uint64, _sz, _sz, ctypes.c_float, _sz, _p, _p], _i),
     "lmx_synth_normal": ([ctypes.c_uint64, ctypes.c_uint64, _sz, _sz, ctypes.c_float, _p], _i),
     "lmx_model_load": ([ctypes.c_char_p, _sz, ctypes.POINTER(_p)], _i),
@@ -244,6 +245,22 @@ def quantize_int4(w, group):
     scales = np.zeros((1, rows, cols // group), np.float32)
     check(lib().lmx_quantize_int4(_np_ptr(w), rows, cols, group, _np_ptr(planes), _np_ptr(scales)))
     return planes, scales
+
+
+QUANT_ROTATE = 1
+QUANT_RESIDUAL = 2
+
+
+def quantize(fmt, w, group, flags=0):
+    """fp32 [rows, cols] -> (planes [P, rows, cols/8], scales [S, rows, groups], group) with
+    the reference's rule for the format (lmx_quantize); group 0 = one scale per row."""
+    w = np.ascontiguousarray(w, np.float32)
+    rows, cols = w.shape
+    ng = 1 if group == 0 else -(-cols // group)
+    planes = np.zeros((PLANES[fmt], rows, cols // 8), np.uint8)
+    scales = np.zeros((STAGES[fmt], rows, ng), np.float32)
+    check(lib().lmx_quantize(fmt, _np_ptr(w), rows, cols, group, flags, _np_ptr(planes), _np_ptr(scales)))
+    return planes, scales, group
 
 
 def synth_int4_normal(seed, stream, rows, cols, std, group):

@@ -32,6 +32,7 @@ SOURCES = [
     ("lmx_repack.cpp", False),
     ("lut_gemm_compat.cpp", False),
     ("lmx_synth.cpp", False),
+    ("lmx_quantize.cpp", False),
     ("lmx_model.cpp", False),
 ]
 

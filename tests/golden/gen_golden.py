@@ -91,7 +91,31 @@ def main():
         assert R.ref_lut_linear(fmt, P(blocks), nb, None, P(xs), P(y_nobias), M, K, batch) == 0
         np.savez_compressed(os.path.join(HERE, f"blocks_{name}.npz"), fmt=fmt, M=M, K=K, blocks=blocks,
                  dequant=deq, x=xs, bias=bias, y=y, y_nobias=y_nobias)
+    quantizer_fixtures(R)
     print("golden fixtures written to", HERE)
+
+
+def quantizer_fixtures(R):
+    """The reference quantizers (quantize_tensor, _binary, _int2) on seeded
+    N(0, 0.02) weights, plain and after the tool's weight rotation
+    (apply_hadamard_rotation over the tensor, tools/lutmac-quantize.cpp:426-447):
+    inputs and the reference's block bytes (own generator, so the fixtures
+    above are unchanged)."""
+    rng = np.random.default_rng(20260202)
+    M, K = 24, 768
+    w = (rng.standard_normal((M, K)) * 0.02).astype(np.float32)
+    w[5] = 0.0   # an all-zero row (ternary scale 1, binary scale 0)
+    out = {"w": w}
+    for fmt, name in [(1, "ternary"), (2, "binary"), (3, "int2")]:
+        for rot in (False, True):
+            src = w.copy()
+            if rot:
+                R.ref_apply_hadamard_rotation(P(src), src.size)
+            n = R.ref_quantize(fmt, P(src), M, K, None, 0)
+            blocks = np.zeros(n, np.uint8)
+            R.ref_quantize(fmt, P(src), M, K, P(blocks), n)
+            out[f"{name}{'_rot' if rot else ''}"] = blocks
+    np.savez_compressed(os.path.join(HERE, "quantizers.npz"), **out)
 
 
 if __name__ == "__main__":
