@@ -9,6 +9,13 @@
  * matched as load_model matches them; a missing lm_head ties it to the
  * embedding, sharing one device weight instead of a copy.
  *
+ * Version 2 adds tensor records {"type": "planes", "format", "group",
+ * "rotated", "offset", "planes_bytes", "scales_bytes"} holding canonical
+ * planes and per-group scales (any group multiple of 128, RRQ-3), as
+ * lutmac_amd/lutmac_file.py writes them from lmx_quantize output; ternary,
+ * binary and RRQ planes must be FWHT-rotated, the others not, the embedding
+ * never.
+ *
  * Supported: decoder-only Llama/Qwen-style models (RMSNorm, SiLU) whose
  * linears and embedding are ternary, binary, 2-bit (Int2Block), 3-bit,
  * 4-bit or 8-bit blocks; norms and biases raw fp32.  5/6-bit tensors, raw

@@ -1,10 +1,23 @@
-// lmx_model.cpp -- .lutmac v1 files onto the device decoder (lutmac_model.h).
+// lmx_model.cpp -- .lutmac files onto the device decoder (lutmac_model.h).
 //
-// File layout (src/format.cpp:146-290, types.hpp:44-45): "LUTMAC01", u32
+// Version 1 (src/format.cpp:146-290, types.hpp:44-45): "LUTMAC01", u32
 // version 1, u32 metadata size, JSON metadata {"config": {...}, "tensors":
 // [{"name", "shape", "offset", "type", "num_blocks", "quant_bits"}, ...]},
 // zero padding to a 256-byte boundary, then each tensor's data at
 // data_start + offset: its AoS blocks, or raw fp32.
+//
+// Version 2 (this build's extension, no reference counterpart): the same
+// container; a tensor may also be a record {"type": "planes", "format":
+// "ternary" | "binary" | "rrq2" | "rrq3" | "int3" | "int4" | "int8",
+// "group": G (a multiple of 128, 0 = one scale per row), "rotated": bool,
+// "offset", "planes_bytes", "scales_bytes"} whose data is the canonical
+// planes [P][rows][cols/8] followed by the scales [S][rows][groups] fp32
+// (the lmx_planes_desc layout), so per-128-group scales and RRQ-3 -- which
+// the 256-weight blocks cannot express -- have a file form.  "rotated" says
+// the weights were FWHT-256-rotated when quantized (lmx_quantize with
+// LMX_QUANT_ROTATE); the runtime rotates the activations of ternary, binary
+// and RRQ linears (lut_linear's rule), so those formats must be rotated and
+// the others not, and the embedding must not be (it is read row by row).
 #include <cstdio>
 #include <cstring>
 #include <fstream>
@@ -148,7 +161,46 @@ struct TensorRec {
   std::string name, type;
   std::vector<size_t> shape;
   size_t offset = 0, num_blocks = 0;
+  // version-2 plane records
+  int format = 0;
+  size_t group = 0, planes_bytes = 0, scales_bytes = 0;
+  bool rotated = false;
 };
+
+int plane_format(const std::string &f) {
+  struct M { const char *name; int fmt; };
+  static const M table[] = {{"ternary", LMX_FMT_TERNARY}, {"binary", LMX_FMT_BINARY}, {"rrq2", LMX_FMT_RRQ2},
+                            {"rrq3", LMX_FMT_RRQ3},       {"int3", LMX_FMT_INT3},     {"int4", LMX_FMT_INT4},
+                            {"int8", LMX_FMT_INT8}};
+  for (const M &m : table)
+    if (f == m.name) return m.fmt;
+  return 0;
+}
+
+bool rotated_format(int fmt) {   // lut_gemm_scalar.cpp:88-96
+  return fmt == LMX_FMT_TERNARY || fmt == LMX_FMT_BINARY || fmt == LMX_FMT_RRQ2 || fmt == LMX_FMT_RRQ3;
+}
+
+// A version-2 plane record's sizes and rotation against its shape and format.
+int check_planes(const TensorRec &t) {
+  if (!t.format) return fail(LMX_ERR_UNSUPPORTED_FORMAT, "tensor %s: unknown plane format", t.name.c_str());
+  if (t.shape.size() != 2 || t.shape[1] % 8)
+    return fail(LMX_ERR_INVALID_ARGUMENT, "tensor %s: planes need [rows, cols] with cols a multiple of 8",
+                t.name.c_str());
+  int P = 0, S = 0;
+  lmx_format_info(t.format, &P, &S);
+  const size_t rows = t.shape[0], cols = t.shape[1];
+  if (t.group && t.group % 128)
+    return fail(LMX_ERR_INVALID_ARGUMENT, "tensor %s: group %zu is not a multiple of 128", t.name.c_str(), t.group);
+  const size_t ng = t.group ? (cols + t.group - 1) / t.group : 1;
+  if (t.planes_bytes != size_t(P) * rows * cols / 8 || t.scales_bytes != size_t(S) * rows * ng * sizeof(float))
+    return fail(LMX_ERR_INVALID_ARGUMENT, "tensor %s: plane/scale sizes do not match its shape", t.name.c_str());
+  if (t.rotated != rotated_format(t.format))
+    return fail(LMX_ERR_UNSUPPORTED_FORMAT,
+                "tensor %s: %s weights must %sbe FWHT-rotated (the runtime rotates the activations of ternary, "
+                "binary and RRQ linears only)", t.name.c_str(), t.type.c_str(), rotated_format(t.format) ? "" : "not ");
+  return LMX_OK;
+}
 
 // Reference block type -> (lmx_format, bytes per 256-weight block); 0 when
 // this path has no kernel for it.
@@ -195,10 +247,61 @@ struct lmx_model {
 
 namespace {
 
+// Version-2 plane records -> one device weight: planes and scales of the
+// parts concatenated row-wise, plane by plane and stage by stage (all parts
+// share format, group and width).
+int make_weight_planes(File &file, const std::vector<const TensorRec *> &parts, size_t cols, lmx_model *m,
+                       lmx_weight **out) {
+  const TensorRec &t0 = *parts[0];
+  int P = 0, S = 0;
+  lmx_format_info(t0.format, &P, &S);
+  size_t rows = 0;
+  for (const TensorRec *t : parts) {
+    if (t->type != "planes" || t->format != t0.format || t->group != t0.group)
+      return fail(LMX_ERR_UNSUPPORTED_FORMAT, "tensor %s: fused tensors must share one format and group",
+                  t->name.c_str());
+    int st = check_planes(*t);
+    if (st) return st;
+    if (t->shape[1] != cols)
+      return fail(LMX_ERR_INVALID_ARGUMENT, "tensor %s: expected [rows, %zu]", t->name.c_str(), cols);
+    rows += t->shape[0];
+  }
+  const size_t rb = cols / 8, ng = t0.group ? (cols + t0.group - 1) / t0.group : 1;
+  std::vector<uint8_t> planes, pbuf;
+  std::vector<float> scales, sbuf;
+  try {
+    planes.resize(size_t(P) * rows * rb);
+    scales.resize(size_t(S) * rows * ng);
+  } catch (const std::bad_alloc &) {
+    return fail(LMX_ERR_OUT_OF_MEMORY, "host buffers for %zu rows", rows);
+  }
+  size_t r0 = 0;
+  for (const TensorRec *t : parts) {
+    const size_t tr = t->shape[0];
+    pbuf.resize(t->planes_bytes);
+    sbuf.resize(t->scales_bytes / sizeof(float));
+    int st = file.read(t->offset, pbuf.data(), t->planes_bytes);
+    if (!st) st = file.read(t->offset + t->planes_bytes, sbuf.data(), t->scales_bytes);
+    if (st) return st;
+    for (int p = 0; p < P; ++p)
+      std::memcpy(planes.data() + (size_t(p) * rows + r0) * rb, pbuf.data() + size_t(p) * tr * rb, tr * rb);
+    for (int s2 = 0; s2 < S; ++s2)
+      std::memcpy(scales.data() + (size_t(s2) * rows + r0) * ng, sbuf.data() + size_t(s2) * tr * ng,
+                  tr * ng * sizeof(float));
+    r0 += tr;
+  }
+  lmx_planes_desc d{t0.format, rows, cols, t0.group, planes.data(), scales.data()};
+  int st = lmx_weight_create(&d, out);
+  if (st) return st;
+  m->owned.push_back(*out);
+  return LMX_OK;
+}
+
 // Quantized tensor(s) -> one device weight: the tensors' block arrays
 // concatenated row-wise (all must share format and width).
 int make_weight(File &file, const std::vector<const TensorRec *> &parts, size_t cols, lmx_model *m,
                 lmx_weight **out) {
+  if (parts[0]->type == "planes") return make_weight_planes(file, parts, cols, m, out);
   int fmt = 0;
   size_t bytes = 0, rows = 0, nblocks = 0;
   for (const TensorRec *t : parts) {
@@ -266,7 +369,8 @@ int lmx_model_load(const char *path, size_t max_seq, lmx_model **out) {
   file.f.read(reinterpret_cast<char *>(&header), 4);
   if (!file.f || std::memcmp(magic, "LUTMAC01", 8) != 0)
     return fail(LMX_ERR_INVALID_ARGUMENT, "%s is not a .lutmac file", path);
-  if (version != 1) return fail(LMX_ERR_UNSUPPORTED_FORMAT, ".lutmac version %u (this loader reads 1)", version);
+  if (version != 1 && version != 2)
+    return fail(LMX_ERR_UNSUPPORTED_FORMAT, ".lutmac version %u (this loader reads 1 and 2)", version);
   std::string meta(header, '\0');
   file.f.read(&meta[0], std::streamsize(header));
   if (!file.f) return fail(LMX_ERR_INVALID_ARGUMENT, "truncated metadata");
@@ -316,6 +420,15 @@ int lmx_model_load(const char *path, size_t max_seq, lmx_model **out) {
       for (const JVal &d : sh->arr) r.shape.push_back(size_t(d.num));
     r.offset = size_t(num_or(t, "offset", 0));
     r.num_blocks = size_t(num_or(t, "num_blocks", 0));
+    if (r.type == "planes") {
+      if (version < 2) return fail(LMX_ERR_INVALID_ARGUMENT, "tensor %s: plane records need version 2", r.name.c_str());
+      const JVal *f = t.get("format"), *rot = t.get("rotated");
+      r.format = f && f->kind == JVal::Str ? plane_format(f->str) : 0;
+      r.group = size_t(num_or(t, "group", 0));
+      r.rotated = rot && rot->kind == JVal::Bool && rot->num != 0.0;
+      r.planes_bytes = size_t(num_or(t, "planes_bytes", 0));
+      r.scales_bytes = size_t(num_or(t, "scales_bytes", 0));
+    }
     recs.push_back(std::move(r));
   }
   // name -> record, matched as load_model matches (model.cpp:589-660)
@@ -356,12 +469,15 @@ int lmx_model_load(const char *path, size_t max_seq, lmx_model **out) {
   // Every tensor the decoder needs, checked before any device work.
   auto quantized = [](const TensorRec *t) -> int {
     size_t b = 0;
+    if (t->type == "planes") return check_planes(*t);
     if (type_format(t->type, &b)) return LMX_OK;
     return fail(LMX_ERR_UNSUPPORTED_FORMAT, "tensor %s has type '%s' (no LUT-GEMV kernel for it)", t->name.c_str(),
                 t->type.c_str());
   };
   {
     int st = quantized(embed);
+    if (!st && embed->type == "planes" && embed->rotated)
+      return fail(LMX_ERR_UNSUPPORTED_FORMAT, "the embedding must not be rotated (int3, int4 or int8 planes)");
     if (!st && head) st = quantized(head);
     for (size_t l = 0; l < c.n_layers && !st; ++l) {
       const LayerRecs &L = lr[l];

@@ -126,6 +126,85 @@ class SyntheticModel:
                 "gate_up": (2 * c.ffn, c.hidden), "down": (c.hidden, c.ffn)}
 
 
+def _fuse(parts):
+    """Row-wise concatenation of plane-form matrices (planes [P, rows, cols/8],
+    scales [S, rows, groups], same format and group)."""
+    return (np.concatenate([p[0] for p in parts], axis=1), np.concatenate([p[1] for p in parts], axis=1),
+            parts[0][2], parts[0][3])
+
+
+class QuantizedModel:
+    """A decoder whose linears are quantized from fp32 weights with lmx_quantize
+    in any format (the reference quantize tool's role, tools/lutmac-quantize.cpp):
+    ``formats`` maps q, k, v, o, gate, up, down, embed to (format, group, flags);
+    ternary, binary and RRQ weights get the tool's FWHT (LMX_QUANT_ROTATE).  The
+    fp32 weights are seeded N(0, 0.02) (lmx_synth_normal, one generator stream
+    per matrix); norms 1 + 0.1 N(0,1).  layers[i] holds the fused q|k|v and
+    gate|up matrices as (planes, scales, format, group), the form Decoder and
+    the oracle take; ``save_v2`` writes the unfused tensors as a .lutmac
+    version-2 file."""
+
+    NAMES = ("q", "k", "v", "o", "gate", "up", "down")
+
+    def __init__(self, cfg, formats, seed=0):
+        from . import quantize, synth_normal, QUANT_ROTATE
+        from .lutmac_file import ROTATED
+        self.cfg, self.formats, self.group = cfg, formats, 0
+        rng = np.random.default_rng(seed)
+        stream = iter(range(1 << 30))
+        h = cfg.hidden
+        shapes = {"q": (cfg.q_dim, h), "k": (cfg.kv_dim, h), "v": (cfg.kv_dim, h), "o": (h, cfg.q_dim),
+                  "gate": (cfg.ffn, h), "up": (cfg.ffn, h), "down": (h, cfg.ffn), "embed": (cfg.vocab, h)}
+
+        def quant(name):
+            fmt, group, flags = formats[name]
+            w = synth_normal(seed, next(stream), *shapes[name], 0.02)
+            rot = fmt in ROTATED
+            pl, sc, g = quantize(fmt, w, group, flags | (QUANT_ROTATE if rot else 0))
+            return (pl, sc, fmt, g), rot
+
+        self.raw, self.rotated, self.layers = [], {}, []
+        for i in range(cfg.n_layers):
+            mats = {}
+            for n in self.NAMES:
+                mats[n], self.rotated[(i, n)] = quant(n)
+            L = {"qkv": _fuse([mats["q"], mats["k"], mats["v"]]), "o": mats["o"],
+                 "gate_up": _fuse([mats["gate"], mats["up"]]), "down": mats["down"],
+                 "in_norm": (1.0 + 0.1 * rng.standard_normal(h)).astype(np.float32),
+                 "post_norm": (1.0 + 0.1 * rng.standard_normal(h)).astype(np.float32), "qkv_bias": None}
+            self.raw.append(mats)
+            self.layers.append(L)
+        self.head, rot = quant("embed")
+        if rot:
+            raise ValueError("the embedding is read row by row: use int3, int4 or int8")
+        self.final_norm = (1.0 + 0.1 * rng.standard_normal(h)).astype(np.float32)
+
+    def shapes(self):
+        return SyntheticModel.shapes(self)
+
+    def save_v2(self, path):
+        """The model as a .lutmac version-2 file (plane records, HF tensor names)."""
+        from .lutmac_file import Planes, write
+        c = self.cfg
+        config = {"model_type": "llama", "vocab_size": c.vocab, "hidden_size": c.hidden,
+                  "intermediate_size": c.ffn, "num_hidden_layers": c.n_layers,
+                  "num_attention_heads": c.n_heads, "num_key_value_heads": c.n_kv_heads, "head_dim": c.head_dim,
+                  "rms_norm_eps": c.rms_eps, "rope_theta": c.rope_theta, "rope_scaling_factor": c.rope_factor}
+        names = {"q": "self_attn.q_proj", "k": "self_attn.k_proj", "v": "self_attn.v_proj",
+                 "o": "self_attn.o_proj", "gate": "mlp.gate_proj", "up": "mlp.up_proj", "down": "mlp.down_proj"}
+        tensors = [("model.embed_tokens.weight", Planes(self.head[2], self.head[0], self.head[1], self.head[3],
+                                                        False))]
+        for i, (mats, L) in enumerate(zip(self.raw, self.layers)):
+            for n in self.NAMES:
+                m = mats[n]
+                tensors.append((f"model.layers.{i}.{names[n]}.weight",
+                                Planes(m[2], m[0], m[1], m[3], self.rotated[(i, n)])))
+            tensors.append((f"model.layers.{i}.input_layernorm.weight", L["in_norm"]))
+            tensors.append((f"model.layers.{i}.post_attention_layernorm.weight", L["post_norm"]))
+        tensors.append(("model.norm.weight", self.final_norm))
+        write(path, config, tensors)
+
+
 class _DecoderOps:
     """Token-step operations over an lmx_decoder handle (self._h)."""
 
@@ -186,15 +265,19 @@ class Decoder(_DecoderOps):
         cs = c.c_struct()
         check(lib().lmx_decoder_create_batched(ctypes.byref(cs), batch, ctypes.byref(h)))
         self._h = h
+        def weight(entry, rows, cols):
+            # (planes, scales) of the model's 4-bit group, or (planes, scales, format, group)
+            fmt, g = (entry[2], entry[3]) if len(entry) == 4 else (FMT_INT4, model.group)
+            return Weight.from_planes(fmt, entry[0], entry[1], rows, cols, g)
+
         for i, L in enumerate(model.layers):
-            ws = [Weight.from_planes(FMT_INT4, L[n][0], L[n][1], *shapes[n], model.group)
-                  for n in ("qkv", "o", "gate_up", "down")]
+            ws = [weight(L[n], *shapes[n]) for n in ("qkv", "o", "gate_up", "down")]
             self.weights += ws
             bias = None if L["qkv_bias"] is None else L["qkv_bias"]
             check(lib().lmx_decoder_set_layer(self._h, i, *[w.handle for w in ws], _np_ptr(L["in_norm"]),
                                               _np_ptr(L["post_norm"]),
                                               None if bias is None else _np_ptr(bias)))
-        self.head = Weight.from_planes(FMT_INT4, model.head[0], model.head[1], c.vocab, c.hidden, model.group)
+        self.head = weight(model.head, c.vocab, c.hidden)
         check(lib().lmx_decoder_set_head(self._h, self.head.handle, self.head.handle, _np_ptr(model.final_norm)))
 
     def close(self):

@@ -185,10 +185,12 @@ class OracleDecoder:
         c = model.cfg
         self.cfg, self._keep = c, []
 
-        def mat(pl_sc, rows, cols):
-            pl, sc = np.ascontiguousarray(pl_sc[0], np.uint8), f32(pl_sc[1])
+        def mat(entry, rows, cols):
+            # (planes, scales) of the model's 4-bit group, or (planes, scales, format, group)
+            fmt, g = (entry[2], entry[3]) if len(entry) == 4 else (FMT_INT4, model.group)
+            pl, sc = np.ascontiguousarray(entry[0], np.uint8), f32(entry[1])
             self._keep += [pl, sc]
-            return OrcMatrix(FMT_INT4, _ptr(pl), _ptr(sc), rows, cols, model.group)
+            return OrcMatrix(fmt, _ptr(pl), _ptr(sc), rows, cols, g if g else cols)
 
         shapes = model.shapes()
         arrs = {}

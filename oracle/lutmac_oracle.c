@@ -518,8 +518,22 @@ static void rope(const orc_model *m, float *v, size_t n_heads, size_t pos) {
   }
 }
 
+/* lut_linear's rotation rule (lut_gemm_scalar.cpp:88-96): activations of
+ * ternary and 1-2 bit weights (binary, RRQ-2, RRQ-3) are FWHT-256-rotated,
+ * in a copy, before the GEMV; cols is a multiple of 256 here. */
 static void linear(const orc_matrix *w, const float *x, float *y) {
-  orc_planes_gemv(w->fmt, w->planes, w->scales, w->rows, w->cols, w->group, x, y);
+  const int rot = w->fmt == ORC_FMT_TERNARY || w->fmt == ORC_FMT_BINARY || w->fmt == ORC_FMT_RRQ2 ||
+                  w->fmt == ORC_FMT_RRQ3;
+  if (!rot) {
+    orc_planes_gemv(w->fmt, w->planes, w->scales, w->rows, w->cols, w->group, x, y);
+    return;
+  }
+  float *xr = malloc(w->cols * sizeof(float));
+  if (!xr) return;
+  memcpy(xr, x, w->cols * sizeof(float));
+  orc_apply_hadamard_rotation(xr, w->cols);
+  orc_planes_gemv(w->fmt, w->planes, w->scales, w->rows, w->cols, w->group, xr, y);
+  free(xr);
 }
 
 static float silu(float x) { return x / (1.0f + expf(-x)); } /* model.cpp:36 */

@@ -118,7 +118,8 @@ void orc_planes_gemv(int fmt, const uint8_t *planes, const float *scales,
  * One token step of src/model.cpp:47-453 for a Llama/Qwen-style model whose
  * linears are canonical-plane matrices (cols a multiple of 256, group G | cols):
  * embedding row of the tied table, per layer RMSNorm (norm.cpp:18-34), fused
- * q|k|v rows (+ bias), RoPE (embedding.cpp:36-75; rope_mode 0 = the
+ * q|k|v rows (+ bias; every linear applies lut_linear's rule: FWHT-256 of
+ * the activations for ternary, binary and RRQ weights), RoPE (embedding.cpp:36-75; rope_mode 0 = the
  * reference's (pos/factor)*theta^(-2d/hd), 1 = Llama-3 frequency scaling),
  * KV append, attention with softmax (model.cpp:326-372, attention.cpp:23-42),
  * o + residual, RMSNorm, fused gate|up, SiLU(gate)*up, down + residual;

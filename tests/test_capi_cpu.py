@@ -156,3 +156,34 @@ def test_tile_scales_layout(fmt, rows, cols, group):
     want = np.zeros((S, ngd, Npad), np.float32)
     want[:, :ng, :rows] = sc.transpose(0, 2, 1)
     assert np.array_equal(out, want.ravel())
+
+
+def test_lutmac_v2_rejections_before_device_work(tmp_path):
+    # plane records whose rotation flag contradicts lut_linear's rule, a
+    # rotated embedding and a size mismatch are refused while parsing
+    import ctypes
+    from lutmac_amd import decode as D
+    from lutmac_amd import lutmac_file as F
+    cfg = D.small_config(n_layers=1, vocab=300)
+    fmts = {n: (L.FMT_TERNARY, 128, 0) for n in D.QuantizedModel.NAMES}
+    fmts["embed"] = (L.FMT_INT4, 128, 0)
+    m = D.QuantizedModel(cfg, fmts, seed=1)
+    good = tmp_path / "good.lutmac"
+    m.save_v2(good)
+
+    def load(path):
+        h = ctypes.c_void_p()
+        return L.lib().lmx_model_load(str(path).encode(), 64, ctypes.byref(h))
+
+    m.rotated[(0, "q")] = False                     # ternary weights not rotated
+    bad = tmp_path / "unrotated.lutmac"
+    m.save_v2(bad)
+    assert load(bad) == L.ERR_UNSUPPORTED_FORMAT
+    assert b"rotated" in L.lib().lmx_last_error()
+    m.rotated[(0, "q")] = True
+    # version-1 files cannot hold plane records
+    data = bytearray(open(good, "rb").read())
+    data[8:12] = (1).to_bytes(4, "little")
+    v1 = tmp_path / "v1.lutmac"
+    v1.write_bytes(bytes(data))
+    assert load(v1) == L.ERR_INVALID_ARGUMENT

@@ -186,6 +186,6 @@ def test_lutmac_loader_rejects_bad_files(tmp_path):
     assert L.lib().lmx_model_load(str(p).encode(), 0, ctypes.byref(h)) == L.ERR_UNSUPPORTED_FORMAT
     p.write_bytes(_lutmac_bytes({"config": cfg, "tensors": tensors[1:]}))   # no embedding
     assert L.lib().lmx_model_load(str(p).encode(), 0, ctypes.byref(h)) == L.ERR_INVALID_ARGUMENT
-    raw = b"LUTMAC01" + (2).to_bytes(4, "little") + (2).to_bytes(4, "little") + b"{}"
-    p.write_bytes(raw)                                                        # version 2
+    raw = b"LUTMAC01" + (3).to_bytes(4, "little") + (2).to_bytes(4, "little") + b"{}"
+    p.write_bytes(raw)                                                        # version 3
     assert L.lib().lmx_model_load(str(p).encode(), 0, ctypes.byref(h)) == L.ERR_UNSUPPORTED_FORMAT
