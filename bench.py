@@ -384,6 +384,28 @@ def qwen_decode_bench(context, n_new, batches=(1, 4, 16), seed=2025):
             "setup_s": round(setup_s, 1)}
 
 
+def attention_position_check(caps=(128, 2048), n_prompt=64, n_new=8, seed=2024):
+    """Attention cost follows the position, not the KV capacity: the
+    Llama-3.2-1B decode step at positions 64..71 with the cache sized for
+    `caps` positions (the attention kernel launches one workgroup per KV head
+    and 64-position chunk of the capacity; chunks past the position load
+    nothing).  Returns the decode ms per step for each capacity; a kernel
+    trace separates the attention kernels by their grid size."""
+    from dataclasses import replace
+    from lutmac_amd import decode as D
+    model = D.SyntheticModel(replace(D.LLAMA_3_2_1B, max_seq=max(caps)), seed=seed, group=128)
+    prompt = np.random.default_rng(seed + 1).integers(0, model.cfg.vocab, n_prompt)
+    out = {}
+    for cap in caps:
+        model.cfg = replace(model.cfg, max_seq=cap)
+        dec = D.Decoder(model)
+        dec.generate(prompt, n_new)
+        _, _, dec_ms = dec.generate(prompt, n_new)
+        dec.close()
+        out[str(cap)] = {"ms_per_step": round(dec_ms / (n_new - 1), 4), "attention_grid": 8 * (-(-cap // 64))}
+    return {"positions": f"{n_prompt}..{n_prompt + n_new - 1}", "per_capacity": out}
+
+
 def cpu_decode_baseline(budget_s, seed=2024):
     """The reference's own Model::forward (oracle/_ref/libref.so, 1 thread:
     lut_linear -> int4_gemv scalar) on the same architecture in its native
@@ -500,6 +522,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true", help="skip the 1B-architecture decode")
     ap.add_argument("--no-batched", action="store_true", help="skip the Qwen-shape batch 1/4/16 sweep")
+    ap.add_argument("--batched-steps", type=int, default=100, help="launches per timed graph in that sweep")
     ap.add_argument("--no-qwen-decode", action="store_true", help="skip the Qwen-2.5-1.5B batch-1 decode")
     ap.add_argument("--qwen-context", type=int, default=2048)
     ap.add_argument("--qwen-tokens", type=int, default=64)
@@ -510,9 +533,14 @@ def main():
                     help="time one stream launch per GEMV only (no HIP-graph replay)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain device copy of 35717120 bytes (counter calibration)")
+    ap.add_argument("--attn-check", action="store_true",
+                    help="only run the attention-vs-KV-capacity check (Llama-1B decode at positions 64..71)")
     args = ap.parse_args()
     if args.calibrate_copy:
         calibrate_copy()
+        return
+    if args.attn_check:
+        print(json.dumps({"attention_position_check": attention_position_check()}), flush=True)
         return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
@@ -565,7 +593,7 @@ def main():
         print(f"# qwen decode (KV {qwen['kv_context']}): " + ", ".join(
             f"bs {b}: {v['tokens_per_s_aggregate']} tokens/s ({v['ms_per_step']} ms/step)"
             for b, v in qwen["per_batch"].items()), file=sys.stderr, flush=True)
-    batched = None if args.no_batched else batched_bench(torch, L)
+    batched = None if args.no_batched else batched_bench(torch, L, steps=args.batched_steps)
     if batched is not None:
         print("# batched linears per step: " + ", ".join(
             f"bs {b}: {v['linears_us_per_step']} us" for b, v in batched["per_batch"].items()),

@@ -319,7 +319,7 @@ __device__ __forceinline__ void merge_pass(const float *ph, int c0, int nb, int 
 // o_c / sum_c e^(m_c - M) l_c with M = max_c m_c, and writes the heads'
 // attention output, so the o-projection is a plain GEMV.  Partials and
 // tickets travel as device-scope relaxed atomics (no L2 writeback needed);
-// the last workgroup clears the ticket for the next step.
+// the merging workgroup clears the ticket for the next step.
 // Cost follows the position, not the cache capacity (the reference loops
 // to pos only, model.cpp:344-372): chunks below spec_chunks load their rows
 // speculatively, before the position is known; later chunks read the
@@ -496,13 +496,17 @@ __global__ __launch_bounds__(512) void attn_kernel(const float *__restrict__ qkv
     }
   }
   }   // !skip
-  // ---- ticket: the last workgroup of this KV head merges ----
+  // ---- ticket: the last of the KV head's live chunks merges ----
+  // Chunks past the position (skipped, or speculative ones that learn it
+  // only now) take no ticket, so they never delay the merge.
+  if (t0 > pos) return;   // uniform over the workgroup
+  const int nlive = pos / kAttnChunk + 1;
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (threadIdx.x == 0)
     ticket = __hip_atomic_fetch_add(tickets + kvh, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   __syncthreads();
-  if (ticket != unsigned(n_chunks - 1)) return;   // uniform over the workgroup
+  if (ticket != unsigned(nlive - 1)) return;   // uniform over the workgroup
   if (wave < group) {
     const int head = kvh * group + wave;
     const float *ph = part + size_t(head) * n_chunks * (HD + 4);
