@@ -826,18 +826,30 @@ size_t gemv_argmax_slots(const GemvArgs &a) {
 // ---------------------------------------------------------------------------
 // Batched GEMV: y_b = W x_b for NB activation vectors with the weights read
 // once (replaces lut_linear's per-row loop, lut_gemm_scalar.cpp:76-79).  A
-// workgroup owns 256 rows and a k-slice of 256 with 4 * NB/VG waves: wave w
-// serves row group w % 4 (one row per lane) for vectors (w / 4)*VG ..
-// (w / 4)*VG + VG - 1, so the LDS lookups of many vectors have enough waves
+// workgroup owns 64*RG rows and a k-slice of 256 with RG * NB/VG waves: wave
+// w serves row group w % RG (one row per lane) for vectors (w / RG)*VG ..
+// (w / RG)*VG + VG - 1, so the LDS lookups of many vectors have enough waves
 // to hide their latency (the weight words of a row group are read by NB/VG
-// waves: one HBM read, the rest cache hits).  The tables of a vector group
-// sit interleaved per group in LDS, table (chunk c, vector group v, group g,
-// vector b of the group) at (((c*NB/VG + v)*32 + g)*VG + b)*64 bytes, so
-// every group block starts 256-byte aligned, one v_perm address serves a
-// wave's VG vectors and the vector picks the ds_read immediate.  Partials
+// waves: one HBM read, the rest cache hits).  RG (1, 2 or 4) is the largest
+// that still gives the grid a workgroup per CU, so small matrices spread
+// over the chip.  The tables of a vector group sit together per group: the
+// 16-entry table of (chunk c, vector group v, group g, vector b of the
+// group) starts at batch_chunk_bytes<VG>() * (c*NB/VG + v) + g*GS + b*64,
+// GS = VG*64 + 16: one v_perm address serves a wave's VG vectors (the
+// vector only changes the ds_read immediate), every chunk base is 256-byte
+// aligned, and the 16 B pad puts 16 consecutive groups' table writes in 16
+// different 4-bank groups (conflict-free 16-byte writes).  Partials
 // [NB][splits][Npad] go through batched_reduce_kernel.
+constexpr int kBatchMinGrid = 256;   // workgroups: one per CU
+
+template <int VG>
+constexpr uint32_t batch_group_stride() { return uint32_t(VG) * 64 + 16; }
+template <int VG>
+constexpr uint32_t batch_chunk_bytes() { return 32 * batch_group_stride<VG>(); }   // a multiple of 256
+
 template <int VG>
 __device__ __forceinline__ void word_lookups_batch(uint32_t v, int i, uint32_t cbase, float *out) {
+  constexpr uint32_t GS = batch_group_stride<VG>();
   const uint32_t hi = (v >> 2) & 0x3C3C3C3Cu, lo = (v << 2) & 0x3C3C3C3Cu;
   uint32_t ad[8];
 #pragma unroll
@@ -849,30 +861,33 @@ __device__ __forceinline__ void word_lookups_batch(uint32_t v, int i, uint32_t c
   for (int n = 0; n < VG; ++n) {
     float t[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) t[j] = lds_load(ad[j] + ((8 * i + j) * VG + n) * 64);
+    for (int j = 0; j < 8; ++j) t[j] = lds_load(ad[j] + uint32_t(8 * i + j) * GS + uint32_t(n) * 64);
     out[n] += ((t[0] + t[1]) + (t[2] + t[3])) + ((t[4] + t[5]) + (t[6] + t[7]));
   }
 }
 
-template <int NB, int VG>
-constexpr int batch_waves() { return 4 * (NB / VG); }
+template <int NB, int VG, int RG>
+constexpr int batch_waves() { return RG * (NB / VG); }
 
-template <int FMT, int NB, int VG>
-__global__ __launch_bounds__((kWave * batch_waves<NB, VG>())) void lut_gemv_batch_kernel(GemvArgs a, int row_blocks,
-                                                                                      int splits) {
+template <int FMT, int NB, int VG, int RG>
+__global__ __launch_bounds__((kWave * batch_waves<NB, VG, RG>())) void lut_gemv_batch_kernel(GemvArgs a,
+                                                                                          int row_blocks,
+                                                                                          int splits) {
   constexpr int P = Fmt<FMT>::P, NA = Fmt<FMT>::NA, S = Fmt<FMT>::S;
   constexpr int CH = kRotChunk / kChunk;   // 2 chunks of 128 per slice
-  constexpr int NW = batch_waves<NB, VG>();
+  constexpr int NW = batch_waves<NB, VG, RG>();
   constexpr int NVG = NB / VG;
+  constexpr int ROWS = RG * kWave;
+  constexpr uint32_t GS = batch_group_stride<VG>(), CB = batch_chunk_bytes<VG>();
   static_assert(NB % VG == 0 && NW <= 16, "whole vector groups, at most 1024 threads");
-  __shared__ __attribute__((aligned(256))) float tables[CH * 32 * NB * 16];
+  __shared__ __attribute__((aligned(256))) char tables[CH * NVG * CB];
   __shared__ float xsum[NB][CH];
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
-  const int rg = wave & 3, vg = wave >> 2;
+  const int rg = wave % RG, vg = wave / RG;
   const int rb = blockIdx.x % row_blocks, split = blockIdx.x / row_blocks;
   const int k0 = split * kRotChunk;
-  const int row = rb * 256 + rg * kWave + lane;
-  const bool active = rb * 256 + rg * kWave < a.Npad;
+  const int row = rb * ROWS + rg * kWave + lane;
+  const bool active = rb * ROWS + rg * kWave < a.Npad;
   const int lr = min(row, a.Npad - 1);
 
   // activations: wave w builds the tables of vectors w, w + NW, ...
@@ -896,7 +911,7 @@ __global__ __launch_bounds__((kWave * batch_waves<NB, VG>())) void lut_gemv_batc
       for (int p = 0; p < P; ++p) {
         const u32x4 *src = pl + (size_t(c0 + c) * P + p) * Npad + lr;
         // one wave per row group streams; the others re-read through the caches
-        w[c][p] = NW == 4 ? __builtin_nontemporal_load(src) : *src;
+        w[c][p] = NVG == 1 ? __builtin_nontemporal_load(src) : *src;
       }
       const int g = (c0 + c) / a.group_chunks;
 #pragma unroll
@@ -912,7 +927,7 @@ __global__ __launch_bounds__((kWave * batch_waves<NB, VG>())) void lut_gemv_batc
     float t[16];
     group_table(x0, x1, x2, x3, t);
     const int c = lane >> 5, g = lane & 31;
-    float4 *dst = reinterpret_cast<float4 *>(tables + (((c * NVG + n / VG) * 32 + g) * VG + n % VG) * 16);
+    float4 *dst = reinterpret_cast<float4 *>(tables + (c * NVG + n / VG) * CB + g * GS + (n % VG) * 64);
     dst[0] = make_float4(t[0], t[1], t[2], t[3]);
     dst[1] = make_float4(t[4], t[5], t[6], t[7]);
     dst[2] = make_float4(t[8], t[9], t[10], t[11]);
@@ -930,7 +945,7 @@ __global__ __launch_bounds__((kWave * batch_waves<NB, VG>())) void lut_gemv_batc
   float acc[VG];
 #pragma unroll
   for (int n = 0; n < VG; ++n) acc[n] = 0.0f;
-  const uint32_t tbase = lds_addr(tables) + uint32_t(vg) * (32 * VG * 64);   // 256-byte aligned
+  const uint32_t tbase = lds_addr(reinterpret_cast<const float *>(tables)) + uint32_t(vg) * CB;   // 256-byte aligned
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
     float A[NA][VG];
@@ -938,7 +953,7 @@ __global__ __launch_bounds__((kWave * batch_waves<NB, VG>())) void lut_gemv_batc
     for (int q = 0; q < NA; ++q)
 #pragma unroll
       for (int n = 0; n < VG; ++n) A[q][n] = 0.0f;
-    const uint32_t cbase = tbase + c * (NVG * 32 * VG * 64);
+    const uint32_t cbase = tbase + uint32_t(c * NVG) * CB;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       uint32_t wi[P], v[NA];
@@ -984,12 +999,22 @@ __global__ __launch_bounds__(64) void batched_reduce_kernel(const float *__restr
   y[size_t(n) * rows + r] = s;
 }
 
+template <int FMT, int NB, int RG>
+static void launch_batch_rg(const GemvArgs &a, int splits, hipStream_t st) {
+  constexpr int VG = NB >= 4 ? NB / 4 : 1;   // vectors per wave
+  const int row_blocks = (a.Npad + RG * kWave - 1) / (RG * kWave);
+  lut_gemv_batch_kernel<FMT, NB, VG, RG>
+      <<<dim3(row_blocks * splits), dim3(kWave * batch_waves<NB, VG, RG>()), 0, st>>>(a, row_blocks, splits);
+}
+
 template <int FMT, int NB>
 static int launch_batch_nb(const GemvArgs &a, hipStream_t st) {
-  const int row_blocks = (a.Npad + 255) / 256, splits = a.Kp / kRotChunk;
-  constexpr int VG = NB >= 4 ? NB / 4 : 1;   // vectors per wave: 16 waves from 4 vectors up
-  lut_gemv_batch_kernel<FMT, NB, VG>
-      <<<dim3(row_blocks * splits), dim3(kWave * batch_waves<NB, VG>()), 0, st>>>(a, row_blocks, splits);
+  const int splits = a.Kp / kRotChunk;
+  // Rows per workgroup: 256 while that leaves a workgroup per CU, else fewer.
+  const auto grid = [&](int rg) { return (a.Npad + rg * kWave - 1) / (rg * kWave) * splits; };
+  if (grid(4) >= kBatchMinGrid) launch_batch_rg<FMT, NB, 4>(a, splits, st);
+  else if (grid(2) >= kBatchMinGrid) launch_batch_rg<FMT, NB, 2>(a, splits, st);
+  else launch_batch_rg<FMT, NB, 1>(a, splits, st);
   batched_reduce_kernel<<<dim3((a.rows + kWave - 1) / kWave, NB), dim3(kWave), 0, st>>>(a.partials, splits, a.Npad,
                                                                                      a.rows, a.bias, a.resid, a.y);
   hipError_t e = hipGetLastError();

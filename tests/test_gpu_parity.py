@@ -302,6 +302,21 @@ def test_batched_gemv(cuda, fmt, batch, rows, cols):
         assert rel_max_err(y[b], ref) < TOL, f"vector {b}"
 
 
+@pytest.mark.parametrize("fmt", [1, 3, 5, 6])
+@pytest.mark.parametrize("batch", [7, 16])
+@pytest.mark.parametrize("rows,cols", [(4160, 4096), (2112, 4096)])
+def test_batched_gemv_row_groups(cuda, fmt, batch, rows, cols):
+    # 256 rows per workgroup (4160 x 4096) and 128 (2112 x 4096), each with a
+    # last workgroup whose upper row groups lie past the matrix
+    planes, scales, g = synth.make_weights(fmt, rows, cols, seed=fmt * 7 + batch, group=128)
+    xs = np.stack([synth.make_activations(cols, seed=2000 + s, outliers=True) for s in range(batch)])
+    w = L.Weight.from_planes(fmt, planes, scales, rows, cols, g)
+    y = w.gemv(dev(xs.ravel()), flags=L.ROTATE_FWHT256).cpu().numpy().reshape(batch, rows)
+    for b in range(batch):
+        ref = oracle_planes_gemv(fmt, planes, scales, rows, cols, g, xs[b], L.ROTATE_FWHT256)
+        assert rel_max_err(y[b], ref) < TOL, f"vector {b}"
+
+
 def test_batched_linear_bias_and_repeat(cuda):
     rows, cols, batch = 2048, 2048, 16
     planes, scales, g = synth.make_weights(L.FMT_INT4, rows, cols, seed=5)
