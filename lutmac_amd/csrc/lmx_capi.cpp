@@ -90,6 +90,7 @@ int choose_fullk(int fmt, size_t Npad, size_t Kp, int kfamily) {
     return size_t(f.waves * f.h * f.cps) >= Kc && fullk_lds_bytes(f.waves, f.h, f.cps, Kc) <= kMaxLdsBytes;
   };
   if (env >= 0) return (env == 0 || !fits(env)) ? kFullK_None : env;
+  const bool wide = env_int("LMX_FULLK_WIDE", 1) != 0;   // 0: auto never picks 8 rows x 64 slices
   auto workgroups = [&](int cfg) { return Npad / size_t(kWave / fullk_shape(cfg).h); };
   // Measured on MI355X (4-bit, decode shapes):
   //  * K <= 2048: 4 waves x 16 rows per workgroup wins from N = 256 up to
@@ -107,7 +108,8 @@ int choose_fullk(int fmt, size_t Npad, size_t Kp, int kfamily) {
   }
   int best = kFullK_None;
   size_t best_wg = 0, best_slots = 0;
-  for (int cfg = kFullK_16x2x2; cfg <= kFullK_4x4x1; ++cfg) {
+  for (int cfg = kFullK_16x2x2; cfg <= kFullK_8x8x1; ++cfg) {
+    if (cfg == kFullK_8x8x1 && !wide) continue;
     if (!fits(cfg)) continue;
     const FullKShape f = fullk_shape(cfg);
     const size_t wg = workgroups(cfg), slots = size_t(f.waves * f.h * f.cps);

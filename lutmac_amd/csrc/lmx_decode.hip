@@ -554,7 +554,8 @@ struct lmx_decoder {
   float *attn_part = nullptr;            // [n_heads][chunks][m, l, -, -, o[head_dim]]
   float *attn_out = nullptr;             // [n_heads * head_dim] merged attention output
   unsigned *attn_tickets = nullptr;      // [n_kv_heads] chunk tickets (zero between steps)
-  float *normed = nullptr, *act = nullptr;   // batch > 1: RMSNorm output [hidden], SiLU*up [ffn] rows
+  float *normed = nullptr;   // batch > 1: RMSNorm output [hidden] rows
+  float *act = nullptr;      // SiLU(gate)*up [ffn] rows
   unsigned *argmax_ticket = nullptr;         // batch > 1: argmax_rows_kernel's ticket
   size_t kv_seq = 0;                         // floats of one sequence's K (or V) cache, all layers
   unsigned long long *amax = nullptr;    // per-wave argmax keys of the head GEMV
@@ -585,9 +586,26 @@ struct lmx_decoder {
 
 namespace {
 
-int gemv(const lmx_weight *w, const float *x, float *y, const float *bias, int xmode, const float *xw, float eps,
-         hipStream_t st, unsigned long long *amax = nullptr) {
+GemvArgs decode_args(const lmx_weight *w, int xmode, int epi) {
   GemvArgs a = weight_args(w);
+  a.rotate = rotates(w->format) ? LMX_ROTATE_FWHT256 : LMX_ROTATE_NONE;
+  a.xmode = xmode;
+  a.epi = epi;
+  return a;
+}
+
+// The gate|up launch writes SiLU(gate)*up itself (kEpiSiluPair) where its
+// kernel plan serves that epilogue; else (or with LMX_SILU_PAIR=0) the down
+// projection forms it in its table prologue.
+bool gate_up_pairs(const lmx_weight *gate_up) {
+  const char *e = std::getenv("LMX_SILU_PAIR");
+  return (!e || std::atoi(e) != 0) && silu_pair_rows(gate_up->format, decode_args(gate_up, kXModeRmsNorm, kEpiSiluPair)) > 0;
+}
+
+int gemv(const lmx_weight *w, const float *x, float *y, const float *bias, int xmode, const float *xw, float eps,
+         hipStream_t st, unsigned long long *amax = nullptr, int epi = kEpiStore) {
+  GemvArgs a = weight_args(w);
+  a.epi = epi;
   a.amax = amax;
   a.x = x;
   a.y = y;
@@ -756,10 +774,17 @@ int step(lmx_decoder *d, float *logits_out, hipStream_t st) {
     const lmx_decoder::Layer &L = d->layers[l];
     if ((r = gemv(L.qkv, d->hidden, d->qkv, L.qkv_bias, kXModeRmsNorm, L.in_norm, c.rms_eps, st)) ||
         (r = attention(d, l, st)) ||
-        (r = gemv(L.o, d->attn_out, d->hidden, d->hidden, kXModeNone, nullptr, 0.0f, st)) ||
-        (r = gemv(L.gate_up, d->hidden, d->gate_up, nullptr, kXModeRmsNorm, L.post_norm, c.rms_eps, st)) ||
-        (r = gemv(L.down, d->gate_up, d->hidden, d->hidden, kXModeSiluMul, nullptr, 0.0f, st)))
+        (r = gemv(L.o, d->attn_out, d->hidden, d->hidden, kXModeNone, nullptr, 0.0f, st)))
       return r;
+    if (gate_up_pairs(L.gate_up)) {
+      if ((r = gemv(L.gate_up, d->hidden, d->act, nullptr, kXModeRmsNorm, L.post_norm, c.rms_eps, st, nullptr,
+                    kEpiSiluPair)) ||
+          (r = gemv(L.down, d->act, d->hidden, d->hidden, kXModeNone, nullptr, 0.0f, st)))
+        return r;
+    } else if ((r = gemv(L.gate_up, d->hidden, d->gate_up, nullptr, kXModeRmsNorm, L.post_norm, c.rms_eps, st)) ||
+               (r = gemv(L.down, d->gate_up, d->hidden, d->hidden, kXModeSiluMul, nullptr, 0.0f, st))) {
+      return r;
+    }
   }
   float *lg = logits_out ? logits_out : d->logits;
   if ((r = gemv(d->head, d->hidden, lg, nullptr, kXModeRmsNorm, d->final_norm, c.rms_eps, st, d->amax))) return r;
@@ -854,7 +879,7 @@ int lmx_decoder_create_batched(const lmx_decoder_config *cfg, size_t batch, lmx_
       (st = d->alloc(reinterpret_cast<void **>(&d->attn_out), B * c.n_heads * c.head_dim * sizeof(float))) ||
       (st = d->alloc(reinterpret_cast<void **>(&d->attn_tickets), B * c.n_kv_heads * sizeof(unsigned))) ||
       (B > 1 && (st = d->alloc(reinterpret_cast<void **>(&d->normed), B * c.hidden * 4))) ||
-      (B > 1 && (st = d->alloc(reinterpret_cast<void **>(&d->act), B * c.ffn * 4))) ||
+      (st = d->alloc(reinterpret_cast<void **>(&d->act), B * c.ffn * 4)) ||
       (B > 1 && (st = d->alloc(reinterpret_cast<void **>(&d->argmax_ticket), sizeof(unsigned)))) ||
       (st = upload(d, &d->freq, fr.data(), fr.size()))) {
     delete d;

@@ -66,7 +66,18 @@ struct GemvArgs {
   const float *xw;         // kXModeRmsNorm: norm weight [cols]
   float eps;               // kXModeRmsNorm: epsilon
   unsigned long long *amax;  // when set: per-wave argmax keys of y (gemv_argmax_slots of them)
+  int epi;                 // output epilogue (kEpi*)
 };
+
+// Output epilogues of the full-K kernels:
+//   kEpiStore:     y[r] = (W x')[r] (+ bias[r])
+//   kEpiSiluPair:  rows = 2h (a fused gate|up weight): y[j] = silu(g_j) * u_j for
+//                  j < h, g_j = row j, u_j = row h + j (each + bias); a
+//                  workgroup computes gate rows and the matching up rows
+//                  (model.cpp:36,413-416), so the activation of the down
+//                  projection leaves the gate|up launch already formed
+constexpr int kEpiStore = 0;
+constexpr int kEpiSiluPair = 1;
 
 // Activation transforms applied while the tables are built:
 //   kXModeRmsNorm:  x'[k] = x[k] * inv_rms * xw[k], inv_rms = 1/sqrt(sum x^2 / cols + eps)
@@ -88,7 +99,8 @@ enum {
   kFullK_8x2x1 = 3,   // 32 rows, 16 slices of 128: K <= 2048
   kFullK_16x1x1 = 4,  // 64 rows, 16 slices of 128: K <= 2048
   kFullK_16x4x1 = 5,  // 16 rows, 64 slices of 128: K <= 8192
-  kFullK_4x4x1 = 6    // 16 rows, 16 slices of 128: K <= 2048
+  kFullK_4x4x1 = 6,   // 16 rows, 16 slices of 128: K <= 2048
+  kFullK_8x8x1 = 7    // 8 rows, 64 slices of 128: K <= 8192
 };
 
 constexpr size_t kMaxLdsBytes = 160 * 1024;  // LDS per workgroup on gfx950
@@ -110,6 +122,7 @@ inline FullKShape fullk_shape(int cfg) {
   case kFullK_16x1x1: return {16, 1, 1};
   case kFullK_16x4x1: return {16, 4, 1};
   case kFullK_4x4x1: return {4, 4, 1};
+  case kFullK_8x8x1: return {8, 8, 1};
   }
   return {0, 0, 0};
 }
@@ -130,6 +143,9 @@ constexpr int kReduceFenceAll = 1;  // same, with a device fence in every thread
 constexpr int kReduceTwoPass = 2;   // partials, then a separate reduce kernel
 
 int launch_gemv(int fmt, const GemvArgs &a, void *stream);
+// Rows of one output half a workgroup covers with kEpiSiluPair for these
+// arguments (format, plan, transform), 0 when that epilogue is not served.
+int silu_pair_rows(int fmt, const GemvArgs &a);
 // nb (2, 4, 8, 16) vectors at a.x + n*cols -> a.y + n*rows; a.partials holds
 // nb * (Kp/256) * Npad floats.
 int launch_gemv_batch(int fmt, const GemvArgs &a, int nb, void *stream);

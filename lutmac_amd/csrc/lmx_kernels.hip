@@ -227,7 +227,8 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restr
 // sit in LDS (16 B per activation); each 256-chunk is rotated by one wave.
 // Slice s keeps its tables at s*(CPS*2048 + 256) bytes; with H = 4, two
 // quarter-wave slices share an LDS pass, so odd slices are shifted by 64 B
-// into other banks (the shift rides in bits 6-7 of the nibble byte).  At the
+// into other banks (the shift rides in bits 6-7 of the nibble byte); with
+// H = 8 four slices share a pass and the same shift halves their overlap.  At the
 // end the NS = WAVES*H slice partials of each row are summed in slice order.
 template <int WAVES, int H, int CPS>
 constexpr uint32_t fullk_prefix_bytes() {
@@ -236,7 +237,7 @@ constexpr uint32_t fullk_prefix_bytes() {
 
 template <int H>
 __device__ __forceinline__ uint32_t slice_shift(int s) {
-  return (H == 4 && (s & 1)) ? 64u : 0u;
+  return ((H == 4 || H == 8) && (s & 1)) ? 64u : 0u;
 }
 
 template <int FMT, int WAVES, int H, int CPS, bool STAGED>
@@ -399,12 +400,15 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_fullk_kernel(GemvArgs 
 // scale addresses in 32-bit offsets with a shift for the scale group, x
 // rotated (ROT) without its final 1/16 (folded into the scales), every wave
 // building the tables of its own 256-chunks only, and the activation
-// transform XM (kXMode*) fixed at compile time.  Needs H*CPS even (each
-// wave owns whole 256-chunks).  No argmax epilogue.
-template <int FMT, bool ROT, int WAVES, int H, int CPS, int XM>
+// transform XM (kXMode*) and the epilogue EPI (kEpi*) fixed at compile
+// time.  Needs H*CPS even (each wave owns whole 256-chunks).  No argmax
+// epilogue.
+template <int FMT, bool ROT, int WAVES, int H, int CPS, int XM, int EPI = kEpiStore>
 __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_plain_kernel(GemvArgs a) {
   constexpr int P = Fmt<FMT>::P, NA = Fmt<FMT>::NA, S = Fmt<FMT>::S;
   constexpr int RW = kWave / H;
+  constexpr bool PAIR = EPI == kEpiSiluPair;
+  constexpr int HR = RW / 2;   // PAIR: gate rows (then as many up rows) per workgroup
   constexpr int NS = WAVES * H;
   constexpr uint32_t SSTRIDE = stag_slice_bytes(CPS);
   constexpr int XJ = H * CPS / 2;
@@ -421,7 +425,9 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_plain_kernel(GemvArgs 
   const int wave = threadIdx.x / kWave;
   const int s = wave * H + lane / RW;
   const int rl = lane % RW;
-  const int row = blockIdx.x * RW + rl;
+  // PAIR: the workgroup's rows are gate rows blockIdx.x*HR + [0, HR) and the
+  // up rows rows/2 + blockIdx.x*HR + [0, HR) (the host checks rows/2 % HR == 0)
+  const int row = PAIR ? (rl < HR ? 0 : a.rows / 2 - HR) + blockIdx.x * HR + rl : blockIdx.x * RW + rl;
   const int lr = min(row, a.Npad - 1);
 
   // ---- x of this wave's 256-chunks (clamped in bounds, masked below) ----
@@ -535,7 +541,19 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_plain_kernel(GemvArgs 
   // ---- in-workgroup reduction over the k-slices, fixed order --------------
   red[s * RW + rl] = acc;
   __syncthreads();
-  if (threadIdx.x < RW) {
+  if constexpr (PAIR) {
+    if (threadIdx.x < HR) {
+      const int j = blockIdx.x * HR + threadIdx.x, h = a.rows / 2;
+      float g = 0.0f, u = 0.0f;
+#pragma unroll 8
+      for (int k = 0; k < NS; ++k) {
+        g += red[k * RW + threadIdx.x];
+        u += red[k * RW + HR + threadIdx.x];
+      }
+      if (a.bias) g += a.bias[j], u += a.bias[h + j];
+      a.y[j] = silu(g) * u;
+    }
+  } else if (threadIdx.x < RW) {
     const int r = blockIdx.x * RW + threadIdx.x;
     float t = 0.0f;
 #pragma unroll 8
@@ -671,19 +689,22 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_ipl_kernel(GemvArgs a)
   }
 }
 
-template <int FMT, bool ROT, int WAVES, int H, int CPS, int XM>
+template <int WAVES, int H, int CPS>
+constexpr size_t plain_lds_bytes(size_t Kc) {
+  return fullk_prefix_bytes<WAVES, H, CPS>() + (Kc + CPS - 1) / CPS * stag_slice_bytes(CPS);
+}
+
+template <int FMT, bool ROT, int WAVES, int H, int CPS, int XM, int EPI = kEpiStore>
 static int launch_plain_kernel(const GemvArgs &a, hipStream_t st) {
-  const size_t Kc = size_t(a.Kp / kChunk);
-  const size_t lds = fullk_prefix_bytes<WAVES, H, CPS>() + (Kc + CPS - 1) / CPS * stag_slice_bytes(CPS);
+  const size_t lds = plain_lds_bytes<WAVES, H, CPS>(size_t(a.Kp / kChunk));
   if (lds > kMaxLdsBytes) return 1;   // staggered tables do not fit: the generic kernel serves it
   static const hipError_t attr = hipFuncSetAttribute(
-      reinterpret_cast<const void *>(&lut_gemv_plain_kernel<FMT, ROT, WAVES, H, CPS, XM>),
+      reinterpret_cast<const void *>(&lut_gemv_plain_kernel<FMT, ROT, WAVES, H, CPS, XM, EPI>),
       hipFuncAttributeMaxDynamicSharedMemorySize, int(kMaxLdsBytes));
   if (attr != hipSuccess) return fail(LMX_ERR_LAUNCH_FAILED, "hipFuncSetAttribute: %s", hipGetErrorString(attr));
-  if (lds > kMaxLdsBytes) return fail(LMX_ERR_INVALID_ARGUMENT, "full-K tables need %zu B of LDS", lds);
   constexpr int RW = kWave / H;
-  lut_gemv_plain_kernel<FMT, ROT, WAVES, H, CPS, XM>
-      <<<dim3((a.Npad + RW - 1) / RW), dim3(WAVES * kWave), lds, st>>>(a);
+  const int blocks = EPI == kEpiSiluPair ? a.rows / RW : (a.Npad + RW - 1) / RW;
+  lut_gemv_plain_kernel<FMT, ROT, WAVES, H, CPS, XM, EPI><<<dim3(blocks), dim3(WAVES * kWave), lds, st>>>(a);
   return LMX_OK;
 }
 
@@ -704,6 +725,13 @@ static int launch_plain_cfg(const GemvArgs &a, hipStream_t st) {
   // Interleaved where it measured faster: two k-slices per wave and at least
   // two steps per wave (one step has nothing to interleave; 17920 x 1536
   // ran 40% slower that way), RRQ-3 excepted (4% slower at 8192^2).
+  if (a.epi == kEpiSiluPair) {
+    // gate|up of the decode step: RMSNorm in, SiLU(gate)*up out (4-bit, unrotated)
+    if constexpr (FMT == LMX_FMT_INT4)
+      if (a.rotate == LMX_ROTATE_NONE && a.xmode == kXModeRmsNorm && a.rows % (kWave / H) == 0)
+        return launch_plain_kernel<FMT, false, WAVES, H, CPS, kXModeRmsNorm, kEpiSiluPair>(a, st);
+    return 1;
+  }
   if (a.xmode != kXModeNone) {
     // Fused transforms on the lean kernel: the decode step's linears (4-bit,
     // unrotated); other formats take the generic kernel.
@@ -738,6 +766,7 @@ static int launch_plain(const GemvArgs &a, hipStream_t st) {
   case kFullK_8x2x1: return launch_plain_cfg<FMT, 8, 2, 1>(a, st);
   case kFullK_16x4x1: return launch_plain_cfg<FMT, 16, 4, 1>(a, st);
   case kFullK_4x4x1: return launch_plain_cfg<FMT, 4, 4, 1>(a, st);
+  case kFullK_8x8x1: return launch_plain_cfg<FMT, 8, 8, 1>(a, st);
   }
   return 1;
 }
@@ -783,12 +812,15 @@ static int launch_fullk(const GemvArgs &a, hipStream_t st) {
   case kFullK_16x1x1: return launch_fullk_cfg<FMT, 16, 1, 1>(a, st);
   case kFullK_16x4x1: return launch_fullk_cfg<FMT, 16, 4, 1>(a, st);
   case kFullK_4x4x1: return launch_fullk_cfg<FMT, 4, 4, 1>(a, st);
+  case kFullK_8x8x1: return launch_fullk_cfg<FMT, 8, 8, 1>(a, st);
   }
   return fail(LMX_ERR_INVALID_ARGUMENT, "unknown full-K configuration %d", a.fullk);
 }
 
 template <int FMT>
 static int launch_fmt(const GemvArgs &a, hipStream_t st) {
+  if (a.epi != kEpiStore && silu_pair_rows(FMT, a) == 0)
+    return fail(LMX_ERR_INVALID_ARGUMENT, "the SiLU-pair epilogue is not served for this weight and transform");
   if (a.fullk) {
     int r = 1;
     if (!a.amax && a.kfamily != kKernelGeneric) r = launch_plain<FMT>(a, st);
@@ -813,6 +845,25 @@ static int launch_fmt(const GemvArgs &a, hipStream_t st) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(LMX_ERR_LAUNCH_FAILED, "lut_gemv launch: %s", hipGetErrorString(e));
   return LMX_OK;
+}
+
+int silu_pair_rows(int fmt, const GemvArgs &a) {
+  if (fmt != LMX_FMT_INT4 || a.rotate != LMX_ROTATE_NONE || a.xmode != kXModeRmsNorm || a.amax ||
+      a.kfamily == kKernelGeneric)
+    return 0;
+  const size_t Kc = size_t(a.Kp / kChunk);
+  size_t lds = 0;
+  switch (a.fullk) {
+  case kFullK_16x2x2: lds = plain_lds_bytes<16, 2, 2>(Kc); break;
+  case kFullK_16x2x3: lds = plain_lds_bytes<16, 2, 3>(Kc); break;
+  case kFullK_8x2x1: lds = plain_lds_bytes<8, 2, 1>(Kc); break;
+  case kFullK_16x4x1: lds = plain_lds_bytes<16, 4, 1>(Kc); break;
+  case kFullK_4x4x1: lds = plain_lds_bytes<4, 4, 1>(Kc); break;
+  case kFullK_8x8x1: lds = plain_lds_bytes<8, 8, 1>(Kc); break;
+  default: return 0;   // split-K, or a configuration only the generic kernel serves
+  }
+  const int rw = kWave / fullk_shape(a.fullk).h;
+  return lds <= kMaxLdsBytes && a.rows % rw == 0 ? rw / 2 : 0;
 }
 
 size_t gemv_argmax_slots(const GemvArgs &a) {

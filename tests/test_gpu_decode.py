@@ -74,6 +74,29 @@ def test_decoder_long_ffn(cuda):
     check_against(dec, oracle.OracleDecoder(m), toks)
 
 
+@pytest.mark.parametrize("ffn", [768, 4096])
+def test_decoder_silu_pair_epilogue(cuda, monkeypatch, ffn):
+    # gate|up writing SiLU(gate)*up itself (the 4-bit batch-1 step) against
+    # the down projection forming it (LMX_SILU_PAIR=0): the same values, and
+    # both within the bar of the oracle.  ffn 4096 gives down (512 x 4096)
+    # the 8-row x 64-slice plan
+    cfg = D.small_config(hidden=512, ffn=ffn, vocab=900, rope_mode=D.ROPE_REFERENCE, rope_factor=1.0,
+                         rope_theta=1e6)
+    m = D.SyntheticModel(cfg, seed=41 + ffn, group=128, random_norms=True)
+    toks = np.random.default_rng(42).integers(0, cfg.vocab, 10)
+    dec = D.Decoder(m)
+    if ffn == 4096:
+        assert dec.weights[3].kernel_config()[0] == 7
+    paired = device_logits(dec, toks)
+    monkeypatch.setenv("LMX_SILU_PAIR", "0")
+    unpaired = device_logits(D.Decoder(m), toks)
+    ref = oracle.OracleDecoder(m)
+    for pos, t in enumerate(toks):
+        want = ref.step(t, pos)
+        assert rel_max_err(paired[pos], unpaired[pos]) < 1e-6, pos
+        assert rel_max_err(paired[pos], want) < DECODE_TOL, pos
+
+
 @pytest.mark.parametrize("head_dim,n_heads,n_kv", [(64, 8, 2), (128, 12, 2)])
 def test_decoder_multi_chunk_context(cuda, head_dim, n_heads, n_kv):
     # 150 positions span three 64-position attention chunks (a fourth, empty,

@@ -219,6 +219,7 @@ PLAN_SHAPES = {
     4: (130, 1536),   # 16 x 1 x 1
     5: (40, 8192),    # 16 x 4 x 1
     6: (33, 2048),    # 4 x 4 x 1
+    7: (44, 7936),    # 8 x 8 x 1 (a ragged last workgroup, 62 of 64 slices used)
 }
 
 
