@@ -538,15 +538,19 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_plain_kernel(GemvArgs 
     }
   }
 
-  // ---- in-workgroup reduction over the k-slices, fixed order --------------
-  red[s * RW + rl] = acc;
+  // ---- in-workgroup reduction: a wave's H slices of a row by a lane
+  // butterfly, then the waves in order (fixed, so deterministic) -----------
+  {
+    const float wsum = strided_sum<RW>(acc, lane);
+    if (lane < RW) red[wave * RW + rl] = wsum;
+  }
   __syncthreads();
   if constexpr (PAIR) {
     if (threadIdx.x < HR) {
       const int j = blockIdx.x * HR + threadIdx.x, h = a.rows / 2;
       float g = 0.0f, u = 0.0f;
 #pragma unroll 8
-      for (int k = 0; k < NS; ++k) {
+      for (int k = 0; k < WAVES; ++k) {
         g += red[k * RW + threadIdx.x];
         u += red[k * RW + HR + threadIdx.x];
       }
@@ -557,7 +561,7 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_plain_kernel(GemvArgs 
     const int r = blockIdx.x * RW + threadIdx.x;
     float t = 0.0f;
 #pragma unroll 8
-    for (int k = 0; k < NS; ++k) t += red[k * RW + threadIdx.x];
+    for (int k = 0; k < WAVES; ++k) t += red[k * RW + threadIdx.x];
     if (r < a.rows) a.y[r] = a.bias ? t + a.bias[r] : t;
   }
 }
@@ -579,7 +583,6 @@ template <int FMT, bool ROT, int WAVES, int CPS>
 __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_ipl_kernel(GemvArgs a) {
   constexpr int P = Fmt<FMT>::P, NA = Fmt<FMT>::NA, S = Fmt<FMT>::S;
   constexpr int RW = kWave / 2;
-  constexpr int NS = WAVES * 2;
   constexpr uint32_t PREFIX = ipl_prefix_bytes<WAVES, CPS>();
   extern __shared__ __attribute__((aligned(256))) float lds[];
   const int Kc = a.Kp / kChunk;
@@ -677,14 +680,18 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_ipl_kernel(GemvArgs a)
     acc = ch < Kc ? nacc : acc;
   }
 
-  // ---- in-workgroup reduction over the 2*WAVES slices, fixed order ----
-  red[(wave * 2 + h) * RW + rl] = acc;
+  // ---- in-workgroup reduction: the two half-wave slices of a row by a
+  // lane swap, then the waves in order (fixed, so deterministic) ----------
+  {
+    const float wsum = strided_sum<RW>(acc, lane);
+    if (h == 0) red[wave * RW + rl] = wsum;
+  }
   __syncthreads();
   if (threadIdx.x < RW) {
     const int r = blockIdx.x * RW + threadIdx.x;
     float t = 0.0f;
 #pragma unroll 8
-    for (int k = 0; k < NS; ++k) t += red[k * RW + threadIdx.x];
+    for (int k = 0; k < WAVES; ++k) t += red[k * RW + threadIdx.x];
     if (r < a.rows) a.y[r] = a.bias ? t + a.bias[r] : t;
   }
 }
@@ -1030,24 +1037,36 @@ __global__ __launch_bounds__((kWave * batch_waves<NB, VG, RG>())) void lut_gemv_
 
 // y[n*rows + r] = sum_s partials[n][s][r] (+ bias[r]) (+ resid[n*rows + r])
 // in split order; resid may be y itself (each element is read and written
-// by one thread).
-__global__ __launch_bounds__(64) void batched_reduce_kernel(const float *__restrict__ partials, int splits, int Npad,
-                                                            int rows, const float *__restrict__ bias,
-                                                            const float *resid, float *y) {
-  const int r = blockIdx.x * kWave + threadIdx.x, n = blockIdx.y;
-  if (r >= rows) return;
-  const float *p = partials + size_t(n) * splits * Npad + r;
-  float s = 0.0f;
-  for (int k0 = 0; k0 < splits; k0 += 32) {   // 32 loads in flight, summed in split order
-    float v[32];
+// by one thread).  A thread sums 4 consecutive rows with 16-byte loads (Npad
+// is a multiple of 64, so the 4 rows of any r0 < rows lie inside the padded
+// partials).
+constexpr int kReduceThreads = 256;
+__global__ __launch_bounds__(kReduceThreads) void batched_reduce_kernel(const float *__restrict__ partials,
+                                                                        int splits, int Npad, int rows,
+                                                                        const float *__restrict__ bias,
+                                                                        const float *resid, float *y) {
+  const int r0 = 4 * int(blockIdx.x * kReduceThreads + threadIdx.x), n = blockIdx.y;
+  if (r0 >= rows) return;
+  const float4 *p = reinterpret_cast<const float4 *>(partials + size_t(n) * splits * Npad + r0);
+  const size_t step = size_t(Npad) / 4;
+  float4 s = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  for (int k0 = 0; k0 < splits; k0 += 16) {   // 16 loads in flight, summed in split order
+    float4 v[16];
 #pragma unroll
-    for (int j = 0; j < 32; ++j) v[j] = k0 + j < splits ? p[size_t(k0 + j) * Npad] : 0.0f;
+    for (int j = 0; j < 16; ++j) v[j] = k0 + j < splits ? p[size_t(k0 + j) * step] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
-    for (int j = 0; j < 32; ++j) s += v[j];
+    for (int j = 0; j < 16; ++j) s.x += v[j].x, s.y += v[j].y, s.z += v[j].z, s.w += v[j].w;
   }
-  if (bias) s += bias[r];
-  if (resid) s += resid[size_t(n) * rows + r];
-  y[size_t(n) * rows + r] = s;
+  const float t[4] = {s.x, s.y, s.z, s.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = r0 + i;
+    if (r >= rows) break;
+    float v = t[i];
+    if (bias) v += bias[r];
+    if (resid) v += resid[size_t(n) * rows + r];
+    y[size_t(n) * rows + r] = v;
+  }
 }
 
 template <int FMT, int NB, int RG>
@@ -1066,7 +1085,8 @@ static int launch_batch_nb(const GemvArgs &a, hipStream_t st) {
   if (grid(4) >= kBatchMinGrid) launch_batch_rg<FMT, NB, 4>(a, splits, st);
   else if (grid(2) >= kBatchMinGrid) launch_batch_rg<FMT, NB, 2>(a, splits, st);
   else launch_batch_rg<FMT, NB, 1>(a, splits, st);
-  batched_reduce_kernel<<<dim3((a.rows + kWave - 1) / kWave, NB), dim3(kWave), 0, st>>>(a.partials, splits, a.Npad,
+  batched_reduce_kernel<<<dim3((a.rows + 4 * kReduceThreads - 1) / (4 * kReduceThreads), NB), dim3(kReduceThreads), 0,
+                          st>>>(a.partials, splits, a.Npad,
                                                                                      a.rows, a.bias, a.resid, a.y);
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? LMX_OK : fail(LMX_ERR_LAUNCH_FAILED, "batched lut_gemv launch: %s", hipGetErrorString(e));

@@ -80,6 +80,19 @@ __device__ __forceinline__ float lane_sum(float v, int lane) {
   else return v;
 }
 
+// Butterfly sum over the lanes that share lane % RW (RW a power of two):
+// lane ^ d for d = 32, 16, ..., RW; every lane of such a set ends with the
+// same bits.
+template <int RW, int D = 32>
+__device__ __forceinline__ float strided_sum(float v, int lane) {
+  if constexpr (D >= RW && D >= 1) {
+    v += lane_xor<D>(v, lane);
+    return strided_sum<RW, D / 2>(v, lane);
+  } else {
+    return v;
+  }
+}
+
 template <int D>
 __device__ __forceinline__ float lane_max(float v, int lane) {
   v = fmaxf(v, lane_xor<D>(v, lane));
