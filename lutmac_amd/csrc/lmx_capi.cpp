@@ -263,16 +263,22 @@ int stage_if_needed(const lmx_weight *w, GemvArgs &a, void *stream) {
 int gemv_batched(const lmx_weight *w, GemvArgs a, const float *x, float *y, size_t batch, void *stream,
                  size_t *done) {
   *done = 0;
+  if (a.epi != kEpiStore && !batched_epilogue_ok(w, a.epi, batch))
+    return fail(LMX_ERR_INVALID_ARGUMENT, "batched epilogue %d does not cover %zu vectors of a %zu x %zu weight", a.epi,
+                batch, w->rows, w->cols);
   if (!w->batched || batch < 4 || reinterpret_cast<size_t>(x) % 16 || w->cols % 4) return LMX_OK;
   const size_t splits = w->Kp / kRotChunk;
   const float *resid = a.resid;   // [batch][rows] residual rows, offset with the vectors
+  float *y2 = a.y2;               // kEpiNormOut: [batch][rows]
+  const size_t out_rows = a.epi == kEpiSiluPair ? w->rows / 2 : w->rows;
   while (batch - *done >= 4) {
     const size_t left = batch - *done;
     const int nb = left >= 16 ? 16 : left >= 8 ? 8 : 4;
     if (size_t(nb) * splits * w->Npad > w->bpartials_cap)
       return fail(LMX_ERR_INVALID_ARGUMENT, "batched partials of %zu floats hold no group of %d", w->bpartials_cap, nb);
     a.x = x + *done * w->cols;
-    a.y = y + *done * w->rows;
+    a.y = y + *done * out_rows;
+    a.y2 = y2 ? y2 + *done * w->rows : nullptr;
     a.resid = resid ? resid + *done * w->rows : nullptr;
     a.cols = int(w->cols);
     a.partials = w->d_bpartials;
@@ -281,6 +287,13 @@ int gemv_batched(const lmx_weight *w, GemvArgs a, const float *x, float *y, size
     *done += size_t(nb);
   }
   return LMX_OK;
+}
+
+bool batched_epilogue_ok(const lmx_weight *w, int epi, size_t batch) {
+  if (!w->batched || batch < 4 || batch % 4 || w->cols % 4) return false;   // every vector in a group of 16/8/4
+  if (epi == kEpiSiluPair) return w->rows % 8 == 0;
+  if (epi == kEpiNormOut) return w->rows <= size_t(kNormOutMaxRows);
+  return epi == kEpiStore;
 }
 
 GemvArgs weight_args(const lmx_weight *w) {

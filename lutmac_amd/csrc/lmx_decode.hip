@@ -725,20 +725,88 @@ int gemv_rows(const lmx_decoder *d, const lmx_weight *w, const float *x, float *
   return LMX_OK;
 }
 
+// The decoder's rows through the batched kernel with a fused epilogue:
+// kEpiNormOut (y = W x + resid, y2 = RMSNorm(y) with weight xw) or
+// kEpiSiluPair (y = SiLU(gate)*up rows); every row must be covered
+// (rows_fuse checks that first).
+int gemv_rows_epi(const lmx_decoder *d, const lmx_weight *w, const float *x, float *y, const float *resid, int epi,
+                  const float *xw, float *y2, hipStream_t st) {
+  GemvArgs a = weight_args(w);
+  a.rotate = rotates(w->format) ? LMX_ROTATE_FWHT256 : LMX_ROTATE_NONE;
+  a.resid = resid;
+  a.epi = epi;
+  a.xw = xw;
+  a.eps = d->cfg.rms_eps;
+  a.y2 = y2;
+  size_t done = 0;
+  const int r = gemv_batched(w, a, x, y, d->batch, st, &done);
+  if (r) return r;
+  return done == d->batch ? LMX_OK
+                          : fail(LMX_ERR_INVALID_ARGUMENT, "fused batched epilogue covered %zu of %zu rows", done,
+                                 d->batch);
+}
+
+// Whether every layer's o / gate|up / down serve the fused epilogues for the
+// decoder's batch (LMX_FUSED_ROWS=0: never; the norms and SiLU*up then run
+// as row kernels).
+bool rows_fuse(const lmx_decoder *d) {
+  const char *e = std::getenv("LMX_FUSED_ROWS");
+  if (e && std::atoi(e) == 0) return false;
+  for (const lmx_decoder::Layer &L : d->layers)
+    if (!batched_epilogue_ok(L.o, kEpiNormOut, d->batch) || !batched_epilogue_ok(L.gate_up, kEpiSiluPair, d->batch) ||
+        !batched_epilogue_ok(L.down, kEpiNormOut, d->batch))
+      return false;
+  return true;
+}
+
 int rmsnorm_rows(const lmx_decoder *d, const float *x, const float *wt, float *y, hipStream_t st) {
   rmsnorm_rows_kernel<<<dim3(unsigned(d->batch)), dim3(256), 0, st>>>(x, wt, int(d->cfg.hidden), d->cfg.rms_eps, y);
   return launch_err("rmsnorm_rows");
 }
 
+int step_batched_rows(lmx_decoder *d, hipStream_t st);
+
 // One token step of `batch` sequences in lockstep: every linear reads its
-// weights once per group of sequences; the norms and SiLU*up run as row
-// kernels (the batched GEMV splits K, so it cannot fuse them), attention and
-// argmax per sequence.
+// weights once per group of sequences.  The batched GEMV splits K, so its
+// table build cannot apply the RMSNorm of its input; instead the reduction
+// that finishes the o and down projections also writes the normed rows, and
+// the gate|up reduction writes SiLU(gate)*up (when every row is in a batched
+// group; else the norms and SiLU*up run as row kernels).  Attention and the
+// argmax run per sequence.
 int step_batched(lmx_decoder *d, float *logits_out, hipStream_t st) {
   const lmx_decoder_config &c = d->cfg;
   const size_t B = d->batch;
   int r = embed(d->embed, d->tokens, d->pos, d->hidden, B, int(c.max_seq + 1), st);
   if (r) return r;
+  if (rows_fuse(d)) {
+    // The o and down reductions write the hidden rows and the next linear's
+    // normed input; the gate|up reduction writes SiLU(gate)*up.
+    if ((r = rmsnorm_rows(d, d->hidden, d->layers[0].in_norm, d->normed, st))) return r;
+    for (size_t l = 0; l < c.n_layers; ++l) {
+      const lmx_decoder::Layer &L = d->layers[l];
+      const float *next_norm = l + 1 < c.n_layers ? d->layers[l + 1].in_norm : d->final_norm;
+      if ((r = gemv_rows(d, L.qkv, d->normed, d->qkv, L.qkv_bias, nullptr, st)) || (r = attention(d, l, st)) ||
+          (r = gemv_rows_epi(d, L.o, d->attn_out, d->hidden, d->hidden, kEpiNormOut, L.post_norm, d->normed, st)) ||
+          (r = gemv_rows_epi(d, L.gate_up, d->normed, d->act, nullptr, kEpiSiluPair, nullptr, nullptr, st)) ||
+          (r = gemv_rows_epi(d, L.down, d->act, d->hidden, d->hidden, kEpiNormOut, next_norm, d->normed, st)))
+        return r;
+    }
+  } else {
+    if ((r = step_batched_rows(d, st))) return r;
+    if ((r = rmsnorm_rows(d, d->hidden, d->final_norm, d->normed, st))) return r;
+  }
+  float *lg = logits_out ? logits_out : d->logits;
+  if ((r = gemv_rows(d, d->head, d->normed, lg, nullptr, nullptr, st))) return r;
+  argmax_rows_kernel<<<dim3(unsigned(B)), dim3(1024), 0, st>>>(lg, int(c.vocab), d->tokens, int(c.max_seq + 1),
+                                                               d->pos, d->n_forced, int(c.max_seq), d->argmax_ticket);
+  return launch_err("argmax_rows");
+}
+
+// The layers of a batched step with the norms and SiLU*up as row kernels.
+int step_batched_rows(lmx_decoder *d, hipStream_t st) {
+  const lmx_decoder_config &c = d->cfg;
+  const size_t B = d->batch;
+  int r = LMX_OK;
   for (size_t l = 0; l < c.n_layers; ++l) {
     const lmx_decoder::Layer &L = d->layers[l];
     if ((r = rmsnorm_rows(d, d->hidden, L.in_norm, d->normed, st)) ||
@@ -753,13 +821,7 @@ int step_batched(lmx_decoder *d, float *logits_out, hipStream_t st) {
     if ((r = launch_err("silu_mul_rows")) || (r = gemv_rows(d, L.down, d->act, d->hidden, nullptr, d->hidden, st)))
       return r;
   }
-  float *lg = logits_out ? logits_out : d->logits;
-  if ((r = rmsnorm_rows(d, d->hidden, d->final_norm, d->normed, st)) ||
-      (r = gemv_rows(d, d->head, d->normed, lg, nullptr, nullptr, st)))
-    return r;
-  argmax_rows_kernel<<<dim3(unsigned(B)), dim3(1024), 0, st>>>(lg, int(c.vocab), d->tokens, int(c.max_seq + 1),
-                                                               d->pos, d->n_forced, int(c.max_seq), d->argmax_ticket);
-  return launch_err("argmax_rows");
+  return LMX_OK;
 }
 
 // One token step of one sequence.  The hidden state already holds the

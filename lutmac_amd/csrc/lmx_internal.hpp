@@ -67,6 +67,7 @@ struct GemvArgs {
   float eps;               // kXModeRmsNorm: epsilon
   unsigned long long *amax;  // when set: per-wave argmax keys of y (gemv_argmax_slots of them)
   int epi;                 // output epilogue (kEpi*)
+  float *y2;               // kEpiNormOut: RMSNorm of y with weight xw [rows] (batched GEMV only)
 };
 
 // Output epilogues of the full-K kernels:
@@ -76,8 +77,13 @@ struct GemvArgs {
 //                  workgroup computes gate rows and the matching up rows
 //                  (model.cpp:36,413-416), so the activation of the down
 //                  projection leaves the gate|up launch already formed
+//   kEpiNormOut:   (batched GEMV) y as kEpiStore (+ resid), and y2 = the
+//                  RMSNorm of each y row with weight xw and epsilon eps
+//                  (norm.cpp:18-34), the next linear's input
 constexpr int kEpiStore = 0;
 constexpr int kEpiSiluPair = 1;
+constexpr int kEpiNormOut = 2;
+constexpr int kNormOutMaxRows = 8192;   // kEpiNormOut keeps a whole row in LDS
 
 // Activation transforms applied while the tables are built:
 //   kXModeRmsNorm:  x'[k] = x[k] * inv_rms * xw[k], inv_rms = 1/sqrt(sum x^2 / cols + eps)
@@ -201,4 +207,7 @@ GemvArgs weight_args(const lmx_weight *w);
 // below 4).
 int gemv_batched(const lmx_weight *w, GemvArgs a, const float *x, float *y, size_t batch, void *stream,
                  size_t *done);
+// Whether gemv_batched serves epilogue epi (kEpi*) for `batch` vectors of w
+// with no vector left to the single-vector path (x 16-byte aligned assumed).
+bool batched_epilogue_ok(const lmx_weight *w, int epi, size_t batch);
 }  // namespace lmx

@@ -1069,6 +1069,93 @@ __global__ __launch_bounds__(kReduceThreads) void batched_reduce_kernel(const fl
   }
 }
 
+// kEpiSiluPair: act[n*h + j] = silu(g) * u with g / u the split-order sums
+// of rows j / h + j (+ bias), h = rows / 2 (h % 4 == 0: the up half's rows
+// keep the 16-byte alignment); the same expression as silu_mul_rows_kernel.
+__global__ __launch_bounds__(kReduceThreads) void batched_reduce_pair_kernel(const float *__restrict__ partials,
+                                                                             int splits, int Npad, int h,
+                                                                             const float *__restrict__ bias,
+                                                                             float *__restrict__ act) {
+  const int j0 = 4 * int(blockIdx.x * kReduceThreads + threadIdx.x), n = blockIdx.y;
+  if (j0 >= h) return;
+  const float4 *pg = reinterpret_cast<const float4 *>(partials + size_t(n) * splits * Npad + j0);
+  const float4 *pu = reinterpret_cast<const float4 *>(partials + size_t(n) * splits * Npad + h + j0);
+  const size_t step = size_t(Npad) / 4;
+  float4 g = make_float4(0.0f, 0.0f, 0.0f, 0.0f), u = g;
+  for (int k0 = 0; k0 < splits; k0 += 8) {   // 16 loads in flight, summed in split order
+    float4 vg[8], vu[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const bool in = k0 + k < splits;
+      vg[k] = in ? pg[size_t(k0 + k) * step] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      vu[k] = in ? pu[size_t(k0 + k) * step] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      g.x += vg[k].x, g.y += vg[k].y, g.z += vg[k].z, g.w += vg[k].w;
+      u.x += vu[k].x, u.y += vu[k].y, u.z += vu[k].z, u.w += vu[k].w;
+    }
+  }
+  const float gs[4] = {g.x, g.y, g.z, g.w}, us[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int j = j0 + i;
+    if (j >= h) break;
+    float a = gs[i], b = us[i];
+    if (bias) a += bias[j], b += bias[h + j];
+    act[size_t(n) * h + j] = a / (1.0f + expf(-a)) * b;
+  }
+}
+
+// kEpiNormOut: one workgroup per vector n: y[n] = split-order sums (+ bias)
+// (+ resid[n], which may be y itself), kept in LDS, then y2[n] = RMSNorm of
+// y[n] with weight w computed exactly as rmsnorm_rows_kernel does (the same
+// thread-to-element assignment, sum order and expression, norm.cpp:18-34), so
+// the fused and the separate forms give the same bits.
+__global__ __launch_bounds__(kReduceThreads) void batched_reduce_norm_kernel(const float *__restrict__ partials,
+                                                                             int splits, int Npad, int rows,
+                                                                             const float *__restrict__ bias,
+                                                                             const float *resid, float *y,
+                                                                             const float *__restrict__ w, float eps,
+                                                                             float *__restrict__ y2) {
+  static_assert(kReduceThreads == 256, "the RMSNorm order is rmsnorm_rows_kernel's (256 threads)");
+  extern __shared__ float row[];   // [rows]
+  __shared__ float red[4];
+  const int n = blockIdx.x;
+  const float *pn = partials + size_t(n) * splits * Npad;
+  const size_t step = size_t(Npad) / 4;
+  for (int r0 = 4 * int(threadIdx.x); r0 < rows; r0 += 4 * kReduceThreads) {
+    const float4 *p = reinterpret_cast<const float4 *>(pn + r0);
+    float4 s = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int k0 = 0; k0 < splits; k0 += 16) {
+      float4 v[16];
+#pragma unroll
+      for (int k = 0; k < 16; ++k) v[k] = k0 + k < splits ? p[size_t(k0 + k) * step] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+      for (int k = 0; k < 16; ++k) s.x += v[k].x, s.y += v[k].y, s.z += v[k].z, s.w += v[k].w;
+    }
+    const float t[4] = {s.x, s.y, s.z, s.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = r0 + i;
+      if (r >= rows) break;
+      float v = t[i];
+      if (bias) v += bias[r];
+      if (resid) v += resid[size_t(n) * rows + r];
+      y[size_t(n) * rows + r] = v;
+      row[r] = v;
+    }
+  }
+  __syncthreads();
+  float ss = 0.0f;
+  for (int k = threadIdx.x; k < rows; k += kReduceThreads) ss += row[k] * row[k];
+  ss = lane_sum<32>(ss, threadIdx.x & (kWave - 1));
+  if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = ss;
+  __syncthreads();
+  const float inv = 1.0f / sqrtf(((red[0] + red[1]) + (red[2] + red[3])) / float(rows) + eps);
+  for (int k = threadIdx.x; k < rows; k += kReduceThreads) y2[size_t(n) * rows + k] = row[k] * inv * w[k];
+}
+
 template <int FMT, int NB, int RG>
 static void launch_batch_rg(const GemvArgs &a, int splits, hipStream_t st) {
   constexpr int VG = NB >= 4 ? NB / 4 : 1;   // vectors per wave
@@ -1085,9 +1172,17 @@ static int launch_batch_nb(const GemvArgs &a, hipStream_t st) {
   if (grid(4) >= kBatchMinGrid) launch_batch_rg<FMT, NB, 4>(a, splits, st);
   else if (grid(2) >= kBatchMinGrid) launch_batch_rg<FMT, NB, 2>(a, splits, st);
   else launch_batch_rg<FMT, NB, 1>(a, splits, st);
-  batched_reduce_kernel<<<dim3((a.rows + 4 * kReduceThreads - 1) / (4 * kReduceThreads), NB), dim3(kReduceThreads), 0,
-                          st>>>(a.partials, splits, a.Npad,
-                                                                                     a.rows, a.bias, a.resid, a.y);
+  if (a.epi == kEpiSiluPair) {
+    const int h = a.rows / 2;
+    batched_reduce_pair_kernel<<<dim3((h + 4 * kReduceThreads - 1) / (4 * kReduceThreads), NB),
+                                 dim3(kReduceThreads), 0, st>>>(a.partials, splits, a.Npad, h, a.bias, a.y);
+  } else if (a.epi == kEpiNormOut) {
+    batched_reduce_norm_kernel<<<dim3(NB), dim3(kReduceThreads), size_t(a.rows) * sizeof(float), st>>>(
+        a.partials, splits, a.Npad, a.rows, a.bias, a.resid, a.y, a.xw, a.eps, a.y2);
+  } else {
+    batched_reduce_kernel<<<dim3((a.rows + 4 * kReduceThreads - 1) / (4 * kReduceThreads), NB),
+                            dim3(kReduceThreads), 0, st>>>(a.partials, splits, a.Npad, a.rows, a.bias, a.resid, a.y);
+  }
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? LMX_OK : fail(LMX_ERR_LAUNCH_FAILED, "batched lut_gemv launch: %s", hipGetErrorString(e));
 }

@@ -241,6 +241,35 @@ def test_batched_decoder_matches_oracle(cuda, batch):
     batched_check(D.Decoder(m, batch=batch), m, toks)
 
 
+@pytest.mark.parametrize("batch", [8, 16])
+def test_batched_decoder_fused_epilogues(cuda, monkeypatch, batch):
+    # o/down reductions writing the normed rows and the gate|up reduction
+    # writing SiLU(gate)*up (every row in a batched group) against the row
+    # kernels (LMX_FUSED_ROWS=0): the same bits, and the oracle's logits
+    cfg = D.small_config(hidden=512, n_heads=8, n_kv_heads=2, head_dim=64, ffn=1024, vocab=700, max_seq=64,
+                         rope_mode=D.ROPE_REFERENCE, rope_factor=1.0, rope_theta=1e6, qkv_bias=True)
+    m = D.SyntheticModel(cfg, seed=35 + batch, group=128, random_norms=True)
+    toks = np.random.default_rng(36).integers(0, cfg.vocab, (batch, 12))
+
+    def logits(dec):
+        dec.reset(toks)
+        lg = torch.empty(batch * cfg.vocab, dtype=torch.float32, device="cuda")
+        out = []
+        for _ in range(toks.shape[1]):
+            dec.step(lg)
+            out.append(lg.cpu().numpy().reshape(batch, cfg.vocab).copy())
+        return out
+
+    fused = logits(D.Decoder(m, batch=batch))
+    monkeypatch.setenv("LMX_FUSED_ROWS", "0")
+    rows = logits(D.Decoder(m, batch=batch))
+    refs = [oracle.OracleDecoder(m) for _ in range(batch)]
+    for pos in range(toks.shape[1]):
+        assert np.array_equal(fused[pos].view(np.uint32), rows[pos].view(np.uint32)), pos
+        for b in range(batch):
+            assert rel_max_err(fused[pos][b], refs[b].step(toks[b, pos], pos)) < DECODE_TOL, (b, pos)
+
+
 def test_batched_decoder_qwen_style(cuda):
     cfg = D.small_config(hidden=512, n_heads=12, n_kv_heads=2, head_dim=128, ffn=768, vocab=1500, max_seq=128,
                          rope_mode=D.ROPE_REFERENCE, rope_factor=1.0, rope_theta=1e6, rms_eps=1e-6,
