@@ -304,7 +304,7 @@ def test_batched_gemv(cuda, fmt, batch, rows, cols):
 
 
 @pytest.mark.parametrize("fmt", [1, 3, 5, 6])
-@pytest.mark.parametrize("batch", [7, 16])
+@pytest.mark.parametrize("batch", [7, 8, 16])
 @pytest.mark.parametrize("rows,cols", [(4160, 4096), (2112, 4096)])
 def test_batched_gemv_row_groups(cuda, fmt, batch, rows, cols):
     # 256 rows per workgroup (4160 x 4096) and 128 (2112 x 4096), each with a
