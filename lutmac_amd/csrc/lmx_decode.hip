@@ -261,24 +261,21 @@ std::vector<float> rope_freqs(const lmx_decoder_config &c) {
 // rows of the first MB chunks; later groups of MB follow.  Rescales the
 // running (M, L, o) to the pass's new maximum and adds the pass's chunks
 // weighted by e^(m_c - M) (each weight read from its lane).
-template <int HD, int MB>
-__device__ __forceinline__ void merge_pass(const float *ph, int c0, int nb, int lane, float &M, float &L,
+template <int HD, int MB, class Load>
+__device__ __forceinline__ void merge_pass(Load ld, int c0, int nb, int lane, float &M, float &L,
                                            float (&o)[HD / kWave]) {
   constexpr int VD = HD / kWave;
   const int c = c0 + lane;
   float mc = -INFINITY, lc = 0.0f;
   if (lane < nb) {
-    mc = __hip_atomic_load(ph + size_t(c) * (HD + 4), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    lc = __hip_atomic_load(ph + size_t(c) * (HD + 4) + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    mc = ld(size_t(c) * (HD + 4));
+    lc = ld(size_t(c) * (HD + 4) + 1);
   }
   float v[MB][VD];
 #pragma unroll
   for (int jj = 0; jj < MB; ++jj)
 #pragma unroll
-    for (int u = 0; u < VD; ++u)
-      v[jj][u] = jj < nb ? __hip_atomic_load(ph + size_t(c0 + jj) * (HD + 4) + 4 + u * kWave + lane,
-                                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                         : 0.0f;
+    for (int u = 0; u < VD; ++u) v[jj][u] = jj < nb ? ld(size_t(c0 + jj) * (HD + 4) + 4 + u * kWave + lane) : 0.0f;
   const float Mn = fmaxf(M, lane_max<32>(mc, lane));   // finite: chunk 0 holds position 0
   const float rs = expf(M - Mn);                        // 0 on the first pass
   L *= rs;
@@ -293,9 +290,7 @@ __device__ __forceinline__ void merge_pass(const float *ph, int c0, int nb, int 
       for (int jj = 0; jj < MB; ++jj)
 #pragma unroll
         for (int u = 0; u < VD; ++u)
-          v[jj][u] = j0 + jj < nb ? __hip_atomic_load(ph + size_t(c0 + j0 + jj) * (HD + 4) + 4 + u * kWave + lane,
-                                                      __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                                  : 0.0f;
+          v[jj][u] = j0 + jj < nb ? ld(size_t(c0 + j0 + jj) * (HD + 4) + 4 + u * kWave + lane) : 0.0f;
     }
 #pragma unroll
     for (int jj = 0; jj < MB; ++jj) {
@@ -303,6 +298,56 @@ __device__ __forceinline__ void merge_pass(const float *ph, int c0, int nb, int 
 #pragma unroll
       for (int u = 0; u < VD; ++u) o[u] += w * v[jj][u];
     }
+  }
+}
+
+// One query head's attention over one 64-position chunk whose K and V rows
+// are in LDS (ks padded rows, vs), with the head's rotated q in LDS (qrow),
+// the new key (knew, LDS) and value (vn, this lane's columns) for the chunk
+// that holds the position (own): scores, a partial softmax and the weighted
+// V sum (model.cpp:326-372, attention.cpp:23-42), returned as (m, l, o).
+// pwrow is the wave's 64-float LDS scratch.  Every lane of the wave calls it.
+template <int HD>
+__device__ __forceinline__ void chunk_attend(const float (*ks)[HD + 4], const float (*vs)[HD], const float *qrow,
+                                             const float *knew, const float (&vn)[HD / kWave], float *pwrow, int t0,
+                                             int pos, bool own, float scale, int lane, float &m, float &l,
+                                             float (&o)[HD / kWave]) {
+  constexpr int VD = HD / kWave;
+  const int t = t0 + lane;
+  const bool valid = t <= pos;
+  const int n = min(kAttnChunk, pos - t0 + 1);
+  const int jnew = own ? pos - t0 : -1;
+  const int nold = own ? n - 1 : n;
+  float sc = -INFINITY;
+  if (valid) {
+    const float *kv = lane == jnew ? knew : ks[lane];
+    float acc = 0.0f;
+#pragma unroll
+    for (int d4 = 0; d4 < HD / 4; ++d4) {
+      const float4 k4 = *reinterpret_cast<const float4 *>(kv + 4 * d4);
+      const float4 q4 = *reinterpret_cast<const float4 *>(qrow + 4 * d4);
+      acc += q4.x * k4.x;
+      acc += q4.y * k4.y;
+      acc += q4.z * k4.z;
+      acc += q4.w * k4.w;
+    }
+    sc = acc * scale;
+  }
+  m = lane_max<32>(sc, lane);
+  const float e = valid ? expf(sc - m) : 0.0f;
+  l = lane_sum<32>(e, lane);
+  pwrow[lane] = lane < nold ? e : 0.0f;      // cached positions only
+  const float enew = __shfl(e, jnew < 0 ? 0 : jnew, 64);
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int u = 0; u < VD; ++u) {
+    const int d = u * kWave + lane;
+    float s8[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+    for (int j = 0; j < kAttnChunk; ++j) s8[j % 8] += pwrow[j] * vs[j][d];
+    o[u] = ((s8[0] + s8[1]) + (s8[2] + s8[3])) + ((s8[4] + s8[5]) + (s8[6] + s8[7]));
+    if (own) o[u] += enew * vn[u];
   }
 }
 
@@ -441,44 +486,7 @@ __global__ __launch_bounds__(512) void attn_kernel(const float *__restrict__ qkv
     float o[VD], m = -INFINITY, l = 0.0f;
 #pragma unroll
     for (int u = 0; u < VD; ++u) o[u] = 0.0f;
-    if (live) {
-      const int t = t0 + lane;
-      const bool valid = t <= pos;
-      const int n = min(kAttnChunk, pos - t0 + 1);
-      const int jnew = own ? pos - t0 : -1;
-      const int nold = own ? n - 1 : n;
-      float sc = -INFINITY;
-      if (valid) {
-        const float *kv = lane == jnew ? knew : ks[lane];
-        float acc = 0.0f;
-#pragma unroll
-        for (int d4 = 0; d4 < HD / 4; ++d4) {
-          const float4 k4 = *reinterpret_cast<const float4 *>(kv + 4 * d4);
-          const float4 q4 = *reinterpret_cast<const float4 *>(&qs[wave][4 * d4]);
-          acc += q4.x * k4.x;
-          acc += q4.y * k4.y;
-          acc += q4.z * k4.z;
-          acc += q4.w * k4.w;
-        }
-        sc = acc * scale;
-      }
-      m = lane_max<32>(sc, lane);
-      const float e = valid ? expf(sc - m) : 0.0f;
-      l = lane_sum<32>(e, lane);
-      pw[wave][lane] = lane < nold ? e : 0.0f;      // cached positions only
-      const float enew = __shfl(e, jnew < 0 ? 0 : jnew, 64);
-      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-#pragma unroll
-      for (int u = 0; u < VD; ++u) {
-        const int d = u * kWave + lane;
-        float s8[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-#pragma unroll
-        for (int j = 0; j < kAttnChunk; ++j) s8[j % 8] += pw[wave][j] * vs[j][d];
-        o[u] = ((s8[0] + s8[1]) + (s8[2] + s8[3])) + ((s8[4] + s8[5]) + (s8[6] + s8[7]));
-        if (own) o[u] += enew * vn[u];
-      }
-    }
+    if (live) chunk_attend<HD>(ks, vs, qs[wave], knew, vn, pw[wave], t0, pos, own, scale, lane, m, l, o);
 #pragma unroll
     for (int u = 0; u < VD; ++u)
       __hip_atomic_store(dst + 4 + u * kWave + lane, o[u], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -517,12 +525,13 @@ __global__ __launch_bounds__(512) void attn_kernel(const float *__restrict__ qkv
     float M = -INFINITY, L = 0.0f, o[VD];
 #pragma unroll
     for (int u = 0; u < VD; ++u) o[u] = 0.0f;
+    const auto ld = [ph](size_t i) { return __hip_atomic_load(ph + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
     for (int c0 = 0; c0 < nused; c0 += kWave) {
       const int nb = min(kWave, nused - c0);
       if (nb <= 8)
-        merge_pass<HD, 8>(ph, c0, nb, lane, M, L, o);
+        merge_pass<HD, 8>(ld, c0, nb, lane, M, L, o);
       else
-        merge_pass<HD, 32>(ph, c0, nb, lane, M, L, o);
+        merge_pass<HD, 32>(ld, c0, nb, lane, M, L, o);
     }
     const float inv = 1.0f / L;
 #pragma unroll

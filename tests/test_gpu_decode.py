@@ -100,8 +100,8 @@ def test_decoder_silu_pair_epilogue(cuda, monkeypatch, ffn):
 @pytest.mark.parametrize("head_dim,n_heads,n_kv", [(64, 8, 2), (128, 12, 2)])
 def test_decoder_multi_chunk_context(cuda, head_dim, n_heads, n_kv):
     # 150 positions span three 64-position attention chunks (a fourth, empty,
-    # chunk still takes its ticket): the chunk merge of the attention kernel
-    # at every step, against the oracle's single-pass softmax.
+    # chunk takes no ticket): the chunk merge of the attention kernel at every
+    # step, against the oracle's single-pass softmax.
     cfg = D.small_config(hidden=512 if head_dim == 128 else 256, n_heads=n_heads, n_kv_heads=n_kv,
                          head_dim=head_dim, ffn=768, vocab=1200, max_seq=256, rope_mode=D.ROPE_REFERENCE,
                          rope_factor=1.0, rope_theta=1e6, qkv_bias=head_dim == 128)
