@@ -20,6 +20,19 @@ __device__ __forceinline__ float lds_load(uint32_t byte_addr) {
   return *(const lds_f32 *)(size_t)byte_addr;
 }
 
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) f32x2 lds_f32x2;
+typedef __attribute__((address_space(3))) f32x4 lds_f32x4;
+
+// 8 / 16 bytes at an 8 / 16-byte aligned LDS byte address.
+__device__ __forceinline__ f32x2 lds_load2(uint32_t byte_addr) {
+  return *(const lds_f32x2 *)(size_t)byte_addr;
+}
+__device__ __forceinline__ f32x4 lds_load4(uint32_t byte_addr) {
+  return *(const lds_f32x4 *)(size_t)byte_addr;
+}
+
 __device__ __forceinline__ uint32_t lds_addr(const float *p) {
   return (uint32_t)(size_t)(const lds_f32 *)p;
 }

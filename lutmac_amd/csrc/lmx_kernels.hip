@@ -892,14 +892,13 @@ size_t gemv_argmax_slots(const GemvArgs &a) {
 // to hide their latency (the weight words of a row group are read by NB/VG
 // waves: one HBM read, the rest cache hits).  RG (1, 2 or 4) is the largest
 // that still gives the grid a workgroup per CU, so small matrices spread
-// over the chip.  The tables of a vector group sit together per group: the
-// 16-entry table of (chunk c, vector group v, group g, vector b of the
-// group) starts at batch_chunk_bytes<VG>() * (c*NB/VG + v) + g*GS + b*64,
-// GS = VG*64 + 16: one v_perm address serves a wave's VG vectors (the
-// vector only changes the ds_read immediate), every chunk base is 256-byte
-// aligned, and the 16 B pad puts 16 consecutive groups' table writes in 16
-// different 4-bank groups (conflict-free 16-byte writes).  Partials
-// [NB][splits][Npad] go through batched_reduce_kernel.
+// over the chip.  The tables of a vector group sit together per group:
+// group g of (chunk c, vector group v) starts at batch_chunk_bytes<VG>() *
+// (c*NB/VG + v) + g*GS, GS = VG*64 + 16 (every chunk base 256-byte aligned),
+// and holds entry m of its vector b at m*4*VG + 4*b, so one v_perm address
+// (nibble * 4*VG) and one 8- or 16-byte LDS read serve a wave's VG vectors;
+// the 16 B pad spreads the table writes of consecutive groups over the
+// banks.  Partials [NB][splits][Npad] go through batched_reduce_kernel.
 constexpr int kBatchMinGrid = 256;   // workgroups: one per CU
 
 template <int VG>
@@ -910,19 +909,42 @@ constexpr uint32_t batch_chunk_bytes() { return 32 * batch_group_stride<VG>(); }
 template <int VG>
 __device__ __forceinline__ void word_lookups_batch(uint32_t v, int i, uint32_t cbase, float *out) {
   constexpr uint32_t GS = batch_group_stride<VG>();
-  const uint32_t hi = (v >> 2) & 0x3C3C3C3Cu, lo = (v << 2) & 0x3C3C3C3Cu;
-  uint32_t ad[8];
-#pragma unroll
-  for (int b = 0; b < 4; ++b) {
-    ad[2 * b] = __builtin_amdgcn_perm(cbase, hi, 0x0C060500u | b);
-    ad[2 * b + 1] = __builtin_amdgcn_perm(cbase, lo, 0x0C060500u | b);
-  }
-#pragma unroll
-  for (int n = 0; n < VG; ++n) {
+  if constexpr (VG == 1) {
+    const uint32_t hi = (v >> 2) & 0x3C3C3C3Cu, lo = (v << 2) & 0x3C3C3C3Cu;
     float t[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) t[j] = lds_load(ad[j] + uint32_t(8 * i + j) * GS + uint32_t(n) * 64);
-    out[n] += ((t[0] + t[1]) + (t[2] + t[3])) + ((t[4] + t[5]) + (t[6] + t[7]));
+    for (int b = 0; b < 4; ++b) {
+      t[2 * b] = lds_load(__builtin_amdgcn_perm(cbase, hi, 0x0C060500u | b) + uint32_t(8 * i + 2 * b) * GS);
+      t[2 * b + 1] = lds_load(__builtin_amdgcn_perm(cbase, lo, 0x0C060500u | b) + uint32_t(8 * i + 2 * b + 1) * GS);
+    }
+    out[0] += ((t[0] + t[1]) + (t[2] + t[3])) + ((t[4] + t[5]) + (t[6] + t[7]));
+  } else {
+    // entry m of the group's VG vectors sits at m * 4*VG: the nibble times
+    // 4*VG is the byte offset, and one 8- or 16-byte read returns the entry
+    // of every vector of the group
+    constexpr uint32_t SH = VG == 2 ? 1 : 0;   // nibble << 3 (VG 2) or << 4 (VG 4)
+    constexpr uint32_t MASK = VG == 2 ? 0x78787878u : 0xF0F0F0F0u;
+    const uint32_t hi = (v >> SH) & MASK, lo = (v << (4 - SH)) & MASK;
+    uint32_t ad[8];
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      ad[2 * b] = __builtin_amdgcn_perm(cbase, hi, 0x0C060500u | b) + uint32_t(8 * i + 2 * b) * GS;
+      ad[2 * b + 1] = __builtin_amdgcn_perm(cbase, lo, 0x0C060500u | b) + uint32_t(8 * i + 2 * b + 1) * GS;
+    }
+    float t[8][VG];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if constexpr (VG == 2) {
+        const f32x2 e = lds_load2(ad[j]);
+        t[j][0] = e.x, t[j][1] = e.y;
+      } else {
+        const f32x4 e = lds_load4(ad[j]);
+        t[j][0] = e.x, t[j][1] = e.y, t[j][2] = e.z, t[j][3] = e.w;
+      }
+    }
+#pragma unroll
+    for (int n = 0; n < VG; ++n)
+      out[n] += ((t[0][n] + t[1][n]) + (t[2][n] + t[3][n])) + ((t[4][n] + t[5][n]) + (t[6][n] + t[7][n]));
   }
 }
 
@@ -987,11 +1009,17 @@ __global__ __launch_bounds__((kWave * batch_waves<NB, VG, RG>())) void lut_gemv_
     float t[16];
     group_table(x0, x1, x2, x3, t);
     const int c = lane >> 5, g = lane & 31;
-    float4 *dst = reinterpret_cast<float4 *>(tables + (c * NVG + n / VG) * CB + g * GS + (n % VG) * 64);
-    dst[0] = make_float4(t[0], t[1], t[2], t[3]);
-    dst[1] = make_float4(t[4], t[5], t[6], t[7]);
-    dst[2] = make_float4(t[8], t[9], t[10], t[11]);
-    dst[3] = make_float4(t[12], t[13], t[14], t[15]);
+    if constexpr (VG == 1) {
+      float4 *dst = reinterpret_cast<float4 *>(tables + (c * NVG + n / VG) * CB + g * GS);
+      dst[0] = make_float4(t[0], t[1], t[2], t[3]);
+      dst[1] = make_float4(t[4], t[5], t[6], t[7]);
+      dst[2] = make_float4(t[8], t[9], t[10], t[11]);
+      dst[3] = make_float4(t[12], t[13], t[14], t[15]);
+    } else {
+      float *dst = reinterpret_cast<float *>(tables + (c * NVG + n / VG) * CB + g * GS) + n % VG;
+#pragma unroll
+      for (int m = 0; m < 16; ++m) dst[m * VG] = t[m];
+    }
     if constexpr (Fmt<FMT>::XS) {
       float xs = t[15];
       xs = lane_sum<16>(xs, lane);
