@@ -1188,7 +1188,7 @@ __global__ __launch_bounds__(kReduceThreads) void batched_reduce_norm_kernel(con
 
 template <int FMT, int NB, int RG>
 static void launch_batch_rg(const GemvArgs &a, int splits, hipStream_t st) {
-  constexpr int VG = NB >= 4 ? NB / 4 : 1;   // vectors per wave
+  constexpr int VG = NB >= 4 ? 4 : 1;   // vectors per wave
   const int row_blocks = (a.Npad + RG * kWave - 1) / (RG * kWave);
   lut_gemv_batch_kernel<FMT, NB, VG, RG>
       <<<dim3(row_blocks * splits), dim3(kWave * batch_waves<NB, VG, RG>()), 0, st>>>(a, row_blocks, splits);
@@ -1197,10 +1197,8 @@ static void launch_batch_rg(const GemvArgs &a, int splits, hipStream_t st) {
 template <int FMT, int NB>
 static int launch_batch_nb(const GemvArgs &a, hipStream_t st) {
   const int splits = a.Kp / kRotChunk;
-  // Rows per workgroup: for 4 vectors 64 (measured: the Qwen linears at
-  // batch 4 run 3 % faster than with larger workgroups); for 8 and 16, 256
-  // while that leaves a workgroup per CU, else fewer (LMX_BATCH_RG = 1, 2 or
-  // 4 forces 64, 128 or 256).
+  // Rows per workgroup: 256 while that leaves a workgroup per CU, else fewer
+  // (LMX_BATCH_RG = 1, 2 or 4 forces 64, 128 or 256).
   const auto grid = [&](int rg) { return (a.Npad + rg * kWave - 1) / (rg * kWave) * splits; };
   static const int force = [] {
     const char *e = std::getenv("LMX_BATCH_RG");
@@ -1208,7 +1206,6 @@ static int launch_batch_nb(const GemvArgs &a, hipStream_t st) {
     return v == 1 || v == 2 || v == 4 ? v : 0;
   }();
   const int rg = force              ? force
-                 : NB <= 4            ? 1
                  : grid(4) >= kBatchMinGrid ? 4
                  : grid(2) >= kBatchMinGrid ? 2
                                             : 1;
