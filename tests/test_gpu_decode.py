@@ -400,3 +400,14 @@ def test_mixed_format_model_and_lutmac_v2_round_trip(cuda, tmp_path):
     assert [ours.weight_format(0, w) for w in range(4)] == [L.FMT_TERNARY, L.FMT_BINARY, L.FMT_RRQ3, L.FMT_RRQ2]
     assert ours.weight_format(-1) == L.FMT_INT4 and ours.weight_format(-2) == L.FMT_INT4
     check_against(ours, oracle.OracleDecoder(m), toks)
+
+
+@pytest.mark.parametrize("batch", [4, 8])
+def test_batched_mixed_format_decoder(cuda, batch):
+    # the batched decoder (fused norm / SiLU epilogues, every row in a group)
+    # on ternary / binary / RRQ-3 / RRQ-2 linears, whose activations the
+    # batched kernel rotates, against one oracle decoder per sequence
+    cfg = D.small_config(rope_mode=D.ROPE_REFERENCE, rope_factor=1.0, rope_theta=10000.0, max_seq=64)
+    m = D.QuantizedModel(cfg, MIXED, seed=63)
+    toks = np.random.default_rng(64).integers(0, cfg.vocab, (batch, 12))
+    batched_check(D.Decoder(m, batch=batch), m, toks)
