@@ -15,16 +15,19 @@
 //                          embedding.cpp:36-75, attention.cpp:23-42)
 //     GEMV o               + residual: the hidden state is the bias and the
 //                          output (model.cpp:376-388)
-//     GEMV gate|up         RMSNorm(post_norm) fused (model.cpp:390-403)
-//     GEMV down            SiLU(gate)*up fused into the prologue, + residual
-//                          (model.cpp:410-426)
+//     GEMV gate|up         RMSNorm(post_norm) fused (model.cpp:390-403); for
+//                          4-bit weights the epilogue writes SiLU(gate)*up
+//                          (gate and up rows paired in each workgroup)
+//     GEMV down            on SiLU(gate)*up (else formed in its prologue from
+//                          the gate|up output), + residual (model.cpp:410-426)
 //   GEMV head              RMSNorm(final_norm) fused, tied table (model.cpp:433-447),
 //                          each wave's first maximum folded into a 64-bit key
 //                          by the GEMV's epilogue (model.cpp:480-490)
 //   finish_embed_kernel    maximum of the keys -> next token, position + 1,
 //                          and the next token's embedding into the hidden state
 // (Batches of sequences start each step with embed_kernel and finish with
-// argmax_rows_kernel, see step_batched.)
+// argmax_rows_kernel; their linears run the batched GEMV, whose reductions
+// also write the normed rows and SiLU(gate)*up, see step_batched.)
 // The position and the token sequence live in device memory, so the same
 // captured step replays for every position.
 #include <hip/hip_runtime.h>

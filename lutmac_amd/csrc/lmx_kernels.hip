@@ -17,7 +17,12 @@
 //     consecutive dwords: no bank conflicts;
 //   * deterministic reductions (fixed slice order, no float atomics).
 // Full-K: a workgroup owns 64/H rows and the whole K (tables of the whole K
-// in LDS), k-slices spread over its lanes, slice partials summed in LDS.
+// in LDS), k-slices spread over its lanes, slice partials summed in LDS (a
+// lane butterfly inside each wave, then the waves in order).
+// Batched (lut_gemv_batch_kernel): NB = 4/8/16 vectors, 4 per wave, each
+// table entry of a wave's 4 vectors side by side so that one 16-byte LDS
+// read serves all 4; split-K partials summed by batched_reduce_kernel (or
+// its SiLU-pair / RMSNorm-out variants).
 // Split-K: a workgroup owns 64*WAVES rows x one k-slice and writes one
 // partial per row; a second kernel (or the last workgroup) sums them.
 //
