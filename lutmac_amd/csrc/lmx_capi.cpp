@@ -256,8 +256,9 @@ int stage_if_needed(const lmx_weight *w, GemvArgs &a, void *stream) {
 }  // namespace
 
 // Batched vectors in groups of 16/8/4 through the batched kernel (weights
-// read once per group; below 4 vectors one GEMV per vector is faster);
-// returns the number of vectors done.  Needs x
+// read once per group; below 4 vectors one GEMV per vector is faster), a
+// group of 4 through the four-vector full-K kernel where the handle's plan
+// has one; returns the number of vectors done.  Needs x
 // 16-byte aligned with cols % 4 == 0 (every vector then is).  Uses the
 // handle's batched partials, allocated with the handle.
 int gemv_batched(const lmx_weight *w, GemvArgs a, const float *x, float *y, size_t batch, void *stream,
@@ -282,6 +283,16 @@ int gemv_batched(const lmx_weight *w, GemvArgs a, const float *x, float *y, size
     a.resid = resid ? resid + *done * w->rows : nullptr;
     a.cols = int(w->cols);
     a.partials = w->d_bpartials;
+    if (nb == 4 && a.epi != kEpiNormOut) {   // one full-K launch where the plan allows
+      const int q = launch_gemv_quad(w->format, a, stream);
+      if (q != 1) {
+        if (q) return q;
+        *done += 4;
+        continue;
+      }
+    }
+    if (a.xmode != kXModeNone)
+      return fail(LMX_ERR_INVALID_ARGUMENT, "the batched kernel applies no activation transform");
     int st = launch_gemv_batch(w->format, a, nb, stream);
     if (st) return st;
     *done += size_t(nb);

@@ -1191,6 +1191,270 @@ __global__ __launch_bounds__(kReduceThreads) void batched_reduce_norm_kernel(con
   for (int k = threadIdx.x; k < rows; k += kReduceThreads) y2[size_t(n) * rows + k] = row[k] * inv * w[k];
 }
 
+// Four vectors through the full-K geometry of the lean kernel (CPS 1): a
+// workgroup owns RW = 64/H rows (PAIR: RW/2 gate rows and the matching up
+// rows) and the whole K, lane l serving row l % RW and 128-chunk
+// wave*H + l/RW.  The tables of the 4 vectors sit side by side (entry m of
+// group g of chunk ch at ch*batch_chunk_bytes<4>() + g*272 + m*16, vector n
+// at +4n, as in the batched kernel), so one v_perm address and one 16-byte
+// LDS read serve the 4 lookups of a weight nibble.  The activation
+// transform (RMSNorm per vector) is fused into the table build and the
+// k-slice sums end in the workgroup, so a group of 4 vectors costs one
+// launch and no partials; the lean kernel's rules apply (each wave builds
+// the tables its own lanes read).
+constexpr uint32_t kQuadChunkBytes = batch_chunk_bytes<4>();
+
+template <int WAVES, int H>
+constexpr uint32_t quad_prefix_bytes() {
+  // xsum [WAVES*H][4], red [WAVES][64/H][4], per-wave norm sums [WAVES][4]
+  return (uint32_t(WAVES * H * 4 + WAVES * (kWave / H) * 4 + WAVES * 4) * 4 + 255) / 256 * 256;
+}
+
+template <int FMT, bool ROT, int WAVES, int H, int XM, int EPI>
+__global__ __launch_bounds__(WAVES * kWave) void lut_gemv_quad_kernel(GemvArgs a) {
+  constexpr int P = Fmt<FMT>::P, NA = Fmt<FMT>::NA, S = Fmt<FMT>::S;
+  constexpr int RW = kWave / H;
+  constexpr int NS = WAVES * H;
+  constexpr int XJ = H / 2;
+  constexpr bool PAIR = EPI == kEpiSiluPair;
+  constexpr int HR = RW / 2;
+  static_assert(H % 2 == 0, "whole 256-chunks per wave");
+  constexpr uint32_t PREFIX = quad_prefix_bytes<WAVES, H>();
+  extern __shared__ __attribute__((aligned(256))) float lds[];
+  float *xsum = lds;                      // [NS][4]
+  float *red = lds + NS * 4;              // [WAVES][RW][4]
+  float *nrm = red + WAVES * RW * 4;      // [WAVES][4]
+  char *tables = reinterpret_cast<char *>(lds) + PREFIX;
+  const int Kc = a.Kp / kChunk;
+  const int C2n = a.Kp / kRotChunk;
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  const int s = wave * H + lane / RW;     // this lane's 128-chunk
+  const int rl = lane % RW;
+  const int row = PAIR ? (rl < HR ? 0 : a.rows / 2 - HR) + blockIdx.x * HR + rl : blockIdx.x * RW + rl;
+  const int lr = min(row, a.Npad - 1);
+  const int c2base = wave * XJ;
+
+  // ---- x of the wave's 256-chunks for the 4 vectors, then the weights ----
+  float4 xr[XJ][4], xa[XJ];
+#pragma unroll
+  for (int j = 0; j < XJ; ++j) {
+    const int k0 = min(c2base + j, C2n - 1) * kRotChunk;
+#pragma unroll
+    for (int n = 0; n < 4; ++n) xr[j][n] = load_x4_raw(a.x + size_t(n) * a.cols, k0, a.cols, lane);
+    if constexpr (XM == kXModeRmsNorm) xa[j] = load_x4_raw(a.xw, k0, a.cols, lane);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_barrier();   // every wave's x requests ahead of the weight stream
+  u32x4 w[P];
+  float sc[S];
+  {
+    const u32x4 *__restrict__ pl = reinterpret_cast<const u32x4 *>(a.planes);
+    const uint32_t Npad = uint32_t(a.Npad);
+    const uint32_t ch = uint32_t(min(s, Kc - 1));
+#pragma unroll
+    for (int p = 0; p < P; ++p) w[p] = __builtin_nontemporal_load(pl + ((ch * P + p) * Npad + uint32_t(lr)));
+    const int g = a.gshift >= 0 ? int(ch) >> a.gshift : int(ch) / a.group_chunks;
+#pragma unroll
+    for (int t = 0; t < S; ++t) sc[t] = a.scales[(uint32_t(t * a.n_groups + g)) * Npad + uint32_t(lr)];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // RMSNorm of each vector: the waves' 256-chunks partition x (norm.cpp:18-34)
+  float inv_rms[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+  if constexpr (XM == kXModeRmsNorm) {
+#pragma unroll
+    for (int n = 0; n < 4; ++n) {
+      float ss = 0.0f;
+#pragma unroll
+      for (int j = 0; j < XJ; ++j) {
+        float x0, x1, x2, x3;
+        mask_x4(xr[j][n], (c2base + j) * kRotChunk, a.cols, lane, x0, x1, x2, x3);
+        if (c2base + j < C2n) ss += (x0 * x0 + x1 * x1) + (x2 * x2 + x3 * x3);
+      }
+      ss = lane_sum<32>(ss, lane);
+      if (lane == 0) nrm[wave * 4 + n] = ss;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int n = 0; n < 4; ++n) {
+      float t = 0.0f;
+#pragma unroll
+      for (int i = 0; i < WAVES; ++i) t += nrm[i * 4 + n];
+      inv_rms[n] = 1.0f / sqrtf(t / float(a.cols) + a.eps);
+    }
+  }
+
+  // ---- tables of the wave's chunks, the 4 vectors side by side ----
+#pragma unroll
+  for (int j = 0; j < XJ; ++j) {
+    const int c2 = c2base + j;
+    if (c2 >= C2n) break;   // wave-uniform
+    const int ch = c2 * 2 + (lane >> 5), g = lane & 31;
+    float *dst = reinterpret_cast<float *>(tables + uint32_t(ch) * kQuadChunkBytes + uint32_t(g) * batch_group_stride<4>());
+#pragma unroll
+    for (int n = 0; n < 4; ++n) {
+      float x0, x1, x2, x3;
+      mask_x4(xr[j][n], c2 * kRotChunk, a.cols, lane, x0, x1, x2, x3);
+      if constexpr (XM == kXModeRmsNorm) {
+        const float aux[4] = {xa[j].x, xa[j].y, xa[j].z, xa[j].w};
+        xform4(XM, inv_rms[n], aux, x0, x1, x2, x3);
+      }
+      if constexpr (ROT) fwht256_regs(x0, x1, x2, x3, lane);
+      float t[16];
+      group_table(x0, x1, x2, x3, t);
+#pragma unroll
+      for (int m = 0; m < 16; ++m) dst[m * 4 + n] = t[m];
+      if constexpr (Fmt<FMT>::XS) {
+        float xs = t[15];
+        xs = lane_sum<16>(xs, lane);
+        if ((lane & 31) == 0) xsum[ch * 4 + n] = xs;
+      }
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+
+  // ---- lookups over this lane's chunk for the 4 vectors ----
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  {
+    const int ch = min(s, Kc - 1);
+    const uint32_t cbase = lds_addr(lds) + PREFIX + uint32_t(ch) * kQuadChunkBytes;   // 256-byte aligned
+    float A[NA][4];
+#pragma unroll
+    for (int q = 0; q < NA; ++q)
+#pragma unroll
+      for (int n = 0; n < 4; ++n) A[q][n] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      uint32_t wi[P], v[NA];
+#pragma unroll
+      for (int p = 0; p < P; ++p) wi[p] = w[p][i];
+      lookup_words<FMT>(wi, v);
+#pragma unroll
+      for (int q = 0; q < NA; ++q) {
+        word_lookups_batch<4>(v[q], i, cbase, A[q]);
+        // the sums of one word complete before the next word's reads: left
+        // free, the compiler sinks every add to the chunk's end (the chunk
+        // is this lane's only one) and holds all 64 read results, spilling
+#pragma unroll
+        for (int n = 0; n < 4; ++n) asm volatile("" : "+v"(A[q][n]));
+      }
+    }
+#pragma unroll
+    for (int n = 0; n < 4; ++n) {
+      float An[NA];
+#pragma unroll
+      for (int q = 0; q < NA; ++q) An[q] = A[q][n];
+      float xs = 0.0f;
+      if constexpr (Fmt<FMT>::XS) xs = xsum[ch * 4 + n];
+      const float nacc = finish_chunk<FMT>(An, xs, sc, 0.0f);
+      acc[n] = s < Kc ? nacc : 0.0f;
+    }
+  }
+
+  // ---- the wave's H slices by a lane butterfly, then the waves in order ----
+#pragma unroll
+  for (int n = 0; n < 4; ++n) {
+    const float wsum = strided_sum<RW>(acc[n], lane);
+    if (lane < RW) red[(wave * RW + rl) * 4 + n] = wsum;
+  }
+  __syncthreads();
+  if constexpr (PAIR) {
+    if (threadIdx.x < HR * 4) {
+      const int t = threadIdx.x % HR, n = threadIdx.x / HR;
+      const int j = blockIdx.x * HR + t, h = a.rows / 2;
+      float g = 0.0f, u = 0.0f;
+#pragma unroll
+      for (int k = 0; k < WAVES; ++k) {
+        g += red[(k * RW + t) * 4 + n];
+        u += red[(k * RW + HR + t) * 4 + n];
+      }
+      if (a.bias) g += a.bias[j], u += a.bias[h + j];
+      a.y[size_t(n) * h + j] = silu(g) * u;
+    }
+  } else if (threadIdx.x < RW * 4) {
+    const int t = threadIdx.x % RW, n = threadIdx.x / RW;
+    const int r = blockIdx.x * RW + t;
+    float v = 0.0f;
+#pragma unroll
+    for (int k = 0; k < WAVES; ++k) v += red[(k * RW + t) * 4 + n];
+    if (r < a.rows) {
+      if (a.bias) v += a.bias[r];
+      if (a.resid) v += a.resid[size_t(n) * a.rows + r];
+      a.y[size_t(n) * a.rows + r] = v;
+    }
+  }
+}
+
+template <int FMT, bool ROT, int WAVES, int H, int XM, int EPI>
+static int launch_quad_kernel(const GemvArgs &a, hipStream_t st) {
+  const size_t lds = quad_prefix_bytes<WAVES, H>() + size_t(a.Kp / kChunk) * kQuadChunkBytes;
+  if (lds > kMaxLdsBytes || a.Kp / kChunk > WAVES * H) return 1;
+  static const hipError_t attr =
+      hipFuncSetAttribute(reinterpret_cast<const void *>(&lut_gemv_quad_kernel<FMT, ROT, WAVES, H, XM, EPI>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, int(kMaxLdsBytes));
+  if (attr != hipSuccess) return fail(LMX_ERR_LAUNCH_FAILED, "hipFuncSetAttribute: %s", hipGetErrorString(attr));
+  constexpr int RW = kWave / H;
+  const int blocks = EPI == kEpiSiluPair ? a.rows / RW : (a.Npad + RW - 1) / RW;
+  lut_gemv_quad_kernel<FMT, ROT, WAVES, H, XM, EPI><<<dim3(blocks), dim3(WAVES * kWave), lds, st>>>(a);
+  return LMX_OK;
+}
+
+template <int FMT, int WAVES, int H>
+static int launch_quad_cfg(const GemvArgs &a, hipStream_t st) {
+  if (a.epi == kEpiSiluPair && a.rows % (kWave / H)) return 1;
+  if (a.epi != kEpiStore && a.epi != kEpiSiluPair) return 1;
+  if (a.xmode != kXModeNone && a.xmode != kXModeRmsNorm) return 1;
+  const bool rot = a.rotate == LMX_ROTATE_FWHT256;
+  if (a.rotate != LMX_ROTATE_NONE && !rot) return 1;
+#define LMX_QUAD(R, XMV, EPV) return launch_quad_kernel<FMT, R, WAVES, H, XMV, EPV>(a, st)
+  if (a.xmode == kXModeRmsNorm) {
+    if (rot) {
+      if (a.epi == kEpiSiluPair) LMX_QUAD(true, kXModeRmsNorm, kEpiSiluPair);
+      LMX_QUAD(true, kXModeRmsNorm, kEpiStore);
+    }
+    if (a.epi == kEpiSiluPair) LMX_QUAD(false, kXModeRmsNorm, kEpiSiluPair);
+    LMX_QUAD(false, kXModeRmsNorm, kEpiStore);
+  }
+  if (rot) {
+    if (a.epi == kEpiSiluPair) LMX_QUAD(true, kXModeNone, kEpiSiluPair);
+    LMX_QUAD(true, kXModeNone, kEpiStore);
+  }
+  if (a.epi == kEpiSiluPair) LMX_QUAD(false, kXModeNone, kEpiSiluPair);
+  LMX_QUAD(false, kXModeNone, kEpiStore);
+#undef LMX_QUAD
+}
+
+// 1 when the handle's plan has no quad form (split-K, or tables of 4
+// vectors over its K do not fit).
+template <int FMT>
+static int launch_quad_fmt(const GemvArgs &a, hipStream_t st) {
+  int r = 1;
+  switch (a.fullk) {
+  case kFullK_8x2x1: r = launch_quad_cfg<FMT, 8, 2>(a, st); break;
+  case kFullK_4x4x1: r = launch_quad_cfg<FMT, 4, 4>(a, st); break;
+  default: return 1;
+  }
+  if (r) return r;
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? LMX_OK : fail(LMX_ERR_LAUNCH_FAILED, "quad lut_gemv launch: %s", hipGetErrorString(e));
+}
+
+int launch_gemv_quad(int fmt, const GemvArgs &a, void *stream) {
+  if (a.amax || a.kfamily == kKernelGeneric || std::getenv("LMX_NO_QUAD")) return 1;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (fmt) {
+  case LMX_FMT_TERNARY: return launch_quad_fmt<LMX_FMT_TERNARY>(a, st);
+  case LMX_FMT_BINARY: return launch_quad_fmt<LMX_FMT_BINARY>(a, st);
+  case LMX_FMT_RRQ2: return launch_quad_fmt<LMX_FMT_RRQ2>(a, st);
+  case LMX_FMT_RRQ3: return launch_quad_fmt<LMX_FMT_RRQ3>(a, st);
+  case LMX_FMT_INT3: return launch_quad_fmt<LMX_FMT_INT3>(a, st);
+  case LMX_FMT_INT4: return launch_quad_fmt<LMX_FMT_INT4>(a, st);
+  case LMX_FMT_INT8: return launch_quad_fmt<LMX_FMT_INT8>(a, st);
+  }
+  return 1;
+}
+
 template <int FMT, int NB, int RG>
 static void launch_batch_rg(const GemvArgs &a, int splits, hipStream_t st) {
   constexpr int VG = NB >= 4 ? 4 : 1;   // vectors per wave

@@ -270,6 +270,38 @@ def test_batched_decoder_fused_epilogues(cuda, monkeypatch, batch):
             assert rel_max_err(fused[pos][b], refs[b].step(toks[b, pos], pos)) < DECODE_TOL, (b, pos)
 
 
+@pytest.mark.parametrize("plan", [3, 6])
+def test_batched_decoder_four_vector_kernel(cuda, monkeypatch, plan):
+    # batch 4 on K <= 2048 plans: qkv and gate|up (SiLU(gate)*up written by
+    # the workgroup) take the four-vector full-K kernel; against the batched
+    # kernel with its reductions (LMX_NO_QUAD=1) and the oracle's logits
+    monkeypatch.setenv("LMX_FULLK", str(plan))
+    cfg = D.small_config(hidden=512, n_heads=8, n_kv_heads=2, head_dim=64, ffn=1024, vocab=700, max_seq=64,
+                         rope_mode=D.ROPE_REFERENCE, rope_factor=1.0, rope_theta=1e6, qkv_bias=True)
+    m = D.SyntheticModel(cfg, seed=51 + plan, group=128, random_norms=True)
+    toks = np.random.default_rng(52).integers(0, cfg.vocab, (4, 12))
+    dec = D.Decoder(m, batch=4)
+    assert all(w.kernel_config()[0] == plan for w in dec.weights[:4])
+
+    def logits(dec):
+        dec.reset(toks)
+        lg = torch.empty(4 * cfg.vocab, dtype=torch.float32, device="cuda")
+        out = []
+        for _ in range(toks.shape[1]):
+            dec.step(lg)
+            out.append(lg.cpu().numpy().reshape(4, cfg.vocab).copy())
+        return out
+
+    quad = logits(dec)
+    monkeypatch.setenv("LMX_NO_QUAD", "1")
+    batched = logits(dec)
+    refs = [oracle.OracleDecoder(m) for _ in range(4)]
+    for pos in range(toks.shape[1]):
+        for b in range(4):
+            assert rel_max_err(quad[pos][b], batched[pos][b]) < 1e-5, (b, pos)
+            assert rel_max_err(quad[pos][b], refs[b].step(toks[b, pos], pos)) < DECODE_TOL, (b, pos)
+
+
 def test_batched_decoder_qwen_style(cuda):
     cfg = D.small_config(hidden=512, n_heads=12, n_kv_heads=2, head_dim=128, ffn=768, vocab=1500, max_seq=128,
                          rope_mode=D.ROPE_REFERENCE, rope_factor=1.0, rope_theta=1e6, rms_eps=1e-6,

@@ -318,6 +318,29 @@ def test_batched_gemv_row_groups(cuda, fmt, batch, rows, cols):
         assert rel_max_err(y[b], ref) < TOL, f"vector {b}"
 
 
+@pytest.mark.parametrize("fmt", [1, 2, 3, 4, 5, 6, 7])
+@pytest.mark.parametrize("cfg", [3, 6])
+@pytest.mark.parametrize("rows,cols", [(70, 2048), (33, 640)])
+@pytest.mark.parametrize("flags", [0, 1])
+def test_four_vector_full_k(cuda, monkeypatch, fmt, cfg, rows, cols, flags):
+    # 4 vectors on a full-K plan of K <= 2048 (8x2x1, 4x4x1) take the kernel
+    # that holds the 4 vectors' tables side by side and sums in the
+    # workgroup: the oracle for each vector, and the batched kernel's values
+    # (LMX_NO_QUAD=1) to the same bar; 640 leaves the upper slices idle
+    monkeypatch.setenv("LMX_FULLK", str(cfg))
+    planes, scales, g = synth.make_weights(fmt, rows, cols, seed=cfg * 31 + fmt, group=128)
+    xs = np.stack([synth.make_activations(cols, seed=3000 + s, outliers=True) for s in range(4)])
+    w = L.Weight.from_planes(fmt, planes, scales, rows, cols, g)
+    assert w.kernel_config()[0] == cfg
+    y = w.gemv(dev(xs.ravel()), flags=flags).cpu().numpy().reshape(4, rows)
+    monkeypatch.setenv("LMX_NO_QUAD", "1")
+    yb = w.gemv(dev(xs.ravel()), flags=flags).cpu().numpy().reshape(4, rows)
+    for b in range(4):
+        ref = oracle_planes_gemv(fmt, planes, scales, rows, cols, g, xs[b], flags)
+        assert rel_max_err(y[b], ref) < TOL, f"vector {b}"
+        assert rel_max_err(y[b], yb[b]) < TOL, f"vector {b}"
+
+
 def test_batched_linear_bias_and_repeat(cuda):
     rows, cols, batch = 2048, 2048, 16
     planes, scales, g = synth.make_weights(L.FMT_INT4, rows, cols, seed=5)
