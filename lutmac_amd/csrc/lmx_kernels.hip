@@ -1144,30 +1144,34 @@ __global__ __launch_bounds__(kReduceThreads) void batched_reduce_pair_kernel(con
 
 // kEpiNormOut: one workgroup per vector n: y[n] = split-order sums (+ bias)
 // (+ resid[n], which may be y itself), kept in LDS, then y2[n] = RMSNorm of
-// y[n] with weight w computed exactly as rmsnorm_rows_kernel does (the same
-// thread-to-element assignment, sum order and expression, norm.cpp:18-34), so
-// the fused and the separate forms give the same bits.
-__global__ __launch_bounds__(kReduceThreads) void batched_reduce_norm_kernel(const float *__restrict__ partials,
-                                                                             int splits, int Npad, int rows,
-                                                                             const float *__restrict__ bias,
-                                                                             const float *resid, float *y,
-                                                                             const float *__restrict__ w, float eps,
-                                                                             float *__restrict__ y2) {
-  static_assert(kReduceThreads == 256, "the RMSNorm order is rmsnorm_rows_kernel's (256 threads)");
+// y[n] with weight w computed exactly as rmsnorm_rows_kernel does (its 256
+// threads' element assignment, sum order and expression, norm.cpp:18-34), so
+// the fused and the separate forms give the same bits.  The row sums take
+// kNormReduceThreads threads, 4 rows each, with up to kNormReduceLoads split
+// loads in flight per thread (a whole 2048-row vector and 48 splits, K up to
+// 12288, in one round trip).
+constexpr int kNormReduceThreads = 512;
+constexpr int kNormReduceLoads = 48;
+__global__ __launch_bounds__(kNormReduceThreads) void batched_reduce_norm_kernel(
+    const float *__restrict__ partials, int splits, int Npad, int rows, const float *__restrict__ bias,
+    const float *resid, float *y, const float *__restrict__ w, float eps, float *__restrict__ y2) {
+  constexpr int NT = 256;   // rmsnorm_rows_kernel's threads
+  static_assert(kNormReduceThreads % NT == 0, "the norm runs on the first 256 threads");
   extern __shared__ float row[];   // [rows]
-  __shared__ float red[4];
+  __shared__ float red[NT / kWave];
   const int n = blockIdx.x;
   const float *pn = partials + size_t(n) * splits * Npad;
   const size_t step = size_t(Npad) / 4;
-  for (int r0 = 4 * int(threadIdx.x); r0 < rows; r0 += 4 * kReduceThreads) {
+  for (int r0 = 4 * int(threadIdx.x); r0 < rows; r0 += 4 * kNormReduceThreads) {
     const float4 *p = reinterpret_cast<const float4 *>(pn + r0);
     float4 s = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    for (int k0 = 0; k0 < splits; k0 += 16) {
-      float4 v[16];
+    for (int k0 = 0; k0 < splits; k0 += kNormReduceLoads) {
+      float4 v[kNormReduceLoads];
 #pragma unroll
-      for (int k = 0; k < 16; ++k) v[k] = k0 + k < splits ? p[size_t(k0 + k) * step] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      for (int k = 0; k < kNormReduceLoads; ++k)
+        v[k] = k0 + k < splits ? p[size_t(k0 + k) * step] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
-      for (int k = 0; k < 16; ++k) s.x += v[k].x, s.y += v[k].y, s.z += v[k].z, s.w += v[k].w;
+      for (int k = 0; k < kNormReduceLoads; ++k) s.x += v[k].x, s.y += v[k].y, s.z += v[k].z, s.w += v[k].w;
     }
     const float t[4] = {s.x, s.y, s.z, s.w};
 #pragma unroll
@@ -1183,12 +1187,13 @@ __global__ __launch_bounds__(kReduceThreads) void batched_reduce_norm_kernel(con
   }
   __syncthreads();
   float ss = 0.0f;
-  for (int k = threadIdx.x; k < rows; k += kReduceThreads) ss += row[k] * row[k];
+  if (threadIdx.x < NT)
+    for (int k = threadIdx.x; k < rows; k += NT) ss += row[k] * row[k];
   ss = lane_sum<32>(ss, threadIdx.x & (kWave - 1));
-  if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = ss;
+  if (threadIdx.x < NT && (threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = ss;
   __syncthreads();
   const float inv = 1.0f / sqrtf(((red[0] + red[1]) + (red[2] + red[3])) / float(rows) + eps);
-  for (int k = threadIdx.x; k < rows; k += kReduceThreads) y2[size_t(n) * rows + k] = row[k] * inv * w[k];
+  for (int k = threadIdx.x; k < rows; k += kNormReduceThreads) y2[size_t(n) * rows + k] = row[k] * inv * w[k];
 }
 
 // Four vectors through the full-K geometry of the lean kernel (CPS 1): a
@@ -1203,6 +1208,7 @@ __global__ __launch_bounds__(kReduceThreads) void batched_reduce_norm_kernel(con
 // launch and no partials; the lean kernel's rules apply (each wave builds
 // the tables its own lanes read).
 constexpr uint32_t kQuadChunkBytes = batch_chunk_bytes<4>();
+constexpr int kQuadMaxBlocks = 256;   // MI355X CUs
 
 template <int WAVES, int H>
 constexpr uint32_t quad_prefix_bytes() {
@@ -1396,6 +1402,16 @@ static int launch_quad_kernel(const GemvArgs &a, hipStream_t st) {
   if (attr != hipSuccess) return fail(LMX_ERR_LAUNCH_FAILED, "hipFuncSetAttribute: %s", hipGetErrorString(attr));
   constexpr int RW = kWave / H;
   const int blocks = EPI == kEpiSiluPair ? a.rows / RW : (a.Npad + RW - 1) / RW;
+  // At most one workgroup per CU (LMX_QUAD_MAX_BLOCKS overrides): every
+  // workgroup builds the 4 vectors' tables of the whole K, which past one
+  // round of workgroups costs more than the batched kernel's per-slice
+  // tables and reduce (Qwen gate|up 17920 x 1536, 560 workgroups: batch 4
+  // decode 2222 -> 2285 tokens/s with the limit).
+  static const int max_blocks = [] {
+    const char *e = std::getenv("LMX_QUAD_MAX_BLOCKS");
+    return e ? std::atoi(e) : kQuadMaxBlocks;
+  }();
+  if (blocks > max_blocks) return 1;
   lut_gemv_quad_kernel<FMT, ROT, WAVES, H, XM, EPI><<<dim3(blocks), dim3(WAVES * kWave), lds, st>>>(a);
   return LMX_OK;
 }
@@ -1486,7 +1502,7 @@ static int launch_batch_nb(const GemvArgs &a, hipStream_t st) {
     batched_reduce_pair_kernel<<<dim3((h + 4 * kReduceThreads - 1) / (4 * kReduceThreads), NB),
                                  dim3(kReduceThreads), 0, st>>>(a.partials, splits, a.Npad, h, a.bias, a.y);
   } else if (a.epi == kEpiNormOut) {
-    batched_reduce_norm_kernel<<<dim3(NB), dim3(kReduceThreads), size_t(a.rows) * sizeof(float), st>>>(
+    batched_reduce_norm_kernel<<<dim3(NB), dim3(kNormReduceThreads), size_t(a.rows) * sizeof(float), st>>>(
         a.partials, splits, a.Npad, a.rows, a.bias, a.resid, a.y, a.xw, a.eps, a.y2);
   } else {
     batched_reduce_kernel<<<dim3((a.rows + 4 * kReduceThreads - 1) / (4 * kReduceThreads), NB),
