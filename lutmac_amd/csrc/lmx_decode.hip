@@ -137,18 +137,38 @@ __global__ __launch_bounds__(1024) void argmax_rows_kernel(const float *__restri
                                                            int *__restrict__ tokens, int tstride,
                                                            int *__restrict__ pos_p, int n_forced, int max_pos,
                                                            unsigned *__restrict__ ticket_p) {
+  constexpr int NT = 1024, IN = 16;   // threads, loads in flight per thread
   __shared__ unsigned long long best[16];
   __shared__ unsigned ticket;
   const float *lg = logits + size_t(blockIdx.x) * vocab;
   unsigned long long key = 0;
-  for (int i = threadIdx.x; i < vocab; i += 1024) {
-    const float v = lg[i];
-    if (__builtin_isnan(v)) continue;
+  // key = orderable value bits << 32 | ~index: the largest value, the lowest
+  // index among equal values; NaN never wins, -0 counts as +0
+  const auto fold = [&key](float v, int i) {
+    if (__builtin_isnan(v)) return;
     uint32_t u = __float_as_uint(v + 0.0f);
     u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
     const unsigned long long k = (static_cast<unsigned long long>(u) << 32) | (0xFFFFFFFFu - uint32_t(i));
     key = k > key ? k : key;
+  };
+  // 16-byte loads, IN per thread in flight (every row is 16-byte aligned when
+  // the logits are and vocab % 4 == 0), then the scalar tail
+  const int n4 = vocab % 4 == 0 && reinterpret_cast<size_t>(logits) % 16 == 0 ? vocab / 4 : 0;
+  const float4 *lg4 = reinterpret_cast<const float4 *>(lg);
+  for (int i0 = threadIdx.x; i0 < n4; i0 += NT * IN) {
+    float4 v[IN];
+#pragma unroll
+    for (int j = 0; j < IN; ++j) {
+      const int i = i0 + j * NT;
+      v[j] = lg4[min(i, n4 - 1)];
+    }
+#pragma unroll
+    for (int j = 0; j < IN; ++j) {
+      const int i = i0 + j * NT;
+      if (i < n4) fold(v[j].x, 4 * i), fold(v[j].y, 4 * i + 1), fold(v[j].z, 4 * i + 2), fold(v[j].w, 4 * i + 3);
+    }
   }
+  for (int i = 4 * n4 + threadIdx.x; i < vocab; i += NT) fold(lg[i], i);
   key = wave_max_key(key, threadIdx.x & (kWave - 1));
   if ((threadIdx.x & (kWave - 1)) == 0) best[threadIdx.x / kWave] = key;
   __syncthreads();

@@ -332,6 +332,26 @@ def test_batched_generate_graph_equals_eager_and_oracle(cuda):
                 assert lg[out[b, pos + 1]] >= lg.max() - DECODE_TOL * np.linalg.norm(lg)
 
 
+@pytest.mark.parametrize("vocab", [1000, 1001])
+def test_batched_greedy_token_is_first_maximum(cuda, vocab):
+    # argmax_rows_kernel: 16-byte loads when vocab % 4 == 0 (1000), the scalar
+    # loop otherwise (1001); every chosen token is numpy's first maximum of the
+    # step's own logits row
+    cfg = D.small_config(vocab=vocab, max_seq=32)
+    m = D.SyntheticModel(cfg, seed=61, group=128, random_norms=True)
+    B, n = 4, 12
+    dec = D.Decoder(m, batch=B)
+    dec.reset(np.random.default_rng(62).integers(0, vocab, (B, 1)))
+    lg = torch.empty(B * vocab, dtype=torch.float32, device="cuda")
+    rows = []
+    for _ in range(n):
+        dec.step(lg)
+        rows.append(lg.cpu().numpy().reshape(B, vocab).copy())
+    toks = dec.tokens(n + 1)
+    for pos in range(n):
+        assert np.array_equal(toks[:, pos + 1], rows[pos].argmax(axis=1)), pos
+
+
 # ---- BASELINE config 5 code paths: long KV context, batch 16, full Qwen ------
 def check_positions(dec, ref, tokens, check_from, tol=DECODE_TOL):
     """Teacher-forced run over all of `tokens`; logits compared from position
