@@ -798,6 +798,35 @@ int rmsnorm_rows(const lmx_decoder *d, const float *x, const float *wt, float *y
 
 int step_batched_rows(lmx_decoder *d, hipStream_t st);
 
+// Four rows of one linear in one group (the four-vector kernel where the
+// plan has it, else the batched kernel): y = W x' (+ bias) (+ resid), x' the
+// RMSNorm of x with weight xw when xmode asks.
+int gemv_group4(const lmx_decoder *d, const lmx_weight *w, const float *x, float *y, const float *bias,
+                const float *resid, int xmode, const float *xw, int epi, hipStream_t st) {
+  GemvArgs a = decode_args(w, xmode, epi);
+  a.bias = bias;
+  a.resid = resid;
+  a.xw = xw;
+  a.eps = d->cfg.rms_eps;
+  size_t done = 0;
+  const int r = gemv_batched(w, a, x, y, 4, st, &done);
+  if (r) return r;
+  return done == 4 ? LMX_OK : fail(LMX_ERR_INVALID_ARGUMENT, "a group of 4 rows covered %zu", done);
+}
+
+// Batch 4 with every layer's qkv and o on the four-vector kernel (LMX_QUAD_STEP=0:
+// never): the norms ride in the kernels' table builds and the residual in
+// their epilogues, so the o projection needs no reduction.
+bool quad_step(const lmx_decoder *d) {
+  const char *e = std::getenv("LMX_QUAD_STEP");
+  if (d->batch != 4 || (e && std::atoi(e) == 0) || !d->head->batched) return false;
+  for (const lmx_decoder::Layer &L : d->layers)
+    if (!quad_serves(decode_args(L.qkv, kXModeRmsNorm, kEpiStore)) || !quad_serves(decode_args(L.o, kXModeNone, kEpiStore)) ||
+        !L.gate_up->batched || !L.down->batched || !batched_epilogue_ok(L.gate_up, kEpiSiluPair, 4))
+      return false;
+  return true;
+}
+
 // One token step of `batch` sequences in lockstep: every linear reads its
 // weights once per group of sequences.  The batched GEMV splits K, so its
 // table build cannot apply the RMSNorm of its input; instead the reduction
@@ -810,7 +839,26 @@ int step_batched(lmx_decoder *d, float *logits_out, hipStream_t st) {
   const size_t B = d->batch;
   int r = embed(d->embed, d->tokens, d->pos, d->hidden, B, int(c.max_seq + 1), st);
   if (r) return r;
-  if (rows_fuse(d)) {
+  float *lg = logits_out ? logits_out : d->logits;
+  const bool quad = quad_step(d);
+  if (quad) {
+    // qkv: RMSNorm in the table build; o: + hidden in the epilogue; gate|up:
+    // RMSNorm in the batched table build, SiLU(gate)*up in its reduction;
+    // down: + hidden in its reduction; the head normalises its own input.
+    for (size_t l = 0; l < c.n_layers; ++l) {
+      const lmx_decoder::Layer &L = d->layers[l];
+      if ((r = gemv_group4(d, L.qkv, d->hidden, d->qkv, L.qkv_bias, nullptr, kXModeRmsNorm, L.in_norm, kEpiStore,
+                           st)) ||
+          (r = attention(d, l, st)) ||
+          (r = gemv_group4(d, L.o, d->attn_out, d->hidden, nullptr, d->hidden, kXModeNone, nullptr, kEpiStore, st)) ||
+          (r = gemv_group4(d, L.gate_up, d->hidden, d->act, nullptr, nullptr, kXModeRmsNorm, L.post_norm,
+                           kEpiSiluPair, st)) ||
+          (r = gemv_group4(d, L.down, d->act, d->hidden, nullptr, d->hidden, kXModeNone, nullptr, kEpiStore, st)))
+        return r;
+    }
+    if ((r = gemv_group4(d, d->head, d->hidden, lg, nullptr, nullptr, kXModeRmsNorm, d->final_norm, kEpiStore, st)))
+      return r;
+  } else if (rows_fuse(d)) {
     // The o and down reductions write the hidden rows and the next linear's
     // normed input; the gate|up reduction writes SiLU(gate)*up.
     if ((r = rmsnorm_rows(d, d->hidden, d->layers[0].in_norm, d->normed, st))) return r;
@@ -827,8 +875,7 @@ int step_batched(lmx_decoder *d, float *logits_out, hipStream_t st) {
     if ((r = step_batched_rows(d, st))) return r;
     if ((r = rmsnorm_rows(d, d->hidden, d->final_norm, d->normed, st))) return r;
   }
-  float *lg = logits_out ? logits_out : d->logits;
-  if ((r = gemv_rows(d, d->head, d->normed, lg, nullptr, nullptr, st))) return r;
+  if (!quad && (r = gemv_rows(d, d->head, d->normed, lg, nullptr, nullptr, st))) return r;
   argmax_rows_kernel<<<dim3(unsigned(B)), dim3(1024), 0, st>>>(lg, int(c.vocab), d->tokens, int(c.max_seq + 1),
                                                                d->pos, d->n_forced, int(c.max_seq), d->argmax_ticket);
   return launch_err("argmax_rows");

@@ -158,8 +158,10 @@ int launch_gemv_batch(int fmt, const GemvArgs &a, int nb, void *stream);
 // Exactly 4 vectors (a.x [4][cols], a.y [4][rows], a.resid [4][rows]) in one
 // full-K launch with the transform a.xmode (none or RMSNorm with a.xw) and
 // epilogue a.epi (store or SiLU pair); returns 1, launching nothing, when
-// the handle's plan has no such form (split-K plans, K above 2048).
+// the handle's plan has no such form (split-K plans, K above 2048, more than
+// one round of workgroups; quad_serves tells beforehand).
 int launch_gemv_quad(int fmt, const GemvArgs &a, void *stream);
+bool quad_serves(const GemvArgs &a);
 // Number of argmax key slots a launch with these arguments writes.
 size_t gemv_argmax_slots(const GemvArgs &a);
 int launch_fwht256(float *x, size_t n, void *stream);

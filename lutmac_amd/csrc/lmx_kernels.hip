@@ -956,7 +956,11 @@ __device__ __forceinline__ void word_lookups_batch(uint32_t v, int i, uint32_t c
 template <int NB, int VG, int RG>
 constexpr int batch_waves() { return RG * (NB / VG); }
 
-template <int FMT, int NB, int VG, int RG>
+// XM = kXModeRmsNorm (groups of 4 vectors): each wave also reads the whole
+// row of its vectors for the sum of squares (every workgroup, so the
+// k-slices need no exchange) and the tables take x * inv_rms * xw
+// (norm.cpp:18-34).
+template <int FMT, int NB, int VG, int RG, int XM = kXModeNone>
 __global__ __launch_bounds__((kWave * batch_waves<NB, VG, RG>())) void lut_gemv_batch_kernel(GemvArgs a,
                                                                                           int row_blocks,
                                                                                           int splits) {
@@ -979,12 +983,22 @@ __global__ __launch_bounds__((kWave * batch_waves<NB, VG, RG>())) void lut_gemv_
 
   // activations: wave w builds the tables of vectors w, w + NW, ...
   constexpr int XV = (NB + NW - 1) / NW;
-  float xv[XV][4];
+  constexpr bool NORM = XM == kXModeRmsNorm;
+  constexpr int RL = NORM ? 8 : 1;   // row loads in flight per lane and vector (2048 columns)
+  static_assert(XM == kXModeNone || (NORM && NB == 4), "RMSNorm for groups of 4 vectors");
+  float xv[XV][4], xw[4];
+  float4 rv[NORM ? XV : 1][RL];
 #pragma unroll
   for (int j = 0; j < XV; ++j) {
     const int n = min(wave + NW * j, NB - 1);
     load_x4(a.x + size_t(n) * a.cols, k0, a.cols, lane, xv[j][0], xv[j][1], xv[j][2], xv[j][3]);
+    if constexpr (NORM) {
+#pragma unroll
+      for (int u = 0; u < RL; ++u)
+        rv[j][u] = *reinterpret_cast<const float4 *>(a.x + size_t(n) * a.cols + min(u * kRotChunk + 4 * lane, a.cols - 4));
+    }
   }
+  if constexpr (NORM) load_x4(a.xw, k0, a.cols, lane, xw[0], xw[1], xw[2], xw[3]);
   __builtin_amdgcn_sched_barrier(0);
   u32x4 w[CH][P];
   float sc[CH][S];
@@ -1005,11 +1019,39 @@ __global__ __launch_bounds__((kWave * batch_waves<NB, VG, RG>())) void lut_gemv_
       for (int t = 0; t < S; ++t) sc[c][t] = a.scales[(size_t(t) * a.n_groups + g) * Npad + lr];
     }
   }
+  // RMSNorm: the sum of squares of each vector's whole row (the loads above
+  // cover 2048 columns, later rounds the rest)
+  float inv_rms[XV];
+#pragma unroll
+  for (int j = 0; j < XV; ++j) inv_rms[j] = 1.0f;
+  if constexpr (NORM) {
+#pragma unroll
+    for (int j = 0; j < XV; ++j) {
+      const int n = min(wave + NW * j, NB - 1);
+      float ss = 0.0f;
+      for (int r0 = 0; r0 < a.cols; r0 += RL * kRotChunk) {
+        if (r0 > 0) {
+#pragma unroll
+          for (int u = 0; u < RL; ++u)
+            rv[j][u] = *reinterpret_cast<const float4 *>(a.x + size_t(n) * a.cols +
+                                                         min(r0 + u * kRotChunk + 4 * lane, a.cols - 4));
+        }
+#pragma unroll
+        for (int u = 0; u < RL; ++u) {
+          const float4 v = rv[j][u];
+          if (r0 + u * kRotChunk + 4 * lane < a.cols) ss += (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
+        }
+      }
+      ss = lane_sum<32>(ss, lane);
+      inv_rms[j] = 1.0f / sqrtf(ss / float(a.cols) + a.eps);
+    }
+  }
 #pragma unroll
   for (int j = 0; j < XV; ++j) {
     const int n = wave + NW * j;
     if (n >= NB) break;   // wave-uniform
     float x0 = xv[j][0], x1 = xv[j][1], x2 = xv[j][2], x3 = xv[j][3];
+    if constexpr (NORM) xform4(kXModeRmsNorm, inv_rms[j], xw, x0, x1, x2, x3);
     if (a.rotate == LMX_ROTATE_FWHT256) fwht256_regs(x0, x1, x2, x3, lane);
     float t[16];
     group_table(x0, x1, x2, x3, t);
@@ -1210,10 +1252,9 @@ __global__ __launch_bounds__(kNormReduceThreads) void batched_reduce_norm_kernel
 constexpr uint32_t kQuadChunkBytes = batch_chunk_bytes<4>();
 constexpr int kQuadMaxBlocks = 256;   // MI355X CUs
 
-template <int WAVES, int H>
-constexpr uint32_t quad_prefix_bytes() {
-  // xsum [WAVES*H][4], red [WAVES][64/H][4], per-wave norm sums [WAVES][4]
-  return (uint32_t(WAVES * H * 4 + WAVES * (kWave / H) * 4 + WAVES * 4) * 4 + 255) / 256 * 256;
+constexpr uint32_t quad_prefix_bytes(int waves, int h) {
+  // xsum [waves*h][4], red [waves][64/h][4], per-wave norm sums [waves][4]
+  return (uint32_t(waves * h * 4 + waves * (kWave / h) * 4 + waves * 4) * 4 + 255) / 256 * 256;
 }
 
 template <int FMT, bool ROT, int WAVES, int H, int XM, int EPI>
@@ -1225,7 +1266,7 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_quad_kernel(GemvArgs a
   constexpr bool PAIR = EPI == kEpiSiluPair;
   constexpr int HR = RW / 2;
   static_assert(H % 2 == 0, "whole 256-chunks per wave");
-  constexpr uint32_t PREFIX = quad_prefix_bytes<WAVES, H>();
+  constexpr uint32_t PREFIX = quad_prefix_bytes(WAVES, H);
   extern __shared__ __attribute__((aligned(256))) float lds[];
   float *xsum = lds;                      // [NS][4]
   float *red = lds + NS * 4;              // [WAVES][RW][4]
@@ -1394,35 +1435,20 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_quad_kernel(GemvArgs a
 
 template <int FMT, bool ROT, int WAVES, int H, int XM, int EPI>
 static int launch_quad_kernel(const GemvArgs &a, hipStream_t st) {
-  const size_t lds = quad_prefix_bytes<WAVES, H>() + size_t(a.Kp / kChunk) * kQuadChunkBytes;
-  if (lds > kMaxLdsBytes || a.Kp / kChunk > WAVES * H) return 1;
+  const size_t lds = quad_prefix_bytes(WAVES, H) + size_t(a.Kp / kChunk) * kQuadChunkBytes;
   static const hipError_t attr =
       hipFuncSetAttribute(reinterpret_cast<const void *>(&lut_gemv_quad_kernel<FMT, ROT, WAVES, H, XM, EPI>),
                           hipFuncAttributeMaxDynamicSharedMemorySize, int(kMaxLdsBytes));
   if (attr != hipSuccess) return fail(LMX_ERR_LAUNCH_FAILED, "hipFuncSetAttribute: %s", hipGetErrorString(attr));
   constexpr int RW = kWave / H;
   const int blocks = EPI == kEpiSiluPair ? a.rows / RW : (a.Npad + RW - 1) / RW;
-  // At most one workgroup per CU (LMX_QUAD_MAX_BLOCKS overrides): every
-  // workgroup builds the 4 vectors' tables of the whole K, which past one
-  // round of workgroups costs more than the batched kernel's per-slice
-  // tables and reduce (Qwen gate|up 17920 x 1536, 560 workgroups: batch 4
-  // decode 2222 -> 2285 tokens/s with the limit).
-  static const int max_blocks = [] {
-    const char *e = std::getenv("LMX_QUAD_MAX_BLOCKS");
-    return e ? std::atoi(e) : kQuadMaxBlocks;
-  }();
-  if (blocks > max_blocks) return 1;
   lut_gemv_quad_kernel<FMT, ROT, WAVES, H, XM, EPI><<<dim3(blocks), dim3(WAVES * kWave), lds, st>>>(a);
   return LMX_OK;
 }
 
 template <int FMT, int WAVES, int H>
-static int launch_quad_cfg(const GemvArgs &a, hipStream_t st) {
-  if (a.epi == kEpiSiluPair && a.rows % (kWave / H)) return 1;
-  if (a.epi != kEpiStore && a.epi != kEpiSiluPair) return 1;
-  if (a.xmode != kXModeNone && a.xmode != kXModeRmsNorm) return 1;
+static int launch_quad_cfg(const GemvArgs &a, hipStream_t st) {   // quad_serves(a) holds
   const bool rot = a.rotate == LMX_ROTATE_FWHT256;
-  if (a.rotate != LMX_ROTATE_NONE && !rot) return 1;
 #define LMX_QUAD(R, XMV, EPV) return launch_quad_kernel<FMT, R, WAVES, H, XMV, EPV>(a, st)
   if (a.xmode == kXModeRmsNorm) {
     if (rot) {
@@ -1456,8 +1482,30 @@ static int launch_quad_fmt(const GemvArgs &a, hipStream_t st) {
   return e == hipSuccess ? LMX_OK : fail(LMX_ERR_LAUNCH_FAILED, "quad lut_gemv launch: %s", hipGetErrorString(e));
 }
 
+bool quad_serves(const GemvArgs &a) {
+  if (a.amax || a.kfamily == kKernelGeneric || std::getenv("LMX_NO_QUAD")) return false;
+  if (a.fullk != kFullK_8x2x1 && a.fullk != kFullK_4x4x1) return false;
+  const FullKShape f = fullk_shape(a.fullk);
+  const int rw = kWave / f.h;
+  if (a.epi != kEpiStore && a.epi != kEpiSiluPair) return false;
+  if (a.epi == kEpiSiluPair && a.rows % rw) return false;
+  if (a.xmode != kXModeNone && a.xmode != kXModeRmsNorm) return false;
+  if (a.rotate != LMX_ROTATE_NONE && a.rotate != LMX_ROTATE_FWHT256) return false;
+  const size_t lds = quad_prefix_bytes(f.waves, f.h) + size_t(a.Kp / kChunk) * kQuadChunkBytes;
+  if (lds > kMaxLdsBytes || a.Kp / kChunk > f.waves * f.h) return false;
+  // At most one workgroup per CU (LMX_QUAD_MAX_BLOCKS overrides): every
+  // workgroup builds the 4 vectors' tables of the whole K, which past one
+  // round of workgroups costs more than the batched kernel's per-slice
+  // tables and reduce (Qwen gate|up 17920 x 1536, 560 workgroups: batch 4
+  // decode 2222 -> 2285 tokens/s with the limit).
+  const char *e = std::getenv("LMX_QUAD_MAX_BLOCKS");
+  const int max_blocks = e ? std::atoi(e) : kQuadMaxBlocks;
+  const int blocks = a.epi == kEpiSiluPair ? a.rows / rw : (a.Npad + rw - 1) / rw;
+  return blocks <= max_blocks;
+}
+
 int launch_gemv_quad(int fmt, const GemvArgs &a, void *stream) {
-  if (a.amax || a.kfamily == kKernelGeneric || std::getenv("LMX_NO_QUAD")) return 1;
+  if (!quad_serves(a)) return 1;
   hipStream_t st = static_cast<hipStream_t>(stream);
   switch (fmt) {
   case LMX_FMT_TERNARY: return launch_quad_fmt<LMX_FMT_TERNARY>(a, st);
@@ -1475,8 +1523,14 @@ template <int FMT, int NB, int RG>
 static void launch_batch_rg(const GemvArgs &a, int splits, hipStream_t st) {
   constexpr int VG = NB >= 4 ? 4 : 1;   // vectors per wave
   const int row_blocks = (a.Npad + RG * kWave - 1) / (RG * kWave);
-  lut_gemv_batch_kernel<FMT, NB, VG, RG>
-      <<<dim3(row_blocks * splits), dim3(kWave * batch_waves<NB, VG, RG>()), 0, st>>>(a, row_blocks, splits);
+  const dim3 grid(row_blocks * splits), block(kWave * batch_waves<NB, VG, RG>());
+  if constexpr (NB == 4) {
+    if (a.xmode == kXModeRmsNorm) {
+      lut_gemv_batch_kernel<FMT, NB, VG, RG, kXModeRmsNorm><<<grid, block, 0, st>>>(a, row_blocks, splits);
+      return;
+    }
+  }
+  lut_gemv_batch_kernel<FMT, NB, VG, RG><<<grid, block, 0, st>>>(a, row_blocks, splits);
 }
 
 template <int FMT, int NB>
@@ -1514,6 +1568,8 @@ static int launch_batch_nb(const GemvArgs &a, hipStream_t st) {
 
 template <int FMT>
 static int launch_batch_fmt(const GemvArgs &a, int nb, hipStream_t st) {
+  if (a.xmode != kXModeNone && (a.xmode != kXModeRmsNorm || nb != 4))
+    return fail(LMX_ERR_INVALID_ARGUMENT, "the batched kernel applies RMSNorm to groups of 4 vectors only");
   switch (nb) {
   case 2: return launch_batch_nb<FMT, 2>(a, st);
   case 4: return launch_batch_nb<FMT, 4>(a, st);

@@ -463,3 +463,39 @@ def test_batched_mixed_format_decoder(cuda, batch):
     m = D.QuantizedModel(cfg, MIXED, seed=63)
     toks = np.random.default_rng(64).integers(0, cfg.vocab, (batch, 12))
     batched_check(D.Decoder(m, batch=batch), m, toks)
+
+
+@pytest.mark.parametrize("max_blocks", [None, "100"])
+def test_batched_decoder_quad_step(cuda, monkeypatch, max_blocks):
+    # Batch 4 with qkv and o on the four-vector kernel (RMSNorm in its table
+    # build, the residual in its epilogue, no reduction).  LMX_QUAD_MAX_BLOCKS
+    # = 100 keeps gate|up and the head (256 workgroups each) on the batched
+    # kernel with the RMSNorm in its own prologue.  Against the step with
+    # the fused reductions (LMX_QUAD_STEP=0) and the oracle's logits.
+    if max_blocks:
+        monkeypatch.setenv("LMX_QUAD_MAX_BLOCKS", max_blocks)
+    cfg = D.small_config(hidden=256, n_heads=8, n_kv_heads=2, head_dim=64, ffn=2048, vocab=4096, max_seq=64,
+                         rope_mode=D.ROPE_REFERENCE, rope_factor=1.0, rope_theta=1e6, qkv_bias=True)
+    m = D.SyntheticModel(cfg, seed=71, group=128, random_norms=True)
+    toks = np.random.default_rng(72).integers(0, cfg.vocab, (4, 10))
+
+    def logits(dec):
+        dec.reset(toks)
+        lg = torch.empty(4 * cfg.vocab, dtype=torch.float32, device="cuda")
+        out = []
+        for _ in range(toks.shape[1]):
+            dec.step(lg)
+            out.append(lg.cpu().numpy().reshape(4, cfg.vocab).copy())
+        return out
+
+    dec = D.Decoder(m, batch=4)
+    assert [w.kernel_config()[0] for w in dec.weights[:3]] == [6, 6, 6]   # qkv, o, gate|up: 4 x 4 x 1
+    quad = logits(dec)
+    monkeypatch.setenv("LMX_QUAD_STEP", "0")
+    fused = logits(dec)
+    refs = [oracle.OracleDecoder(m) for _ in range(4)]
+    for pos in range(toks.shape[1]):
+        for b in range(4):
+            want = refs[b].step(toks[b, pos], pos)
+            assert rel_max_err(quad[pos][b], fused[pos][b]) < 1e-5, (b, pos)
+            assert rel_max_err(quad[pos][b], want) < DECODE_TOL, (b, pos)
