@@ -822,7 +822,8 @@ bool quad_step(const lmx_decoder *d) {
   if (d->batch != 4 || (e && std::atoi(e) == 0) || !d->head->batched) return false;
   for (const lmx_decoder::Layer &L : d->layers)
     if (!quad_serves(decode_args(L.qkv, kXModeRmsNorm, kEpiStore)) || !quad_serves(decode_args(L.o, kXModeNone, kEpiStore)) ||
-        !L.gate_up->batched || !L.down->batched || !batched_epilogue_ok(L.gate_up, kEpiSiluPair, 4))
+        !L.qkv->batched || !L.o->batched || !L.gate_up->batched || !L.down->batched ||
+        !batched_epilogue_ok(L.gate_up, kEpiSiluPair, 4))
       return false;
   return true;
 }

@@ -179,20 +179,21 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_kernel(GemvArgs a, int
   const int r = rb * ROWS + threadIdx.x;
   float out = 0.0f;
   if (r < a.rows) {
-    // Sum the partials in split order; loads go out 32 at a time so their
-    // latencies overlap (one round trip up to 32 splits, K = 8192 at
+    // Sum the partials in split order; loads go out 48 at a time so their
+    // latencies overlap (one round trip up to 48 splits, K = 12288 at
     // 256-wide slices).
+    constexpr int RL = 48;
     float s = 0.0f;
     const float *pr = a.partials + r;
-    for (int k0s = 0; k0s < splits; k0s += 32) {
-      float v[32];
+    for (int k0s = 0; k0s < splits; k0s += RL) {
+      float v[RL];
 #pragma unroll
-      for (int j = 0; j < 32; ++j)
+      for (int j = 0; j < RL; ++j)
         v[j] = k0s + j < splits
                    ? __hip_atomic_load(pr + size_t(k0s + j) * a.Npad, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
                    : 0.0f;
 #pragma unroll
-      for (int j = 0; j < 32; ++j) s += v[j];
+      for (int j = 0; j < RL; ++j) s += v[j];
     }
     out = a.bias ? s + a.bias[r] : s;
     a.y[r] = out;
