@@ -454,11 +454,16 @@ def test_mixed_format_model_and_lutmac_v2_round_trip(cuda, tmp_path):
     check_against(ours, oracle.OracleDecoder(m), toks)
 
 
-@pytest.mark.parametrize("batch", [4, 8])
-def test_batched_mixed_format_decoder(cuda, batch):
-    # the batched decoder (fused norm / SiLU epilogues, every row in a group)
-    # on ternary / binary / RRQ-3 / RRQ-2 linears, whose activations the
-    # batched kernel rotates, against one oracle decoder per sequence
+@pytest.mark.parametrize("batch,max_blocks", [(4, None), (4, "50"), (8, None)])
+def test_batched_mixed_format_decoder(cuda, monkeypatch, batch, max_blocks):
+    # the batched decoder on ternary / binary / RRQ-3 / RRQ-2 linears, whose
+    # activations the kernels rotate, against one oracle decoder per
+    # sequence: batch 8 with the fused norm / SiLU epilogues, batch 4 with
+    # the four-vector kernels (LMX_QUAD_MAX_BLOCKS = 50: gate|up (64
+    # workgroups) and the head (63) on the batched kernel with its RMSNorm
+    # prologue and the rotation after it)
+    if max_blocks:
+        monkeypatch.setenv("LMX_QUAD_MAX_BLOCKS", max_blocks)
     cfg = D.small_config(rope_mode=D.ROPE_REFERENCE, rope_factor=1.0, rope_theta=10000.0, max_seq=64)
     m = D.QuantizedModel(cfg, MIXED, seed=63)
     toks = np.random.default_rng(64).integers(0, cfg.vocab, (batch, 12))
