@@ -81,6 +81,9 @@ int choose_fullk(int fmt, size_t Npad, size_t Kp, int kfamily) {
   format_info(fmt, &fi);
   auto fits = [&](int cfg) {
     const FullKShape f = fullk_shape(cfg);
+    if (cfg == kFullK_8x8x2L)   // the lean kernel only, which serves every 4-bit transform
+      return fmt == LMX_FMT_INT4 && kfamily != kKernelGeneric && size_t(f.waves * f.h * f.cps) >= Kc &&
+             layered_lds_bytes(f.waves, f.h, f.cps, Kc) <= kMaxLdsBytes;
     // Weight words stay in registers (no spills): up to 8 plane words per
     // lane in the generic kernel; 16 (int8 over two steps) in the
     // interleaved kernel, which always serves 16x2x2 when it is allowed.
@@ -108,8 +111,8 @@ int choose_fullk(int fmt, size_t Npad, size_t Kp, int kfamily) {
   }
   int best = kFullK_None;
   size_t best_wg = 0, best_slots = 0;
-  for (int cfg = kFullK_16x2x2; cfg <= kFullK_8x8x1; ++cfg) {
-    if (cfg == kFullK_8x8x1 && !wide) continue;
+  for (int cfg = kFullK_16x2x2; cfg <= kFullK_8x8x2L; ++cfg) {
+    if ((cfg == kFullK_8x8x1 || cfg == kFullK_8x8x2L) && !wide) continue;
     if (!fits(cfg)) continue;
     const FullKShape f = fullk_shape(cfg);
     const size_t wg = workgroups(cfg), slots = size_t(f.waves * f.h * f.cps);

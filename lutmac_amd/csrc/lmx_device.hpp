@@ -106,9 +106,7 @@ __host__ __device__ constexpr uint32_t group_offset(int g) {
   return STAG ? uint32_t(64 * g + 16 * ((g >> 2) & 3) + 64 * (g >> 4)) : uint32_t(64 * g);
 }
 constexpr uint32_t kStagChunkBytes = 2176;
-// A staggered chunk block rounded up to 256 B (v_perm keeps only bytes 1-2
-// of a table base), the stride of chunks whose tables sit back to back.
-constexpr uint32_t kIplChunkBytes = 2304;   // group_offset<true>(31) + 64, 16-byte multiple
+static_assert(kIplChunkBytes >= group_offset<true>(31) + 64 + 64, "a staggered chunk block and its 64-byte slice shift");
 // One k-slice of CPS staggered chunk blocks plus 64 B (room for the H = 4
 // slice shift), rounded up to 256 B so every slice base is 256-byte aligned.
 __host__ __device__ constexpr uint32_t stag_slice_bytes(int cps) { return (cps * kStagChunkBytes + 64 + 255) / 256 * 256; }

@@ -106,13 +106,24 @@ enum {
   kFullK_16x1x1 = 4,  // 64 rows, 16 slices of 128: K <= 2048
   kFullK_16x4x1 = 5,  // 16 rows, 64 slices of 128: K <= 8192
   kFullK_4x4x1 = 6,   // 16 rows, 16 slices of 128: K <= 2048
-  kFullK_8x8x1 = 7    // 8 rows, 64 slices of 128: K <= 8192
+  kFullK_8x8x1 = 7,   // 8 rows, 64 slices of 128: K <= 8192
+  kFullK_8x8x2L = 8   // 8 rows, 64 slices x 2 layered chunks (slice s: chunks s, s + 64): 4-bit,
+                      // the lean kernel only, K <= 8960 (tables of 70 chunks back to back)
 };
 
 constexpr size_t kMaxLdsBytes = 160 * 1024;  // LDS per workgroup on gfx950
 
 // LDS of a full-K launch: x sums + slice partials (rounded to 256 B), then
 // one table region of cps*2048 + 256 B per slice that holds chunks.
+// A staggered chunk block rounded up to 256 B (v_perm keeps only bytes 1-2
+// of a table base), the stride of chunks whose tables sit back to back.
+constexpr uint32_t kIplChunkBytes = 2304;
+
+// LDS of a layered launch (kFullK_8x8x2L): the prefix, then Kc chunk blocks.
+inline size_t layered_lds_bytes(int waves, int h, int cps, size_t Kc) {
+  return (size_t(waves * h * cps + waves * kWave) * 4 + 255) / 256 * 256 + Kc * kIplChunkBytes;
+}
+
 inline size_t fullk_lds_bytes(int waves, int h, int cps, size_t Kc) {
   const size_t prefix = (size_t(waves * h * cps + waves * kWave) * 4 + 255) / 256 * 256;
   const size_t used = (Kc + cps - 1) / cps;
@@ -129,6 +140,7 @@ inline FullKShape fullk_shape(int cfg) {
   case kFullK_16x4x1: return {16, 4, 1};
   case kFullK_4x4x1: return {4, 4, 1};
   case kFullK_8x8x1: return {8, 8, 1};
+  case kFullK_8x8x2L: return {8, 8, 2};
   }
   return {0, 0, 0};
 }

@@ -411,7 +411,11 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_fullk_kernel(GemvArgs 
 // transform XM (kXMode*) and the epilogue EPI (kEpi*) fixed at compile
 // time.  Needs H*CPS even (each wave owns whole 256-chunks).  No argmax
 // epilogue.
-template <int FMT, bool ROT, int WAVES, int H, int CPS, int XM, int EPI = kEpiStore>
+// LAY (layered): slice s owns chunks s, s + NS, s + 2 NS, ... (not CPS
+// consecutive ones), and chunk ch keeps its tables at ch * kIplChunkBytes,
+// back to back: the last layer may be ragged (K = 8960 = 70 chunks on 64
+// slices: 6 slices do two chunks), and 70 chunks' tables fit the LDS.
+template <int FMT, bool ROT, int WAVES, int H, int CPS, int XM, int EPI = kEpiStore, bool LAY = false>
 __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_plain_kernel(GemvArgs a) {
   constexpr int P = Fmt<FMT>::P, NA = Fmt<FMT>::NA, S = Fmt<FMT>::S;
   constexpr int RW = kWave / H;
@@ -420,6 +424,7 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_plain_kernel(GemvArgs 
   constexpr int NS = WAVES * H;
   constexpr uint32_t SSTRIDE = stag_slice_bytes(CPS);
   constexpr int XJ = H * CPS / 2;
+  static_assert(!LAY || H % 2 == 0, "layered: whole 256-chunks per wave and layer");
   static_assert(H * CPS % 2 == 0, "whole 256-chunks per wave");
   constexpr uint32_t PREFIX = fullk_prefix_bytes<WAVES, H, CPS>();
   extern __shared__ __attribute__((aligned(256))) float lds[];
@@ -441,11 +446,15 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_plain_kernel(GemvArgs 
   // ---- x of this wave's 256-chunks (clamped in bounds, masked below) ----
   const int C2n = a.Kp / kRotChunk;
   const int c2base = wave * XJ;
+  // the wave's j-th 256-chunk (increasing in j)
+  const auto c2_of = [&](int j) { return LAY ? (j / (H / 2)) * (NS / 2) + wave * (H / 2) + j % (H / 2) : c2base + j; };
+  // the chunk that slice s looks up at its step c
+  const auto chunk_of = [&](int c) { return LAY ? c * NS + s : s * CPS + c; };
   constexpr bool AUX = XM == kXModeRmsNorm || XM == kXModeSiluMul;
   float4 xr[XJ], xa[XJ];
 #pragma unroll
   for (int j = 0; j < XJ; ++j) {
-    const int k = min(min(c2base + j, C2n - 1) * kRotChunk + 4 * lane, a.cols - 4);
+    const int k = min(min(c2_of(j), C2n - 1) * kRotChunk + 4 * lane, a.cols - 4);
     xr[j] = *reinterpret_cast<const float4 *>(a.x + k);
     // norm weight, or the up half of a gate|up vector
     if constexpr (AUX) xa[j] = *reinterpret_cast<const float4 *>((XM == kXModeRmsNorm ? a.xw : a.x + a.cols) + k);
@@ -459,14 +468,14 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_plain_kernel(GemvArgs 
   const u32x4 *__restrict__ pl = reinterpret_cast<const u32x4 *>(a.planes);
   const uint32_t Npad = uint32_t(a.Npad);
   auto load_planes = [&](int c) {
-    const uint32_t ch = uint32_t(min(s * CPS + c, Kc - 1));
+    const uint32_t ch = uint32_t(min(chunk_of(c), Kc - 1));
 #pragma unroll
     for (int p = 0; p < P; ++p) w[c][p] = __builtin_nontemporal_load(pl + ((ch * P + p) * Npad + uint32_t(lr)));
   };
   load_planes(0);
 #pragma unroll
   for (int c = 0; c < CPS; ++c) {
-    const int ch = min(s * CPS + c, Kc - 1);
+    const int ch = min(chunk_of(c), Kc - 1);
     const int g = a.gshift >= 0 ? ch >> a.gshift : ch / a.group_chunks;
 #pragma unroll
     for (int t = 0; t < S; ++t) sc[c][t] = a.scales[(uint32_t(t * a.n_groups + g)) * Npad + uint32_t(lr)];
@@ -482,8 +491,8 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_plain_kernel(GemvArgs 
 #pragma unroll
     for (int j = 0; j < XJ; ++j) {
       float x0, x1, x2, x3;
-      mask_x4(xr[j], (c2base + j) * kRotChunk, a.cols, lane, x0, x1, x2, x3);
-      if (c2base + j < C2n) ss += (x0 * x0 + x1 * x1) + (x2 * x2 + x3 * x3);
+      mask_x4(xr[j], c2_of(j) * kRotChunk, a.cols, lane, x0, x1, x2, x3);
+      if (c2_of(j) < C2n) ss += (x0 * x0 + x1 * x1) + (x2 * x2 + x3 * x3);
     }
     inv_rms = wg_inv_rms_from<WAVES * kWave>(ss, a.cols, a.eps, red);
   }
@@ -492,7 +501,7 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_plain_kernel(GemvArgs 
   const uint32_t goff = group_offset<true>(lane & 31);
 #pragma unroll
   for (int j = 0; j < XJ; ++j) {
-    const int c2 = c2base + j;
+    const int c2 = c2_of(j);
     if (c2 >= C2n) break;   // wave-uniform
     float x0, x1, x2, x3;
     mask_x4(xr[j], c2 * kRotChunk, a.cols, lane, x0, x1, x2, x3);
@@ -504,9 +513,9 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_plain_kernel(GemvArgs 
     float t[16];
     group_table(x0, x1, x2, x3, t);
     const int ch = c2 * 2 + (lane >> 5);
-    const int ts = ch / CPS;
-    float4 *dst = reinterpret_cast<float4 *>(tables + ts * SSTRIDE + slice_shift<H>(ts) +
-                                             (ch % CPS) * kStagChunkBytes + goff);
+    const int ts = LAY ? ch % NS : ch / CPS;   // the slice that looks it up
+    float4 *dst = reinterpret_cast<float4 *>(
+        tables + (LAY ? ch * kIplChunkBytes : ts * SSTRIDE + (ch % CPS) * kStagChunkBytes) + slice_shift<H>(ts) + goff);
     dst[0] = make_float4(t[0], t[1], t[2], t[3]);
     dst[1] = make_float4(t[4], t[5], t[6], t[7]);
     dst[2] = make_float4(t[8], t[9], t[10], t[11]);
@@ -527,15 +536,18 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_plain_kernel(GemvArgs 
   constexpr float kScale = ROT ? 0.0625f : 1.0f;   // the FWHT's 1/16, exact
   float acc = 0.0f;
   {
-    const uint32_t tbase = lds_addr(lds) + PREFIX + min(s, used - 1) * SSTRIDE;
+    const uint32_t tbase = lds_addr(lds) + PREFIX + (LAY ? 0u : min(s, used - 1) * SSTRIDE);
     const uint32_t shift = slice_shift<H>(s) * 0x01010101u;
 #pragma unroll
     for (int c = 0; c < CPS; ++c) {
       float A[NA];
 #pragma unroll
       for (int i = 0; i < NA; ++i) A[i] = 0.0f;
-      chunk_lookups<FMT, true>(w[c], tbase, shift, A, c * kStagChunkBytes);
-      const int ch = s * CPS + c;
+      if constexpr (LAY)
+        chunk_lookups<FMT, true>(w[c], tbase + uint32_t(min(chunk_of(c), Kc - 1)) * kIplChunkBytes, shift, A);
+      else
+        chunk_lookups<FMT, true>(w[c], tbase, shift, A, c * kStagChunkBytes);
+      const int ch = chunk_of(c);
       float xs = 0.0f;
       if constexpr (Fmt<FMT>::XS) xs = xsum[min(ch, Kc - 1)];
       float scl[S];
@@ -704,22 +716,23 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_ipl_kernel(GemvArgs a)
   }
 }
 
-template <int WAVES, int H, int CPS>
+template <int WAVES, int H, int CPS, bool LAY = false>
 constexpr size_t plain_lds_bytes(size_t Kc) {
-  return fullk_prefix_bytes<WAVES, H, CPS>() + (Kc + CPS - 1) / CPS * stag_slice_bytes(CPS);
+  return fullk_prefix_bytes<WAVES, H, CPS>() +
+         (LAY ? Kc * kIplChunkBytes : (Kc + CPS - 1) / CPS * stag_slice_bytes(CPS));
 }
 
-template <int FMT, bool ROT, int WAVES, int H, int CPS, int XM, int EPI = kEpiStore>
+template <int FMT, bool ROT, int WAVES, int H, int CPS, int XM, int EPI = kEpiStore, bool LAY = false>
 static int launch_plain_kernel(const GemvArgs &a, hipStream_t st) {
-  const size_t lds = plain_lds_bytes<WAVES, H, CPS>(size_t(a.Kp / kChunk));
+  const size_t lds = plain_lds_bytes<WAVES, H, CPS, LAY>(size_t(a.Kp / kChunk));
   if (lds > kMaxLdsBytes) return 1;   // staggered tables do not fit: the generic kernel serves it
   static const hipError_t attr = hipFuncSetAttribute(
-      reinterpret_cast<const void *>(&lut_gemv_plain_kernel<FMT, ROT, WAVES, H, CPS, XM, EPI>),
+      reinterpret_cast<const void *>(&lut_gemv_plain_kernel<FMT, ROT, WAVES, H, CPS, XM, EPI, LAY>),
       hipFuncAttributeMaxDynamicSharedMemorySize, int(kMaxLdsBytes));
   if (attr != hipSuccess) return fail(LMX_ERR_LAUNCH_FAILED, "hipFuncSetAttribute: %s", hipGetErrorString(attr));
   constexpr int RW = kWave / H;
   const int blocks = EPI == kEpiSiluPair ? a.rows / RW : (a.Npad + RW - 1) / RW;
-  lut_gemv_plain_kernel<FMT, ROT, WAVES, H, CPS, XM, EPI><<<dim3(blocks), dim3(WAVES * kWave), lds, st>>>(a);
+  lut_gemv_plain_kernel<FMT, ROT, WAVES, H, CPS, XM, EPI, LAY><<<dim3(blocks), dim3(WAVES * kWave), lds, st>>>(a);
   return LMX_OK;
 }
 
@@ -735,7 +748,7 @@ static int launch_ipl_kernel(const GemvArgs &a, hipStream_t st) {
   return LMX_OK;
 }
 
-template <int FMT, int WAVES, int H, int CPS>
+template <int FMT, int WAVES, int H, int CPS, bool LAY = false>
 static int launch_plain_cfg(const GemvArgs &a, hipStream_t st) {
   // Interleaved where it measured faster: two k-slices per wave and at least
   // two steps per wave (one step has nothing to interleave; 17920 x 1536
@@ -744,7 +757,7 @@ static int launch_plain_cfg(const GemvArgs &a, hipStream_t st) {
     // gate|up of the decode step: RMSNorm in, SiLU(gate)*up out (4-bit, unrotated)
     if constexpr (FMT == LMX_FMT_INT4)
       if (a.rotate == LMX_ROTATE_NONE && a.xmode == kXModeRmsNorm && a.rows % (kWave / H) == 0)
-        return launch_plain_kernel<FMT, false, WAVES, H, CPS, kXModeRmsNorm, kEpiSiluPair>(a, st);
+        return launch_plain_kernel<FMT, false, WAVES, H, CPS, kXModeRmsNorm, kEpiSiluPair, LAY>(a, st);
     return 1;
   }
   if (a.xmode != kXModeNone) {
@@ -753,22 +766,22 @@ static int launch_plain_cfg(const GemvArgs &a, hipStream_t st) {
     if constexpr (FMT == LMX_FMT_INT4) {
       if (a.rotate == LMX_ROTATE_NONE) {
         switch (a.xmode) {
-        case kXModeRmsNorm: return launch_plain_kernel<FMT, false, WAVES, H, CPS, kXModeRmsNorm>(a, st);
-        case kXModeSiluMul: return launch_plain_kernel<FMT, false, WAVES, H, CPS, kXModeSiluMul>(a, st);
+        case kXModeRmsNorm: return launch_plain_kernel<FMT, false, WAVES, H, CPS, kXModeRmsNorm, kEpiStore, LAY>(a, st);
+        case kXModeSiluMul: return launch_plain_kernel<FMT, false, WAVES, H, CPS, kXModeSiluMul, kEpiStore, LAY>(a, st);
         }
       }
     }
     return 1;
   }
-  if constexpr (H == 2 && CPS >= 2 && FMT != LMX_FMT_RRQ3) {
+  if constexpr (!LAY && H == 2 && CPS >= 2 && FMT != LMX_FMT_RRQ3) {
     if (a.kfamily != kKernelLean) {
       const int r = a.rotate == LMX_ROTATE_FWHT256 ? launch_ipl_kernel<FMT, true, WAVES, CPS>(a, st)
                                                    : launch_ipl_kernel<FMT, false, WAVES, CPS>(a, st);
       if (r != 1) return r;
     }
   }
-  if (a.rotate == LMX_ROTATE_FWHT256) return launch_plain_kernel<FMT, true, WAVES, H, CPS, kXModeNone>(a, st);
-  return launch_plain_kernel<FMT, false, WAVES, H, CPS, kXModeNone>(a, st);
+  if (a.rotate == LMX_ROTATE_FWHT256) return launch_plain_kernel<FMT, true, WAVES, H, CPS, kXModeNone, kEpiStore, LAY>(a, st);
+  return launch_plain_kernel<FMT, false, WAVES, H, CPS, kXModeNone, kEpiStore, LAY>(a, st);
 }
 
 // The plain kernel serves full-K launches without a fused transform or an
@@ -782,6 +795,9 @@ static int launch_plain(const GemvArgs &a, hipStream_t st) {
   case kFullK_16x4x1: return launch_plain_cfg<FMT, 16, 4, 1>(a, st);
   case kFullK_4x4x1: return launch_plain_cfg<FMT, 4, 4, 1>(a, st);
   case kFullK_8x8x1: return launch_plain_cfg<FMT, 8, 8, 1>(a, st);
+  case kFullK_8x8x2L:
+    if constexpr (FMT == LMX_FMT_INT4) return launch_plain_cfg<FMT, 8, 8, 2, true>(a, st);
+    return 1;
   }
   return 1;
 }
@@ -828,6 +844,8 @@ static int launch_fullk(const GemvArgs &a, hipStream_t st) {
   case kFullK_16x4x1: return launch_fullk_cfg<FMT, 16, 4, 1>(a, st);
   case kFullK_4x4x1: return launch_fullk_cfg<FMT, 4, 4, 1>(a, st);
   case kFullK_8x8x1: return launch_fullk_cfg<FMT, 8, 8, 1>(a, st);
+  case kFullK_8x8x2L:
+    return fail(LMX_ERR_INVALID_ARGUMENT, "the layered 8 x 8 x 2 plan has no form for this format and transform");
   }
   return fail(LMX_ERR_INVALID_ARGUMENT, "unknown full-K configuration %d", a.fullk);
 }
@@ -875,6 +893,7 @@ int silu_pair_rows(int fmt, const GemvArgs &a) {
   case kFullK_16x4x1: lds = plain_lds_bytes<16, 4, 1>(Kc); break;
   case kFullK_4x4x1: lds = plain_lds_bytes<4, 4, 1>(Kc); break;
   case kFullK_8x8x1: lds = plain_lds_bytes<8, 8, 1>(Kc); break;
+  case kFullK_8x8x2L: lds = plain_lds_bytes<8, 8, 2, true>(Kc); break;
   default: return 0;   // split-K, or a configuration only the generic kernel serves
   }
   const int rw = kWave / fullk_shape(a.fullk).h;

@@ -61,17 +61,20 @@ def test_decoder_matches_oracle_qwen_style(cuda):
     check_against(D.Decoder(m), oracle.OracleDecoder(m), toks)
 
 
-def test_decoder_long_ffn(cuda):
-    # FFN 8960 (Qwen-2.5-1.5B's width): the down projection's K = 8960 fits
-    # no full-K configuration and runs split-K (35 slices) with SiLU*up fused,
-    # gate|up (17920 rows) the 8 x 32 small-K configuration
+def test_decoder_long_ffn(cuda, monkeypatch):
+    # FFN 8960 (Qwen-2.5-1.5B's width): the down projection's K = 8960 takes
+    # the layered 8 x 8 x 2 plan (70 chunks on 64 slices), gate|up (17920
+    # rows) the 8 x 32 small-K configuration; with LMX_SILU_PAIR=0 the down
+    # projection forms SiLU*up in its own table build
     cfg = D.small_config(hidden=256, ffn=8960, vocab=1000, rope_mode=D.ROPE_REFERENCE, rope_factor=1.0,
                          rope_theta=1e6)
     m = D.SyntheticModel(cfg, seed=31, group=128, random_norms=True)
     dec = D.Decoder(m)
-    assert [w.kernel_config()[0] for w in dec.weights[:4]] == [6, 6, 3, 0]   # qkv, o, gate|up, down
+    assert [w.kernel_config()[0] for w in dec.weights[:4]] == [6, 6, 3, 8]   # qkv, o, gate|up, down
     toks = np.random.default_rng(32).integers(0, cfg.vocab, 12)
     check_against(dec, oracle.OracleDecoder(m), toks)
+    monkeypatch.setenv("LMX_SILU_PAIR", "0")
+    check_against(D.Decoder(m), oracle.OracleDecoder(m), toks)
 
 
 @pytest.mark.parametrize("ffn", [768, 4096])

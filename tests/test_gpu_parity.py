@@ -220,6 +220,7 @@ PLAN_SHAPES = {
     5: (40, 8192),    # 16 x 4 x 1
     6: (33, 2048),    # 4 x 4 x 1
     7: (44, 7936),    # 8 x 8 x 1 (a ragged last workgroup, 62 of 64 slices used)
+    8: (40, 8960),    # 8 x 8 x 2 layered (70 chunks on 64 slices; 4-bit, lean kernel only)
 }
 
 
@@ -239,6 +240,8 @@ def test_forced_kernel_plans(cuda, monkeypatch, fmt, cfg, staged, family):
     used, _, st = w.kernel_config()
     cps = {1: 2, 2: 3}.get(cfg, 1)
     fits = cfg == 0 or L.PLANES[fmt] * cps <= 8 or (cfg == 1 and family == 0 and L.PLANES[fmt] * cps <= 16)
+    if cfg == 8:
+        fits = fmt == L.FMT_INT4 and family != 1
     assert used == (cfg if fits else 0) and st == staged
     y = w.gemv(dev(x), flags=L.ROTATE_FWHT256).cpu().numpy()
     ref = oracle_planes_gemv(fmt, planes, scales, rows, cols, g, x, L.ROTATE_FWHT256)
