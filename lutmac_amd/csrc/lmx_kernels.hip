@@ -857,6 +857,13 @@ static int launch_fmt(const GemvArgs &a, hipStream_t st) {
   if (a.fullk) {
     int r = 1;
     if (!a.amax && a.kfamily != kKernelGeneric) r = launch_plain<FMT>(a, st);
+    if (r == 1 && a.fullk == kFullK_8x8x2L) {
+      // the layered plan has no generic form (argmax epilogue, a transform
+      // with rotation): the split-K kernel, whose scratch every handle holds
+      GemvArgs b = a;
+      b.fullk = kFullK_None;
+      return launch_fmt<FMT>(b, st);
+    }
     if (r == 1) r = launch_fullk<FMT>(a, st);
     if (r) return r;
     hipError_t e = hipGetLastError();

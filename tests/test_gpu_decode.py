@@ -77,6 +77,25 @@ def test_decoder_long_ffn(cuda, monkeypatch):
     check_against(D.Decoder(m), oracle.OracleDecoder(m), toks)
 
 
+def test_decoder_layered_head_takes_split_k(cuda):
+    # hidden 8960: the tied 1000 x 8960 head gets the layered 8 x 8 x 2 plan,
+    # which has no argmax form, so the head GEMV (RMSNorm in, argmax keys out)
+    # runs the split-K kernel; the down projection (8960 x 256) is full-K
+    cfg = D.small_config(hidden=8960, n_layers=1, n_heads=2, n_kv_heads=1, head_dim=64, ffn=256, vocab=1000,
+                         max_seq=32, rope_mode=D.ROPE_REFERENCE, rope_factor=1.0, rope_theta=1e6)
+    m = D.SyntheticModel(cfg, seed=45, group=128, random_norms=True)
+    dec = D.Decoder(m)
+    assert dec.head.kernel_config()[0] == 8
+    toks = np.random.default_rng(46).integers(0, cfg.vocab, 6)
+    check_against(dec, oracle.OracleDecoder(m), toks)
+    out, _, _ = dec.generate(toks[:3], 6)                  # greedy: the argmax epilogue
+    o = oracle.OracleDecoder(m)
+    for pos in range(len(out) - 1):
+        lg = o.step(out[pos], pos)
+        if pos + 1 >= 3:
+            assert lg[out[pos + 1]] >= lg.max() - DECODE_TOL * np.linalg.norm(lg)
+
+
 @pytest.mark.parametrize("ffn", [768, 4096])
 def test_decoder_silu_pair_epilogue(cuda, monkeypatch, ffn):
     # gate|up writing SiLU(gate)*up itself (the 4-bit batch-1 step) against
