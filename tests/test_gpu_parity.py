@@ -344,6 +344,23 @@ def test_four_vector_full_k(cuda, monkeypatch, fmt, cfg, rows, cols, flags):
         assert rel_max_err(y[b], yb[b]) < TOL, f"vector {b}"
 
 
+@pytest.mark.parametrize("fmt", [L.FMT_INT4, L.FMT_TERNARY])
+def test_four_vector_linear_bias(cuda, fmt):
+    # lmx_linear on exactly 4 vectors of a 4 x 4 x 1 plan: the four-vector
+    # kernel's bias epilogue (ternary: the FWHT-256 lut_linear applies)
+    rows, cols = 2048, 1536
+    planes, scales, g = synth.make_weights(fmt, rows, cols, seed=90 + fmt, group=128)
+    xs = np.stack([synth.make_activations(cols, seed=900 + s, outliers=True) for s in range(4)])
+    bias = np.random.default_rng(91).standard_normal(rows).astype(np.float32)
+    w = L.Weight.from_planes(fmt, planes, scales, rows, cols, g)
+    assert w.kernel_config()[0] == 6
+    y = w.linear(dev(xs.ravel()), bias=dev(bias)).cpu().numpy().reshape(4, rows)
+    rot = L.ROTATE_FWHT256 if fmt == L.FMT_TERNARY else L.ROTATE_NONE
+    for b in range(4):
+        ref = oracle_planes_gemv(fmt, planes, scales, rows, cols, g, xs[b], rot) + bias
+        assert rel_max_err(y[b], ref) < TOL, b
+
+
 def test_batched_linear_bias_and_repeat(cuda):
     rows, cols, batch = 2048, 2048, 16
     planes, scales, g = synth.make_weights(L.FMT_INT4, rows, cols, seed=5)
