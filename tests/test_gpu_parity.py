@@ -361,6 +361,32 @@ def test_four_vector_linear_bias(cuda, fmt):
         assert rel_max_err(y[b], ref) < TOL, b
 
 
+def test_four_vector_graph_replays(cuda):
+    # the four-vector launch captured in a graph: every replay equals the
+    # eager call, with eager calls on the same handle in between
+    rows, cols = 2048, 1536
+    planes, scales, g = synth.make_weights(L.FMT_INT4, rows, cols, seed=95, group=128)
+    xs = dev(np.stack([synth.make_activations(cols, seed=950 + s) for s in range(4)]).ravel())
+    w = L.Weight.from_planes(L.FMT_INT4, planes, scales, rows, cols, g)
+    eager = w.gemv(xs).cpu().numpy()
+    out = torch.empty(4 * rows, dtype=torch.float32, device="cuda")
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        w.gemv(xs, y=out)
+    torch.cuda.current_stream().wait_stream(s)
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gr):
+        w.gemv(xs, y=out)
+    for _ in range(3):
+        out.zero_()
+        gr.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(out.cpu().numpy().view(np.uint32), eager.view(np.uint32))
+        w.gemv(xs)
+        torch.cuda.synchronize()
+
+
 def test_batched_linear_bias_and_repeat(cuda):
     rows, cols, batch = 2048, 2048, 16
     planes, scales, g = synth.make_weights(L.FMT_INT4, rows, cols, seed=5)
