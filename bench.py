@@ -544,7 +544,7 @@ def main():
         return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
-              "(see DESIGN.md for how the GEMV would shard)", file=sys.stderr)
+              "(a sharded GEMV would run this path on each GPU's row block)", file=sys.stderr)
         sys.exit(2)
 
     import torch
