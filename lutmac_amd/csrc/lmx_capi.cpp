@@ -214,7 +214,9 @@ int upload(int fmt, size_t rows, size_t cols, size_t group, const uint8_t *plane
   // Batched partials for the largest vector group (16), allocated with the
   // handle so that no GEMV call allocates (graph capture stays possible).
   if (w->batched) {
-    const size_t n = 16 * max_splits * w->Npad;
+    // 128-wide k-slices (twice the splits) where 256-wide ones give the
+    // batched kernel less than a workgroup per CU (batched_slice_splits)
+    const size_t n = 16 * batched_slice_splits(w->Npad, w->Kp) * w->Npad;
     if ((e = hipMalloc(reinterpret_cast<void **>(&w->d_bpartials), n * sizeof(float))) != hipSuccess) {
       free_weight(w);
       return hip_fail(e, "hipMalloc (batched partials)");
@@ -278,7 +280,7 @@ int gemv_batched(const lmx_weight *w, GemvArgs a, const float *x, float *y, size
   while (batch - *done >= 4) {
     const size_t left = batch - *done;
     const int nb = left >= 16 ? 16 : left >= 8 ? 8 : 4;
-    if (size_t(nb) * splits * w->Npad > w->bpartials_cap)
+    if (size_t(nb) * batched_slice_splits(w->Npad, w->Kp) * w->Npad > w->bpartials_cap)
       return fail(LMX_ERR_INVALID_ARGUMENT, "batched partials of %zu floats hold no group of %d", w->bpartials_cap, nb);
     a.x = x + *done * w->cols;
     a.y = y + *done * out_rows;

@@ -167,6 +167,15 @@ int silu_pair_rows(int fmt, const GemvArgs &a);
 // nb (2, 4, 8, 16) vectors at a.x + n*cols -> a.y + n*rows; a.partials holds
 // nb * (Kp/256) * Npad floats.
 int launch_gemv_batch(int fmt, const GemvArgs &a, int nb, void *stream);
+// k-slices of the batched kernel for a weight: 256-wide, or 128-wide where
+// the 256-wide grid at 64 rows per workgroup has fewer than kBatchMinGrid128
+// workgroups (CUs idle); the batched partials hold 16 x this x Npad floats.
+constexpr size_t kBatchMinGrid128 = 256;
+inline size_t batched_slice_splits(size_t Npad, size_t Kp) {
+  const size_t s256 = Kp / kRotChunk;
+  return (Npad / kWave) * s256 < kBatchMinGrid128 ? 2 * s256 : s256;
+}
+
 // Exactly 4 vectors (a.x [4][cols], a.y [4][rows], a.resid [4][rows]) in one
 // full-K launch with the transform a.xmode (none or RMSNorm with a.xw) and
 // epilogue a.epi (store or SiLU pair); returns 1, launching nothing, when

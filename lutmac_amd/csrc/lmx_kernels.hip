@@ -987,12 +987,15 @@ constexpr int batch_waves() { return RG * (NB / VG); }
 // row of its vectors for the sum of squares (every workgroup, so the
 // k-slices need no exchange) and the tables take x * inv_rms * xw
 // (norm.cpp:18-34).
-template <int FMT, int NB, int VG, int RG, int XM = kXModeNone>
+// CH = 2: 256-wide k-slices; CH = 1: 128-wide (twice the workgroups for
+// small matrices), the workgroup rotating the 256-chunk that holds its slice
+// and keeping the tables of its half.
+template <int FMT, int NB, int VG, int RG, int XM = kXModeNone, int CH = 2>
 __global__ __launch_bounds__((kWave * batch_waves<NB, VG, RG>())) void lut_gemv_batch_kernel(GemvArgs a,
                                                                                           int row_blocks,
                                                                                           int splits) {
   constexpr int P = Fmt<FMT>::P, NA = Fmt<FMT>::NA, S = Fmt<FMT>::S;
-  constexpr int CH = kRotChunk / kChunk;   // 2 chunks of 128 per slice
+  static_assert(CH == 1 || CH == 2, "128- or 256-wide k-slices");
   constexpr int NW = batch_waves<NB, VG, RG>();
   constexpr int NVG = NB / VG;
   constexpr int ROWS = RG * kWave;
@@ -1003,7 +1006,8 @@ __global__ __launch_bounds__((kWave * batch_waves<NB, VG, RG>())) void lut_gemv_
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
   const int rg = wave % RG, vg = wave / RG;
   const int rb = blockIdx.x % row_blocks, split = blockIdx.x / row_blocks;
-  const int k0 = split * kRotChunk;
+  const int c0 = split * CH;                        // the slice's first 128-chunk
+  const int k0 = (c0 / 2) * kRotChunk;              // the 256-chunk that holds it
   const int row = rb * ROWS + rg * kWave + lane;
   const bool active = rb * ROWS + rg * kWave < a.Npad;
   const int lr = min(row, a.Npad - 1);
@@ -1032,7 +1036,6 @@ __global__ __launch_bounds__((kWave * batch_waves<NB, VG, RG>())) void lut_gemv_
   {
     const u32x4 *__restrict__ pl = reinterpret_cast<const u32x4 *>(a.planes);
     const size_t Npad = size_t(a.Npad);
-    const int c0 = k0 / kChunk;
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
 #pragma unroll
@@ -1082,22 +1085,26 @@ __global__ __launch_bounds__((kWave * batch_waves<NB, VG, RG>())) void lut_gemv_
     if (a.rotate == LMX_ROTATE_FWHT256) fwht256_regs(x0, x1, x2, x3, lane);
     float t[16];
     group_table(x0, x1, x2, x3, t);
-    const int c = lane >> 5, g = lane & 31;
-    if constexpr (VG == 1) {
-      float4 *dst = reinterpret_cast<float4 *>(tables + (c * NVG + n / VG) * CB + g * GS);
-      dst[0] = make_float4(t[0], t[1], t[2], t[3]);
-      dst[1] = make_float4(t[4], t[5], t[6], t[7]);
-      dst[2] = make_float4(t[8], t[9], t[10], t[11]);
-      dst[3] = make_float4(t[12], t[13], t[14], t[15]);
-    } else {
-      float *dst = reinterpret_cast<float *>(tables + (c * NVG + n / VG) * CB + g * GS) + n % VG;
+    const int half = lane >> 5, g = lane & 31;
+    const int c = CH == 2 ? half : 0;              // table slot
+    const bool keep = CH == 2 || half == (c0 & 1);   // CH = 1: the slice's half only
+    if (keep) {
+      if constexpr (VG == 1) {
+        float4 *dst = reinterpret_cast<float4 *>(tables + (c * NVG + n / VG) * CB + g * GS);
+        dst[0] = make_float4(t[0], t[1], t[2], t[3]);
+        dst[1] = make_float4(t[4], t[5], t[6], t[7]);
+        dst[2] = make_float4(t[8], t[9], t[10], t[11]);
+        dst[3] = make_float4(t[12], t[13], t[14], t[15]);
+      } else {
+        float *dst = reinterpret_cast<float *>(tables + (c * NVG + n / VG) * CB + g * GS) + n % VG;
 #pragma unroll
-      for (int m = 0; m < 16; ++m) dst[m * VG] = t[m];
+        for (int m = 0; m < 16; ++m) dst[m * VG] = t[m];
+      }
     }
     if constexpr (Fmt<FMT>::XS) {
       float xs = t[15];
       xs = lane_sum<16>(xs, lane);
-      if ((lane & 31) == 0) xsum[n][c] = xs;
+      if ((lane & 31) == 0 && keep) xsum[n][c] = xs;
     }
   }
   __syncthreads();
@@ -1546,23 +1553,29 @@ int launch_gemv_quad(int fmt, const GemvArgs &a, void *stream) {
   return 1;
 }
 
-template <int FMT, int NB, int RG>
+template <int FMT, int NB, int RG, int CH = 2>
 static void launch_batch_rg(const GemvArgs &a, int splits, hipStream_t st) {
   constexpr int VG = NB >= 4 ? 4 : 1;   // vectors per wave
   const int row_blocks = (a.Npad + RG * kWave - 1) / (RG * kWave);
   const dim3 grid(row_blocks * splits), block(kWave * batch_waves<NB, VG, RG>());
   if constexpr (NB == 4) {
     if (a.xmode == kXModeRmsNorm) {
-      lut_gemv_batch_kernel<FMT, NB, VG, RG, kXModeRmsNorm><<<grid, block, 0, st>>>(a, row_blocks, splits);
+      lut_gemv_batch_kernel<FMT, NB, VG, RG, kXModeRmsNorm, CH><<<grid, block, 0, st>>>(a, row_blocks, splits);
       return;
     }
   }
-  lut_gemv_batch_kernel<FMT, NB, VG, RG><<<grid, block, 0, st>>>(a, row_blocks, splits);
+  lut_gemv_batch_kernel<FMT, NB, VG, RG, kXModeNone, CH><<<grid, block, 0, st>>>(a, row_blocks, splits);
 }
 
 template <int FMT, int NB>
 static int launch_batch_nb(const GemvArgs &a, hipStream_t st) {
-  const int splits = a.Kp / kRotChunk;
+  // 128-wide slices (one row group) where 256-wide ones would leave CUs idle
+  static const bool s128 = [] {
+    const char *e = std::getenv("LMX_BATCH_S128");
+    return !(e && std::atoi(e) == 0);
+  }();
+  const bool narrow = s128 && batched_slice_splits(size_t(a.Npad), size_t(a.Kp)) != size_t(a.Kp / kRotChunk);
+  const int splits = narrow ? a.Kp / kChunk : a.Kp / kRotChunk;
   // Rows per workgroup: 256 while that leaves a workgroup per CU, else fewer
   // (LMX_BATCH_RG = 1, 2 or 4 forces 64, 128 or 256).
   const auto grid = [&](int rg) { return (a.Npad + rg * kWave - 1) / (rg * kWave) * splits; };
@@ -1575,7 +1588,8 @@ static int launch_batch_nb(const GemvArgs &a, hipStream_t st) {
                  : grid(4) >= kBatchMinGrid ? 4
                  : grid(2) >= kBatchMinGrid ? 2
                                             : 1;
-  if (rg == 4) launch_batch_rg<FMT, NB, 4>(a, splits, st);
+  if (narrow) launch_batch_rg<FMT, NB, 1, 1>(a, splits, st);
+  else if (rg == 4) launch_batch_rg<FMT, NB, 4>(a, splits, st);
   else if (rg == 2) launch_batch_rg<FMT, NB, 2>(a, splits, st);
   else launch_batch_rg<FMT, NB, 1>(a, splits, st);
   if (a.epi == kEpiSiluPair) {
