@@ -273,8 +273,7 @@ int gemv_batched(const lmx_weight *w, GemvArgs a, const float *x, float *y, size
     return fail(LMX_ERR_INVALID_ARGUMENT, "batched epilogue %d does not cover %zu vectors of a %zu x %zu weight", a.epi,
                 batch, w->rows, w->cols);
   if (!w->batched || batch < 4 || reinterpret_cast<size_t>(x) % 16 || w->cols % 4) return LMX_OK;
-  const size_t splits = w->Kp / kRotChunk;
-  const float *resid = a.resid;   // [batch][rows] residual rows, offset with the vectors
+  const float *resid = a.resid;  // [batch][rows] residual rows, offset with the vectors
   float *y2 = a.y2;               // kEpiNormOut: [batch][rows]
   const size_t out_rows = a.epi == kEpiSiluPair ? w->rows / 2 : w->rows;
   while (batch - *done >= 4) {

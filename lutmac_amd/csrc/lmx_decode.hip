@@ -130,17 +130,24 @@ __global__ __launch_bounds__(256) void silu_mul_rows_kernel(const float *__restr
   act[size_t(blockIdx.y) * ffn + k] = a / (1.0f + expf(-a)) * g[ffn + k];
 }
 
+constexpr int kArgmaxParts = 32;   // most workgroups per logits row
+
 // Greedy token of every sequence: the first maximum of its logits row
-// (model.cpp:480-490); written unless the next position is forced.  The last
-// workgroup to finish (a ticket) advances the shared position.
+// (model.cpp:480-490); written unless the next position is forced.  Each
+// row is scanned by gridDim.x workgroups (part blockIdx.x of sequence
+// blockIdx.y), each leaving its slice's key in slots; the last of a
+// sequence's workgroups (a ticket) takes the largest key, and the last
+// sequence to finish (a second ticket) advances the shared position.
 __global__ __launch_bounds__(1024) void argmax_rows_kernel(const float *__restrict__ logits, int vocab,
                                                            int *__restrict__ tokens, int tstride,
                                                            int *__restrict__ pos_p, int n_forced, int max_pos,
-                                                           unsigned *__restrict__ ticket_p) {
-  constexpr int NT = 1024, IN = 16;   // threads, loads in flight per thread
+                                                           unsigned *__restrict__ ticket_p,
+                                                           unsigned long long *__restrict__ slots,
+                                                           unsigned *__restrict__ seq_tickets) {
+  constexpr int NT = 1024, IN = 4;   // threads, loads in flight per thread
   __shared__ unsigned long long best[16];
-  __shared__ unsigned ticket;
-  const float *lg = logits + size_t(blockIdx.x) * vocab;
+  const int part = blockIdx.x, parts = gridDim.x, b = blockIdx.y;
+  const float *lg = logits + size_t(b) * vocab;
   unsigned long long key = 0;
   // key = orderable value bits << 32 | ~index: the largest value, the lowest
   // index among equal values; NaN never wins, -0 counts as +0
@@ -151,38 +158,52 @@ __global__ __launch_bounds__(1024) void argmax_rows_kernel(const float *__restri
     const unsigned long long k = (static_cast<unsigned long long>(u) << 32) | (0xFFFFFFFFu - uint32_t(i));
     key = k > key ? k : key;
   };
-  // 16-byte loads, IN per thread in flight (every row is 16-byte aligned when
-  // the logits are and vocab % 4 == 0), then the scalar tail
-  const int n4 = vocab % 4 == 0 && reinterpret_cast<size_t>(logits) % 16 == 0 ? vocab / 4 : 0;
-  const float4 *lg4 = reinterpret_cast<const float4 *>(lg);
-  for (int i0 = threadIdx.x; i0 < n4; i0 += NT * IN) {
-    float4 v[IN];
+  // this part's slice of the row: 16-byte loads (every row is 16-byte aligned
+  // when the logits are and vocab % 4 == 0), else 4-byte ones
+  const bool vec = vocab % 4 == 0 && reinterpret_cast<size_t>(logits) % 16 == 0;
+  const int span = (vocab + 4 * parts - 1) / (4 * parts) * 4;
+  const int i0 = part * span, i1 = min(vocab, i0 + span);
+  if (vec) {
+    const float4 *lg4 = reinterpret_cast<const float4 *>(lg);
+    const int q0 = i0 / 4, q1 = i1 / 4;   // i1 is a multiple of 4 or vocab
+    for (int q = q0 + int(threadIdx.x); q < q1; q += NT * IN) {
+      float4 v[IN];
 #pragma unroll
-    for (int j = 0; j < IN; ++j) {
-      const int i = i0 + j * NT;
-      v[j] = lg4[min(i, n4 - 1)];
-    }
+      for (int j = 0; j < IN; ++j) v[j] = lg4[min(q + j * NT, q1 - 1)];
 #pragma unroll
-    for (int j = 0; j < IN; ++j) {
-      const int i = i0 + j * NT;
-      if (i < n4) fold(v[j].x, 4 * i), fold(v[j].y, 4 * i + 1), fold(v[j].z, 4 * i + 2), fold(v[j].w, 4 * i + 3);
+      for (int j = 0; j < IN; ++j) {
+        const int qq = q + j * NT;
+        if (qq < q1) fold(v[j].x, 4 * qq), fold(v[j].y, 4 * qq + 1), fold(v[j].z, 4 * qq + 2), fold(v[j].w, 4 * qq + 3);
+      }
     }
+  } else {
+    for (int i = i0 + int(threadIdx.x); i < i1; i += NT) fold(lg[i], i);
   }
-  for (int i = 4 * n4 + threadIdx.x; i < vocab; i += NT) fold(lg[i], i);
   key = wave_max_key(key, threadIdx.x & (kWave - 1));
   if ((threadIdx.x & (kWave - 1)) == 0) best[threadIdx.x / kWave] = key;
   __syncthreads();
-  if (threadIdx.x == 0) {
-    for (int w = 1; w < 16; ++w) key = best[w] > key ? best[w] : key;
-    const int idx = key ? int(0xFFFFFFFFu - uint32_t(key)) : 0;
-    const int pos = *pos_p;
-    if (pos + 1 >= n_forced && pos + 1 <= max_pos) tokens[size_t(blockIdx.x) * tstride + pos + 1] = idx;
+  if (threadIdx.x != 0) return;
+  for (int w = 1; w < 16; ++w) key = best[w] > key ? best[w] : key;
+  if (parts > 1) {
+    __hip_atomic_store(slots + size_t(b) * parts + part, key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __builtin_amdgcn_s_waitcnt(0);
-    ticket = __hip_atomic_fetch_add(ticket_p, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (ticket == gridDim.x - 1) {   // every workgroup has read the position
-      *pos_p = pos + 1;
-      __hip_atomic_store(ticket_p, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const unsigned t = __hip_atomic_fetch_add(seq_tickets + b, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (t != unsigned(parts - 1)) return;   // another part finishes the sequence
+    for (int q = 0; q < parts; ++q) {
+      const unsigned long long k =
+          __hip_atomic_load(slots + size_t(b) * parts + q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      key = k > key ? k : key;
     }
+    __hip_atomic_store(seq_tickets + b, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  const int idx = key ? int(0xFFFFFFFFu - uint32_t(key)) : 0;
+  const int pos = *pos_p;
+  if (pos + 1 >= n_forced && pos + 1 <= max_pos) tokens[size_t(b) * tstride + pos + 1] = idx;
+  __builtin_amdgcn_s_waitcnt(0);
+  const unsigned t = __hip_atomic_fetch_add(ticket_p, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (t == gridDim.y - 1) {   // every sequence has read the position
+    *pos_p = pos + 1;
+    __hip_atomic_store(ticket_p, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -589,6 +610,8 @@ struct lmx_decoder {
   float *normed = nullptr;   // batch > 1: RMSNorm output [hidden] rows
   float *act = nullptr;      // SiLU(gate)*up [ffn] rows
   unsigned *argmax_ticket = nullptr;         // batch > 1: argmax_rows_kernel's ticket
+  unsigned long long *argmax_slots = nullptr;   // batch > 1: [batch][kArgmaxParts] keys
+  unsigned *argmax_seq_tickets = nullptr;       // batch > 1: [batch] tickets
   size_t kv_seq = 0;                         // floats of one sequence's K (or V) cache, all layers
   unsigned long long *amax = nullptr;    // per-wave argmax keys of the head GEMV
   size_t amax_slots = 0;
@@ -877,8 +900,12 @@ int step_batched(lmx_decoder *d, float *logits_out, hipStream_t st) {
     if ((r = rmsnorm_rows(d, d->hidden, d->final_norm, d->normed, st))) return r;
   }
   if (!quad && (r = gemv_rows(d, d->head, d->normed, lg, nullptr, nullptr, st))) return r;
-  argmax_rows_kernel<<<dim3(unsigned(B)), dim3(1024), 0, st>>>(lg, int(c.vocab), d->tokens, int(c.max_seq + 1),
-                                                               d->pos, d->n_forced, int(c.max_seq), d->argmax_ticket);
+  // parts per row: about 256 workgroups in all (LMX_ARGMAX_PARTS overrides)
+  const char *ap = std::getenv("LMX_ARGMAX_PARTS");
+  const int parts = std::max(1, std::min(kArgmaxParts, ap ? std::atoi(ap) : int(256 / B)));
+  argmax_rows_kernel<<<dim3(unsigned(parts), unsigned(B)), dim3(1024), 0, st>>>(
+      lg, int(c.vocab), d->tokens, int(c.max_seq + 1), d->pos, d->n_forced, int(c.max_seq), d->argmax_ticket,
+      d->argmax_slots, d->argmax_seq_tickets);
   return launch_err("argmax_rows");
 }
 
@@ -1023,6 +1050,8 @@ int lmx_decoder_create_batched(const lmx_decoder_config *cfg, size_t batch, lmx_
       (B > 1 && (st = d->alloc(reinterpret_cast<void **>(&d->normed), B * c.hidden * 4))) ||
       (st = d->alloc(reinterpret_cast<void **>(&d->act), B * c.ffn * 4)) ||
       (B > 1 && (st = d->alloc(reinterpret_cast<void **>(&d->argmax_ticket), sizeof(unsigned)))) ||
+      (B > 1 && (st = d->alloc(reinterpret_cast<void **>(&d->argmax_slots), B * kArgmaxParts * 8))) ||
+      (B > 1 && (st = d->alloc(reinterpret_cast<void **>(&d->argmax_seq_tickets), B * sizeof(unsigned)))) ||
       (st = upload(d, &d->freq, fr.data(), fr.size()))) {
     delete d;
     return st;

@@ -354,13 +354,20 @@ def test_batched_generate_graph_equals_eager_and_oracle(cuda):
                 assert lg[out[b, pos + 1]] >= lg.max() - DECODE_TOL * np.linalg.norm(lg)
 
 
+@pytest.mark.parametrize("parts", [None, "1", "3"])
 @pytest.mark.parametrize("vocab", [1000, 1001])
-def test_batched_greedy_token_is_first_maximum(cuda, vocab):
+def test_batched_greedy_token_is_first_maximum(cuda, monkeypatch, vocab, parts):
     # argmax_rows_kernel: 16-byte loads when vocab % 4 == 0 (1000), the scalar
-    # loop otherwise (1001); every chosen token is numpy's first maximum of the
-    # step's own logits row
+    # loop otherwise (1001); each row split over the default number of
+    # workgroups, over one, or over three; every chosen token is numpy's first
+    # maximum of the step's own logits row.  Head rows repeat with period 97,
+    # so every maximum recurs in other workgroups' slices of the row.
+    if parts is not None:
+        monkeypatch.setenv("LMX_ARGMAX_PARTS", parts)
     cfg = D.small_config(vocab=vocab, max_seq=32)
     m = D.SyntheticModel(cfg, seed=61, group=128, random_norms=True)
+    per = np.arange(vocab) % 97
+    m.head = (m.head[0][:, per].copy(), m.head[1][:, per].copy())
     B, n = 4, 12
     dec = D.Decoder(m, batch=B)
     dec.reset(np.random.default_rng(62).integers(0, vocab, (B, 1)))
