@@ -351,7 +351,9 @@ __device__ __forceinline__ void merge_pass(Load ld, int c0, int nb, int lane, fl
 // that holds the position (own): scores, a partial softmax and the weighted
 // V sum (model.cpp:326-372, attention.cpp:23-42), returned as (m, l, o).
 // pwrow is the wave's 64-float LDS scratch.  Every lane of the wave calls it.
-template <int HD>
+// LEAN unrolls the loops partially (fewer registers, for a caller that holds
+// the next chunk's rows in registers meanwhile).
+template <int HD, bool LEAN = false>
 __device__ __forceinline__ void chunk_attend(const float (*ks)[HD + 4], const float (*vs)[HD], const float *qrow,
                                              const float *knew, const float (&vn)[HD / kWave], float *pwrow, int t0,
                                              int pos, bool own, float scale, int lane, float &m, float &l,
@@ -366,7 +368,7 @@ __device__ __forceinline__ void chunk_attend(const float (*ks)[HD + 4], const fl
   if (valid) {
     const float *kv = lane == jnew ? knew : ks[lane];
     float acc = 0.0f;
-#pragma unroll
+#pragma unroll(LEAN ? 8 : HD / 4)
     for (int d4 = 0; d4 < HD / 4; ++d4) {
       const float4 k4 = *reinterpret_cast<const float4 *>(kv + 4 * d4);
       const float4 q4 = *reinterpret_cast<const float4 *>(qrow + 4 * d4);
@@ -388,43 +390,49 @@ __device__ __forceinline__ void chunk_attend(const float (*ks)[HD + 4], const fl
   for (int u = 0; u < VD; ++u) {
     const int d = u * kWave + lane;
     float s8[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-#pragma unroll
+#pragma unroll(LEAN ? 16 : kAttnChunk)
     for (int j = 0; j < kAttnChunk; ++j) s8[j % 8] += pwrow[j] * vs[j][d];
     o[u] = ((s8[0] + s8[1]) + (s8[2] + s8[3])) + ((s8[4] + s8[5]) + (s8[6] + s8[7]));
     if (own) o[u] += enew * vn[u];
   }
 }
 
-// Attention with the chunk merge inside: one workgroup per (KV head, 64
-// positions), 8 waves.  All 8 waves first load the chunk's 64 cached K and V
-// rows of the KV head into LDS (every row is in bounds: the cache holds whole
-// chunks), so the chunk costs one memory round trip whatever the head
-// dimension; wave w < group then serves query head kvh*group + w: RoPE of q
-// (and of the new key in the chunk holding the position), scores, a partial
-// softmax and the weighted V sum of the chunk (model.cpp:326-372,
-// attention.cpp:23-42), written as (m, l, o[HD]).  The last workgroup of the
-// KV head to finish (a device-scope ticket, the split-K handoff of the GEMV)
-// merges the chunks up to the position in chunk order, x = sum_c e^(m_c - M)
-// o_c / sum_c e^(m_c - M) l_c with M = max_c m_c, and writes the heads'
-// attention output, so the o-projection is a plain GEMV.  Partials and
-// tickets travel as device-scope relaxed atomics (no L2 writeback needed);
-// the merging workgroup clears the ticket for the next step.
+// Attention with the chunk merge inside: one workgroup per (KV head, CPW
+// consecutive 64-position chunks, a "unit"), 8 waves.  All 8 waves first
+// request the first chunk's cached K and V rows of the KV head (every row is
+// in bounds: the cache holds whole chunks), so a chunk costs one memory round
+// trip whatever the head dimension (a second chunk's rows are requested
+// when the first's are in LDS, and arrive while it is attended); chunk by
+// chunk the rows pass through LDS and wave w < group serves query head
+// kvh*group + w: RoPE of q (and of the new key in the chunk holding the
+// position), scores, a partial softmax and the weighted V sum of the chunk
+// (model.cpp:326-372, attention.cpp:23-42);
+// the unit's chunks combine as (m, l, o[HD]) with the larger maximum.  The
+// last workgroup of the KV head to finish (a device-scope ticket, the
+// split-K handoff of the GEMV) merges the units up to the position in order,
+// x = sum_u e^(m_u - M) o_u / sum_u e^(m_u - M) l_u with M = max_u m_u, and
+// writes the heads' attention output, so the o-projection is a plain GEMV.
+// Partials and tickets travel as device-scope relaxed atomics (no L2
+// writeback needed); the merging workgroup clears the ticket for the next
+// step.  CPW = 2 halves the workgroups where one per chunk would not all be
+// resident at once (two workgroups per CU by their LDS).
 // Cost follows the position, not the cache capacity (the reference loops
-// to pos only, model.cpp:344-372): chunks below spec_chunks load their rows
-// speculatively, before the position is known; later chunks read the
-// position first and, when it lies before them, load nothing and only take
-// their ticket (the merge reads chunks up to the position only).
-template <int HD>
+// to pos only, model.cpp:344-372): units below spec_units load their rows
+// speculatively, before the position is known; later units read the
+// position first and, when it lies before them, load nothing and take no
+// ticket (the merge reads units up to the position only).
+template <int HD, int CPW>
 __global__ __launch_bounds__(512) void attn_kernel(const float *__restrict__ qkv, float *__restrict__ kc,
                                                    float *__restrict__ vc, const int *__restrict__ pos_p,
                                                    const float *__restrict__ freq, float pos_div, int n_heads,
                                                    int n_kv, int group, int max_seq, float scale,
                                                    float *__restrict__ part, int n_chunks,
                                                    unsigned *__restrict__ tickets, float *__restrict__ out,
-                                                   size_t qkv_stride, size_t kv_stride, int spec_chunks) {
+                                                   size_t qkv_stride, size_t kv_stride, int spec_units) {
   constexpr int VD = HD / kWave;          // value columns per lane
   constexpr int NT = 512;
-  constexpr int KV4 = kAttnChunk * HD / 4 / NT;   // float4 of K (and of V) per thread
+  constexpr int KV4 = kAttnChunk * HD / 4 / NT;   // float4 of K (and of V) per thread and chunk
+  constexpr int UNIT = CPW * kAttnChunk;          // positions per workgroup
   static_assert(KV4 >= 1, "chunk rows cover the workgroup");
   __shared__ float ks[kAttnChunk][HD + 4];   // padded rows: lane j reads row j without bank conflicts
   __shared__ float vs[kAttnChunk][HD];
@@ -444,33 +452,48 @@ __global__ __launch_bounds__(512) void attn_kernel(const float *__restrict__ qkv
     out += b * size_t(n_heads) * HD;
   }
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
-  const int kvh = blockIdx.x % n_kv, chunk = blockIdx.x / n_kv;
+  const int kvh = blockIdx.x % n_kv, unit = blockIdx.x / n_kv;
   const size_t row = size_t(n_kv) * HD;
-  const int t0 = chunk * kAttnChunk;
+  const int t0 = unit * UNIT;
   const float *kin = qkv + size_t(n_heads) * HD + kvh * HD;
   const float *vin = kin + row;
   const int pos = min(*pos_p, max_seq - 1);
-  // Past the speculative window a chunk learns the position first (an
+  // Past the speculative window a unit learns the position first (an
   // atomic load: never hoisted above this uniform branch, so the window's
-  // chunks issue their loads without waiting for it).
+  // units issue their loads without waiting for it).
   bool skip = false;
-  if (chunk >= spec_chunks)
+  if (unit >= spec_units)
     skip = t0 > min(__hip_atomic_load(pos_p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), max_seq - 1);
   if (!skip) {   // uniform over the workgroup
 
   // ---- every global operand requested before the first wait (one round
-  // trip): the chunk's K and V rows, the query head's q, the new key and
+  // trip): the unit's K and V rows, the query head's q, the new key and
   // value, and the RoPE frequencies (all waves load them; in bounds) ----
   constexpr int HALF = HD / 2;
   constexpr int RP = (HALF + kWave - 1) / kWave;   // rotation pairs per lane
   float4 kr[KV4], vr[KV4];
+  const auto load_rows = [&](int q) {
+    // a unit's chunk past the cache's last one (odd chunk count) loads that
+    // last chunk's rows and holds no position
+    const int tq = min(t0 + q * kAttnChunk, (n_chunks - 1) * kAttnChunk);
 #pragma unroll
-  for (int i = 0; i < KV4; ++i) {
-    const int f = int(threadIdx.x) + i * NT;          // float4 index in the 64 x HD chunk
-    const int r = f / (HD / 4), c4 = f % (HD / 4);
-    kr[i] = *reinterpret_cast<const float4 *>(kc + size_t(t0 + r) * row + kvh * HD + 4 * c4);
-    vr[i] = *reinterpret_cast<const float4 *>(vc + size_t(t0 + r) * row + kvh * HD + 4 * c4);
-  }
+    for (int i = 0; i < KV4; ++i) {
+      const int f = int(threadIdx.x) + i * NT;          // float4 index in the 64 x HD chunk
+      const int r = f / (HD / 4), c4 = f % (HD / 4);
+      kr[i] = *reinterpret_cast<const float4 *>(kc + size_t(tq + r) * row + kvh * HD + 4 * c4);
+      vr[i] = *reinterpret_cast<const float4 *>(vc + size_t(tq + r) * row + kvh * HD + 4 * c4);
+    }
+  };
+  load_rows(0);
+  const auto store_rows = [&]() {
+#pragma unroll
+    for (int i = 0; i < KV4; ++i) {
+      const int f = int(threadIdx.x) + i * NT;
+      const int r = f / (HD / 4), c4 = f % (HD / 4);
+      *reinterpret_cast<float4 *>(&ks[r][4 * c4]) = kr[i];
+      *reinterpret_cast<float4 *>(&vs[r][4 * c4]) = vr[i];
+    }
+  };
   const float *qin = qkv + size_t(kvh * group + (wave < group ? wave : 0)) * HD;
   float qa[RP], qb[RP], ka[RP], kb[RP], fr[RP], vn[VD];
 #pragma unroll
@@ -494,15 +517,9 @@ __global__ __launch_bounds__(512) void attn_kernel(const float *__restrict__ qkv
   for (int i = 0; i < RP; ++i) asm volatile("" ::"v"(fr[i]), "v"(qa[i]), "v"(qb[i]), "v"(ka[i]), "v"(kb[i]));
 #pragma unroll
   for (int u = 0; u < VD; ++u) asm volatile("" ::"v"(vn[u]));
-#pragma unroll
-  for (int i = 0; i < KV4; ++i) {
-    const int f = int(threadIdx.x) + i * NT;
-    const int r = f / (HD / 4), c4 = f % (HD / 4);
-    *reinterpret_cast<float4 *>(&ks[r][4 * c4]) = kr[i];
-    *reinterpret_cast<float4 *>(&vs[r][4 * c4]) = vr[i];
-  }
-  const bool live = t0 <= pos;                      // chunk holds positions of the sequence
-  const bool own = pos / kAttnChunk == chunk;       // the chunk holds the new position
+  store_rows();   // the first chunk's rows
+  const bool live = t0 <= pos;                      // the unit holds positions of the sequence
+  const bool own = pos / UNIT == unit;              // the unit holds the new position
   const float pf = float(pos) / pos_div;
   // RoPE: pairs (d, d + HD/2) rotated by pf * freq[d] (embedding.cpp:36-75),
   // computed by every lane so that no load sinks into a branch
@@ -522,15 +539,41 @@ __global__ __launch_bounds__(512) void attn_kernel(const float *__restrict__ qkv
       }
     }
   }
-  __syncthreads();
+
+  float o[VD], m = -INFINITY, l = 0.0f;
+#pragma unroll
+  for (int u = 0; u < VD; ++u) o[u] = 0.0f;
+#pragma unroll
+  for (int q = 0; q < CPW; ++q) {
+    if (q > 0) {
+      __syncthreads();   // every wave is done with the previous chunk's rows
+      store_rows();
+    }
+    __syncthreads();
+    // the next chunk's rows stream in while this one is attended
+    if (q + 1 < CPW) load_rows(q + 1);
+    const int tq = t0 + q * kAttnChunk;
+    if (wave < group && tq <= pos) {   // chunk 0 of a live unit always holds positions
+      float mq, lq, oq[VD];
+      const bool ownq = pos / kAttnChunk == unit * CPW + q;   // the chunk holds the new position
+      chunk_attend<HD, (CPW > 1)>(ks, vs, qs[wave], knew, vn, pw[wave], tq, pos, ownq, scale, lane, mq, lq, oq);
+      if (q == 0) {
+        m = mq, l = lq;
+#pragma unroll
+        for (int u = 0; u < VD; ++u) o[u] = oq[u];
+      } else {   // both maxima finite: each chunk holds a position
+        const float M = fmaxf(m, mq), ra = expf(m - M), rb = expf(mq - M);
+        l = l * ra + lq * rb;
+#pragma unroll
+        for (int u = 0; u < VD; ++u) o[u] = o[u] * ra + oq[u] * rb;
+        m = M;
+      }
+    }
+  }
 
   if (wave < group) {
     const int head = kvh * group + wave;
-    float *dst = part + (size_t(head) * n_chunks + chunk) * (HD + 4);   // m, l, -, -, o[HD]
-    float o[VD], m = -INFINITY, l = 0.0f;
-#pragma unroll
-    for (int u = 0; u < VD; ++u) o[u] = 0.0f;
-    if (live) chunk_attend<HD>(ks, vs, qs[wave], knew, vn, pw[wave], t0, pos, own, scale, lane, m, l, o);
+    float *dst = part + (size_t(head) * n_chunks + unit) * (HD + 4);   // m, l, -, -, o[HD]
 #pragma unroll
     for (int u = 0; u < VD; ++u)
       __hip_atomic_store(dst + 4 + u * kWave + lane, o[u], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -548,11 +591,11 @@ __global__ __launch_bounds__(512) void attn_kernel(const float *__restrict__ qkv
     }
   }
   }   // !skip
-  // ---- ticket: the last of the KV head's live chunks merges ----
-  // Chunks past the position (skipped, or speculative ones that learn it
+  // ---- ticket: the last of the KV head's live units merges ----
+  // Units past the position (skipped, or speculative ones that learn it
   // only now) take no ticket, so they never delay the merge.
   if (t0 > pos) return;   // uniform over the workgroup
-  const int nlive = pos / kAttnChunk + 1;
+  const int nlive = pos / UNIT + 1;   // units holding positions
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (threadIdx.x == 0)
@@ -562,16 +605,15 @@ __global__ __launch_bounds__(512) void attn_kernel(const float *__restrict__ qkv
   if (wave < group) {
     const int head = kvh * group + wave;
     const float *ph = part + size_t(head) * n_chunks * (HD + 4);
-    const int nused = pos / kAttnChunk + 1;        // chunks holding positions
-    // Passes of 64 chunks (lane c holds chunk c0 + c) rescale a running
+    // Passes of 64 units (lane c holds unit c0 + c) rescale a running
     // maximum; the batch of o rows loaded with the weights is sized to the
-    // chunks in use (8 or 32).
+    // units in use (8 or 32).
     float M = -INFINITY, L = 0.0f, o[VD];
 #pragma unroll
     for (int u = 0; u < VD; ++u) o[u] = 0.0f;
     const auto ld = [ph](size_t i) { return __hip_atomic_load(ph + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
-    for (int c0 = 0; c0 < nused; c0 += kWave) {
-      const int nb = min(kWave, nused - c0);
+    for (int c0 = 0; c0 < nlive; c0 += kWave) {
+      const int nb = min(kWave, nlive - c0);
       if (nb <= 8)
         merge_pass<HD, 8>(ld, c0, nb, lane, M, L, o);
       else
@@ -623,6 +665,7 @@ struct lmx_decoder {
   // (LMX_ATTN_SPEC overrides; later chunks wait for the position and load
   // only when they hold positions).
   int spec_chunks = 8;
+  int n_cu = 256;   // compute units of the device (attention's chunks per workgroup)
   std::vector<void *> allocs;
   hipStream_t stream = nullptr;   // capture/replay stream of lmx_decoder_generate
 
@@ -729,16 +772,25 @@ int attention(lmx_decoder *d, size_t layer, hipStream_t st) {
   const size_t per_layer = size_t(nch) * kAttnChunk * c.n_kv_heads * c.head_dim;
   float *kc = d->kcache + layer * per_layer, *vc = d->vcache + layer * per_layer;
   const float scale = 1.0f / std::sqrt(float(c.head_dim));   // model.cpp:337
-  const dim3 grid(unsigned(c.n_kv_heads * nch), unsigned(d->batch));
+  // Two chunks per workgroup where one per chunk would exceed the two
+  // workgroups per CU that the LDS holds (LMX_ATTN_CPW = 1 or 2 overrides).
+  const char *cp = std::getenv("LMX_ATTN_CPW");
+  const size_t one = c.n_kv_heads * size_t(nch) * d->batch;
+  const int cpw = cp ? (std::atoi(cp) == 2 ? 2 : 1) : (one > 2 * size_t(d->n_cu) ? 2 : 1);
+  const int units = (nch + cpw - 1) / cpw, spec_units = (spec + cpw - 1) / cpw;
+  const dim3 grid(unsigned(c.n_kv_heads * units), unsigned(d->batch));
   const size_t qkv_stride = (c.n_heads + 2 * c.n_kv_heads) * c.head_dim;
-  if (c.head_dim == 64)
-    attn_kernel<64><<<grid, dim3(512), 0, st>>>(d->qkv, kc, vc, d->pos, d->freq, d->pos_div, int(c.n_heads),
-                                                int(c.n_kv_heads), group, int(c.max_seq), scale, d->attn_part, nch,
-                                                d->attn_tickets, d->attn_out, qkv_stride, d->kv_seq, spec);
-  else
-    attn_kernel<128><<<grid, dim3(512), 0, st>>>(d->qkv, kc, vc, d->pos, d->freq, d->pos_div, int(c.n_heads),
-                                                 int(c.n_kv_heads), group, int(c.max_seq), scale, d->attn_part, nch,
-                                                 d->attn_tickets, d->attn_out, qkv_stride, d->kv_seq, spec);
+#define LMX_ATTN(HD, CPW)                                                                                          \
+  attn_kernel<HD, CPW><<<grid, dim3(512), 0, st>>>(d->qkv, kc, vc, d->pos, d->freq, d->pos_div, int(c.n_heads),    \
+                                                   int(c.n_kv_heads), group, int(c.max_seq), scale, d->attn_part, \
+                                                   nch, d->attn_tickets, d->attn_out, qkv_stride, d->kv_seq,      \
+                                                   spec_units)
+  if (c.head_dim == 64) {
+    if (cpw == 2) LMX_ATTN(64, 2); else LMX_ATTN(64, 1);
+  } else {
+    if (cpw == 2) LMX_ATTN(128, 2); else LMX_ATTN(128, 1);
+  }
+#undef LMX_ATTN
   return launch_err("attention");
 }
 
@@ -1029,6 +1081,8 @@ int lmx_decoder_create_batched(const lmx_decoder_config *cfg, size_t batch, lmx_
   d->layers.resize(c.n_layers);
   d->pos_div = c.rope_mode == LMX_ROPE_REFERENCE ? c.rope_factor : 1.0f;
   if (const char *sp = std::getenv("LMX_ATTN_SPEC")) d->spec_chunks = std::max(1, std::atoi(sp));
+  if (hipDeviceGetAttribute(&d->n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || d->n_cu < 1)
+    d->n_cu = 256;
   const size_t qkv_rows = (c.n_heads + 2 * c.n_kv_heads) * c.head_dim;
   const size_t kv = c.n_layers * attn_chunks(c) * kAttnChunk * c.n_kv_heads * c.head_dim;   // whole chunks
   d->kv_seq = kv;

@@ -119,11 +119,14 @@ def test_decoder_silu_pair_epilogue(cuda, monkeypatch, ffn):
         assert rel_max_err(paired[pos], want) < DECODE_TOL, pos
 
 
+@pytest.mark.parametrize("cpw", ["1", "2"])
 @pytest.mark.parametrize("head_dim,n_heads,n_kv", [(64, 8, 2), (128, 12, 2)])
-def test_decoder_multi_chunk_context(cuda, head_dim, n_heads, n_kv):
+def test_decoder_multi_chunk_context(cuda, monkeypatch, head_dim, n_heads, n_kv, cpw):
     # 150 positions span three 64-position attention chunks (a fourth, empty,
     # chunk takes no ticket): the chunk merge of the attention kernel at every
-    # step, against the oracle's single-pass softmax.
+    # step, against the oracle's single-pass softmax; one chunk per workgroup,
+    # or two (LMX_ATTN_CPW=2: the second chunk of the second unit is empty).
+    monkeypatch.setenv("LMX_ATTN_CPW", cpw)
     cfg = D.small_config(hidden=512 if head_dim == 128 else 256, n_heads=n_heads, n_kv_heads=n_kv,
                          head_dim=head_dim, ffn=768, vocab=1200, max_seq=256, rope_mode=D.ROPE_REFERENCE,
                          rope_factor=1.0, rope_theta=1e6, qkv_bias=head_dim == 128)
@@ -417,6 +420,20 @@ def test_decoder_past_512_positions(cuda, monkeypatch, spec):
     check_positions(D.Decoder(m), oracle.OracleDecoder(m), toks, check_from=0)
 
 
+@pytest.mark.parametrize("head_dim,n_heads,n_kv", [(64, 8, 2), (128, 12, 2)])
+def test_attention_two_chunk_units_odd_cache(cuda, monkeypatch, head_dim, n_heads, n_kv):
+    # two chunks per workgroup over a 3-chunk cache: the second unit's second
+    # chunk lies past the cache (its loads are clamped to the last chunk, it
+    # holds no position), speculatively loaded from the first step on
+    monkeypatch.setenv("LMX_ATTN_CPW", "2")
+    cfg = D.small_config(hidden=512 if head_dim == 128 else 256, n_heads=n_heads, n_kv_heads=n_kv,
+                         head_dim=head_dim, ffn=768, vocab=700, max_seq=192, rope_mode=D.ROPE_REFERENCE,
+                         rope_factor=1.0, rope_theta=1e6, qkv_bias=head_dim == 128)
+    m = D.SyntheticModel(cfg, seed=63 + head_dim, group=128, random_norms=True)
+    toks = np.random.default_rng(64).integers(0, cfg.vocab, 190)
+    check_positions(D.Decoder(m), oracle.OracleDecoder(m), toks, check_from=0)
+
+
 def test_decoder_past_4096_positions(cuda):
     # 4112 positions = 65 chunks: two passes of the merge (64 chunks, then 1)
     cfg = qwen_small(n_heads=4, n_kv_heads=2, vocab=256, max_seq=4160)
@@ -425,9 +442,13 @@ def test_decoder_past_4096_positions(cuda):
     check_positions(D.Decoder(m), oracle.OracleDecoder(m), toks, check_from=4030)
 
 
-def test_batched_decoder_batch16_past_512(cuda):
+@pytest.mark.parametrize("cpw", [None, "2"])
+def test_batched_decoder_batch16_past_512(cuda, monkeypatch, cpw):
     # batch 16 = one full group of the batched GEMV, with the attention of every
-    # sequence past 512 positions (32-chunk merge)
+    # sequence past 512 positions (32-chunk merge); one chunk per workgroup
+    # (the automatic choice at this cache size) or two (5 units over 9 chunks)
+    if cpw is not None:
+        monkeypatch.setenv("LMX_ATTN_CPW", cpw)
     cfg = qwen_small(max_seq=576)
     m = D.SyntheticModel(cfg, seed=55, group=128, random_norms=True)
     B, n = 16, 530
