@@ -131,6 +131,8 @@ __global__ __launch_bounds__(256) void silu_mul_rows_kernel(const float *__restr
 }
 
 constexpr int kArgmaxParts = 32;   // most workgroups per logits row
+constexpr int kAttnMaxSplit = 8;   // most workgroups sharing one KV head's query heads
+constexpr int kTicketPad = 32;     // unsigneds per ticket (attention, greedy pick): one 128-byte line each
 
 // Greedy token of every sequence: the first maximum of its logits row
 // (model.cpp:480-490); written unless the next position is forced.  Each
@@ -187,14 +189,15 @@ __global__ __launch_bounds__(1024) void argmax_rows_kernel(const float *__restri
   if (parts > 1) {
     __hip_atomic_store(slots + size_t(b) * parts + part, key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __builtin_amdgcn_s_waitcnt(0);
-    const unsigned t = __hip_atomic_fetch_add(seq_tickets + b, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const unsigned t =
+        __hip_atomic_fetch_add(seq_tickets + b * kTicketPad, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (t != unsigned(parts - 1)) return;   // another part finishes the sequence
     for (int q = 0; q < parts; ++q) {
       const unsigned long long k =
           __hip_atomic_load(slots + size_t(b) * parts + q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       key = k > key ? k : key;
     }
-    __hip_atomic_store(seq_tickets + b, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(seq_tickets + b * kTicketPad, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   const int idx = key ? int(0xFFFFFFFFu - uint32_t(key)) : 0;
   const int pos = *pos_p;
@@ -368,7 +371,8 @@ __device__ __forceinline__ void chunk_attend(const float (*ks)[HD + 4], const fl
   if (valid) {
     const float *kv = lane == jnew ? knew : ks[lane];
     float acc = 0.0f;
-#pragma unroll(LEAN ? 8 : HD / 4)
+    constexpr int kUnrollD = LEAN ? 8 : HD / 4;
+#pragma unroll kUnrollD
     for (int d4 = 0; d4 < HD / 4; ++d4) {
       const float4 k4 = *reinterpret_cast<const float4 *>(kv + 4 * d4);
       const float4 q4 = *reinterpret_cast<const float4 *>(qrow + 4 * d4);
@@ -390,7 +394,8 @@ __device__ __forceinline__ void chunk_attend(const float (*ks)[HD + 4], const fl
   for (int u = 0; u < VD; ++u) {
     const int d = u * kWave + lane;
     float s8[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-#pragma unroll(LEAN ? 16 : kAttnChunk)
+    constexpr int kUnrollJ = LEAN ? 16 : kAttnChunk;
+#pragma unroll kUnrollJ
     for (int j = 0; j < kAttnChunk; ++j) s8[j % 8] += pwrow[j] * vs[j][d];
     o[u] = ((s8[0] + s8[1]) + (s8[2] + s8[3])) + ((s8[4] + s8[5]) + (s8[6] + s8[7]));
     if (own) o[u] += enew * vn[u];
@@ -398,24 +403,26 @@ __device__ __forceinline__ void chunk_attend(const float (*ks)[HD + 4], const fl
 }
 
 // Attention with the chunk merge inside: one workgroup per (KV head, CPW
-// consecutive 64-position chunks, a "unit"), 8 waves.  All 8 waves first
-// request the first chunk's cached K and V rows of the KV head (every row is
-// in bounds: the cache holds whole chunks), so a chunk costs one memory round
+// consecutive 64-position chunks, a "unit", part hs of hsplit of the KV
+// head's query heads), 8 waves.  All 8 waves first request the first
+// chunk's cached K and V rows of the KV head (every row is in bounds: the
+// cache holds whole chunks), so a chunk costs one memory round
 // trip whatever the head dimension (a second chunk's rows are requested
 // when the first's are in LDS, and arrive while it is attended); chunk by
-// chunk the rows pass through LDS and wave w < group serves query head
-// kvh*group + w: RoPE of q (and of the new key in the chunk holding the
-// position), scores, a partial softmax and the weighted V sum of the chunk
-// (model.cpp:326-372, attention.cpp:23-42);
+// chunk the rows pass through LDS and wave w < group/hsplit serves query
+// head kvh*group + hs*group/hsplit + w: RoPE of q (and of the new key in
+// the chunk holding the position), scores, a partial softmax and the
+// weighted V sum of the chunk (model.cpp:326-372, attention.cpp:23-42);
 // the unit's chunks combine as (m, l, o[HD]) with the larger maximum.  The
-// last workgroup of the KV head to finish (a device-scope ticket, the
-// split-K handoff of the GEMV) merges the units up to the position in order,
+// last workgroup of the KV head's part hs to finish (a device-scope ticket,
+// the split-K handoff of the GEMV) merges the units up to the position in order,
 // x = sum_u e^(m_u - M) o_u / sum_u e^(m_u - M) l_u with M = max_u m_u, and
 // writes the heads' attention output, so the o-projection is a plain GEMV.
 // Partials and tickets travel as device-scope relaxed atomics (no L2
 // writeback needed); the merging workgroup clears the ticket for the next
 // step.  CPW = 2 halves the workgroups where one per chunk would not all be
-// resident at once (two workgroups per CU by their LDS).
+// resident at once (two workgroups per CU by their LDS); hsplit > 1 spreads
+// a small grid's per-head work over more CUs (each part loads the rows).
 // Cost follows the position, not the cache capacity (the reference loops
 // to pos only, model.cpp:344-372): units below spec_units load their rows
 // speculatively, before the position is known; later units read the
@@ -428,7 +435,8 @@ __global__ __launch_bounds__(512) void attn_kernel(const float *__restrict__ qkv
                                                    int n_kv, int group, int max_seq, float scale,
                                                    float *__restrict__ part, int n_chunks,
                                                    unsigned *__restrict__ tickets, float *__restrict__ out,
-                                                   size_t qkv_stride, size_t kv_stride, int spec_units) {
+                                                   size_t qkv_stride, size_t kv_stride, int spec_units,
+                                                   int hsplit) {
   constexpr int VD = HD / kWave;          // value columns per lane
   constexpr int NT = 512;
   constexpr int KV4 = kAttnChunk * HD / 4 / NT;   // float4 of K (and of V) per thread and chunk
@@ -448,11 +456,14 @@ __global__ __launch_bounds__(512) void attn_kernel(const float *__restrict__ qkv
     kc += b * kv_stride;
     vc += b * kv_stride;
     part += b * size_t(n_heads) * n_chunks * (HD + 4);
-    tickets += b * n_kv;
+    tickets += b * n_kv * kAttnMaxSplit * kTicketPad;
     out += b * size_t(n_heads) * HD;
   }
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
-  const int kvh = blockIdx.x % n_kv, unit = blockIdx.x / n_kv;
+  // part hs of hsplit of the KV head's query heads: hpw heads from h0
+  const int hs = blockIdx.x % hsplit, kvu = blockIdx.x / hsplit;
+  const int kvh = kvu % n_kv, unit = kvu / n_kv;
+  const int hpw = group / hsplit, h0 = kvh * group + hs * hpw;
   const size_t row = size_t(n_kv) * HD;
   const int t0 = unit * UNIT;
   const float *kin = qkv + size_t(n_heads) * HD + kvh * HD;
@@ -494,7 +505,7 @@ __global__ __launch_bounds__(512) void attn_kernel(const float *__restrict__ qkv
       *reinterpret_cast<float4 *>(&vs[r][4 * c4]) = vr[i];
     }
   };
-  const float *qin = qkv + size_t(kvh * group + (wave < group ? wave : 0)) * HD;
+  const float *qin = qkv + size_t(h0 + (wave < hpw ? wave : 0)) * HD;
   float qa[RP], qb[RP], ka[RP], kb[RP], fr[RP], vn[VD];
 #pragma unroll
   for (int i = 0; i < RP; ++i) {
@@ -530,7 +541,7 @@ __global__ __launch_bounds__(512) void attn_kernel(const float *__restrict__ qkv
     sincosf(pf * fr[i], &sn, &cs);
     const float q0 = qa[i] * cs - qb[i] * sn, q1 = qa[i] * sn + qb[i] * cs;
     const float k0 = ka[i] * cs - kb[i] * sn, k1 = ka[i] * sn + kb[i] * cs;
-    if (live && wave < group && d < HALF) {
+    if (live && wave < hpw && d < HALF) {
       qs[wave][d] = q0;
       qs[wave][d + HALF] = q1;
       if (own && wave == 0) {
@@ -553,7 +564,7 @@ __global__ __launch_bounds__(512) void attn_kernel(const float *__restrict__ qkv
     // the next chunk's rows stream in while this one is attended
     if (q + 1 < CPW) load_rows(q + 1);
     const int tq = t0 + q * kAttnChunk;
-    if (wave < group && tq <= pos) {   // chunk 0 of a live unit always holds positions
+    if (wave < hpw && tq <= pos) {   // chunk 0 of a live unit always holds positions
       float mq, lq, oq[VD];
       const bool ownq = pos / kAttnChunk == unit * CPW + q;   // the chunk holds the new position
       chunk_attend<HD, (CPW > 1)>(ks, vs, qs[wave], knew, vn, pw[wave], tq, pos, ownq, scale, lane, mq, lq, oq);
@@ -571,8 +582,8 @@ __global__ __launch_bounds__(512) void attn_kernel(const float *__restrict__ qkv
     }
   }
 
-  if (wave < group) {
-    const int head = kvh * group + wave;
+  if (wave < hpw) {
+    const int head = h0 + wave;
     float *dst = part + (size_t(head) * n_chunks + unit) * (HD + 4);   // m, l, -, -, o[HD]
 #pragma unroll
     for (int u = 0; u < VD; ++u)
@@ -581,7 +592,7 @@ __global__ __launch_bounds__(512) void attn_kernel(const float *__restrict__ qkv
       __hip_atomic_store(dst, m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       __hip_atomic_store(dst + 1, l, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    if (own && wave == 0) {   // append the new position to the cache
+    if (own && wave == 0 && hs == 0) {   // append the new position to the cache
 #pragma unroll
       for (int u = 0; u < VD; ++u) {
         const int d = u * kWave + lane;
@@ -599,11 +610,12 @@ __global__ __launch_bounds__(512) void attn_kernel(const float *__restrict__ qkv
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (threadIdx.x == 0)
-    ticket = __hip_atomic_fetch_add(tickets + kvh, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    ticket = __hip_atomic_fetch_add(tickets + (kvh * kAttnMaxSplit + hs) * kTicketPad, 1u, __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_AGENT);
   __syncthreads();
   if (ticket != unsigned(nlive - 1)) return;   // uniform over the workgroup
-  if (wave < group) {
-    const int head = kvh * group + wave;
+  if (wave < hpw) {
+    const int head = h0 + wave;
     const float *ph = part + size_t(head) * n_chunks * (HD + 4);
     // Passes of 64 units (lane c holds unit c0 + c) rescale a running
     // maximum; the batch of o rows loaded with the weights is sized to the
@@ -623,7 +635,9 @@ __global__ __launch_bounds__(512) void attn_kernel(const float *__restrict__ qkv
 #pragma unroll
     for (int u = 0; u < VD; ++u) out[size_t(head) * HD + u * kWave + lane] = o[u] * inv;
   }
-  if (threadIdx.x == 0) __hip_atomic_store(tickets + kvh, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (threadIdx.x == 0)
+    __hip_atomic_store(tickets + (kvh * kAttnMaxSplit + hs) * kTicketPad, 0u, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
 }
 
 size_t attn_chunks(const lmx_decoder_config &c) { return (c.max_seq + kAttnChunk - 1) / kAttnChunk; }
@@ -648,12 +662,12 @@ struct lmx_decoder {
   float *kcache = nullptr, *vcache = nullptr, *freq = nullptr;
   float *attn_part = nullptr;            // [n_heads][chunks][m, l, -, -, o[head_dim]]
   float *attn_out = nullptr;             // [n_heads * head_dim] merged attention output
-  unsigned *attn_tickets = nullptr;      // [n_kv_heads] chunk tickets (zero between steps)
+  unsigned *attn_tickets = nullptr;      // [n_kv_heads][kAttnMaxSplit] unit tickets (zero between steps)
   float *normed = nullptr;   // batch > 1: RMSNorm output [hidden] rows
   float *act = nullptr;      // SiLU(gate)*up [ffn] rows
   unsigned *argmax_ticket = nullptr;         // batch > 1: argmax_rows_kernel's ticket
   unsigned long long *argmax_slots = nullptr;   // batch > 1: [batch][kArgmaxParts] keys
-  unsigned *argmax_seq_tickets = nullptr;       // batch > 1: [batch] tickets
+  unsigned *argmax_seq_tickets = nullptr;       // batch > 1: [batch] tickets, one 128-byte line each
   size_t kv_seq = 0;                         // floats of one sequence's K (or V) cache, all layers
   unsigned long long *amax = nullptr;    // per-wave argmax keys of the head GEMV
   size_t amax_slots = 0;
@@ -778,13 +792,24 @@ int attention(lmx_decoder *d, size_t layer, hipStream_t st) {
   const size_t one = c.n_kv_heads * size_t(nch) * d->batch;
   const int cpw = cp ? (std::atoi(cp) == 2 ? 2 : 1) : (one > 2 * size_t(d->n_cu) ? 2 : 1);
   const int units = (nch + cpw - 1) / cpw, spec_units = (spec + cpw - 1) / cpw;
-  const dim3 grid(unsigned(c.n_kv_heads * units), unsigned(d->batch));
+  // The KV head's query heads split over two workgroups (each loads the
+  // unit's rows) where that keeps the grid within one workgroup per CU
+  // (LMX_ATTN_HS overrides: a divisor of the group, at most 8).
+  int hsplit = 1;
+  const size_t wgs = c.n_kv_heads * size_t(units) * d->batch;
+  if (const char *hv = std::getenv("LMX_ATTN_HS")) {
+    const int v = std::atoi(hv);
+    if (v >= 1 && v <= kAttnMaxSplit && group % v == 0) hsplit = v;
+  } else if (group % 2 == 0 && wgs * 2 <= size_t(d->n_cu)) {
+    hsplit = 2;
+  }
+  const dim3 grid(unsigned(c.n_kv_heads * units * hsplit), unsigned(d->batch));
   const size_t qkv_stride = (c.n_heads + 2 * c.n_kv_heads) * c.head_dim;
 #define LMX_ATTN(HD, CPW)                                                                                          \
   attn_kernel<HD, CPW><<<grid, dim3(512), 0, st>>>(d->qkv, kc, vc, d->pos, d->freq, d->pos_div, int(c.n_heads),    \
                                                    int(c.n_kv_heads), group, int(c.max_seq), scale, d->attn_part, \
                                                    nch, d->attn_tickets, d->attn_out, qkv_stride, d->kv_seq,      \
-                                                   spec_units)
+                                                   spec_units, hsplit)
   if (c.head_dim == 64) {
     if (cpw == 2) LMX_ATTN(64, 2); else LMX_ATTN(64, 1);
   } else {
@@ -1100,12 +1125,14 @@ int lmx_decoder_create_batched(const lmx_decoder_config *cfg, size_t batch, lmx_
       (st = d->alloc(reinterpret_cast<void **>(&d->attn_part),
                      B * c.n_heads * attn_chunks(c) * (c.head_dim + 4) * sizeof(float))) ||
       (st = d->alloc(reinterpret_cast<void **>(&d->attn_out), B * c.n_heads * c.head_dim * sizeof(float))) ||
-      (st = d->alloc(reinterpret_cast<void **>(&d->attn_tickets), B * c.n_kv_heads * sizeof(unsigned))) ||
+      (st = d->alloc(reinterpret_cast<void **>(&d->attn_tickets),
+                     B * c.n_kv_heads * kAttnMaxSplit * kTicketPad * sizeof(unsigned))) ||
       (B > 1 && (st = d->alloc(reinterpret_cast<void **>(&d->normed), B * c.hidden * 4))) ||
       (st = d->alloc(reinterpret_cast<void **>(&d->act), B * c.ffn * 4)) ||
       (B > 1 && (st = d->alloc(reinterpret_cast<void **>(&d->argmax_ticket), sizeof(unsigned)))) ||
       (B > 1 && (st = d->alloc(reinterpret_cast<void **>(&d->argmax_slots), B * kArgmaxParts * 8))) ||
-      (B > 1 && (st = d->alloc(reinterpret_cast<void **>(&d->argmax_seq_tickets), B * sizeof(unsigned)))) ||
+      (B > 1 && (st = d->alloc(reinterpret_cast<void **>(&d->argmax_seq_tickets),
+                               B * kTicketPad * sizeof(unsigned)))) ||
       (st = upload(d, &d->freq, fr.data(), fr.size()))) {
     delete d;
     return st;

@@ -119,14 +119,19 @@ def test_decoder_silu_pair_epilogue(cuda, monkeypatch, ffn):
         assert rel_max_err(paired[pos], want) < DECODE_TOL, pos
 
 
+@pytest.mark.parametrize("hs", [None, "1", "group"])
 @pytest.mark.parametrize("cpw", ["1", "2"])
 @pytest.mark.parametrize("head_dim,n_heads,n_kv", [(64, 8, 2), (128, 12, 2)])
-def test_decoder_multi_chunk_context(cuda, monkeypatch, head_dim, n_heads, n_kv, cpw):
+def test_decoder_multi_chunk_context(cuda, monkeypatch, head_dim, n_heads, n_kv, cpw, hs):
     # 150 positions span three 64-position attention chunks (a fourth, empty,
     # chunk takes no ticket): the chunk merge of the attention kernel at every
     # step, against the oracle's single-pass softmax; one chunk per workgroup,
-    # or two (LMX_ATTN_CPW=2: the second chunk of the second unit is empty).
+    # or two (LMX_ATTN_CPW=2: the second chunk of the second unit is empty);
+    # a KV head's query heads in the automatic number of workgroups, in one,
+    # or one head per workgroup (LMX_ATTN_HS)
     monkeypatch.setenv("LMX_ATTN_CPW", cpw)
+    if hs is not None:
+        monkeypatch.setenv("LMX_ATTN_HS", str(n_heads // n_kv) if hs == "group" else hs)
     cfg = D.small_config(hidden=512 if head_dim == 128 else 256, n_heads=n_heads, n_kv_heads=n_kv,
                          head_dim=head_dim, ffn=768, vocab=1200, max_seq=256, rope_mode=D.ROPE_REFERENCE,
                          rope_factor=1.0, rope_theta=1e6, qkv_bias=head_dim == 128)
