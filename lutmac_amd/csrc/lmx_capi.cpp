@@ -287,7 +287,7 @@ int gemv_batched(const lmx_weight *w, GemvArgs a, const float *x, float *y, size
     a.resid = resid ? resid + *done * w->rows : nullptr;
     a.cols = int(w->cols);
     a.partials = w->d_bpartials;
-    if (nb == 4 && a.epi != kEpiNormOut) {   // one full-K launch where the plan allows
+    if (nb == 4 && a.epi != kEpiNormOut && a.epi != kEpiPartials) {   // one full-K launch where the plan allows
       const int q = launch_gemv_quad(w->format, a, stream);
       if (q != 1) {
         if (q) return q;
@@ -306,6 +306,7 @@ bool batched_epilogue_ok(const lmx_weight *w, int epi, size_t batch) {
   if (!w->batched || batch < 4 || batch % 4 || w->cols % 4) return false;   // every vector in a group of 16/8/4
   if (epi == kEpiSiluPair) return w->rows % 8 == 0;
   if (epi == kEpiNormOut) return w->rows <= size_t(kNormOutMaxRows);
+  if (epi == kEpiPartials) return batch == 4 || batch == 8 || batch == 16;   // one group: one set of partials
   return epi == kEpiStore;
 }
 

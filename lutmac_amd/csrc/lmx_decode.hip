@@ -133,6 +133,7 @@ __global__ __launch_bounds__(256) void silu_mul_rows_kernel(const float *__restr
 constexpr int kArgmaxParts = 32;   // most workgroups per logits row
 constexpr int kAttnMaxSplit = 8;   // most workgroups sharing one KV head's query heads
 constexpr int kTicketPad = 32;     // unsigneds per ticket (attention, greedy pick): one 128-byte line each
+constexpr int kAttnMaxParts = 16;  // most q|k|v split partials attention sums itself
 
 // Greedy token of every sequence: the first maximum of its logits row
 // (model.cpp:480-490); written unless the next position is forced.  Each
@@ -428,15 +429,21 @@ __device__ __forceinline__ void chunk_attend(const float (*ks)[HD + 4], const fl
 // speculatively, before the position is known; later units read the
 // position first and, when it lies before them, load nothing and take no
 // ticket (the merge reads units up to the position only).
-template <int HD, int CPW>
-__global__ __launch_bounds__(512) void attn_kernel(const float *__restrict__ qkv, float *__restrict__ kc,
+// PARTS: the q|k|v rows arrive as the batched GEMV's split partials
+// qparts [batch][qsplits][qnpad] (no reduction launch before attention); the
+// workgroup sums the rows it needs in split order (+ qbias), exactly as the
+// batched reduction would, into LDS, loading them in the same round trip as
+// the unit's K and V rows.
+template <int HD, int CPW, bool PARTS>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void attn_kernel(const float *__restrict__ qkv, float *__restrict__ kc,
                                                    float *__restrict__ vc, const int *__restrict__ pos_p,
                                                    const float *__restrict__ freq, float pos_div, int n_heads,
                                                    int n_kv, int group, int max_seq, float scale,
                                                    float *__restrict__ part, int n_chunks,
                                                    unsigned *__restrict__ tickets, float *__restrict__ out,
                                                    size_t qkv_stride, size_t kv_stride, int spec_units,
-                                                   int hsplit) {
+                                                   int hsplit, const float *__restrict__ qparts, int qsplits,
+                                                   int qnpad, const float *__restrict__ qbias) {
   constexpr int VD = HD / kWave;          // value columns per lane
   constexpr int NT = 512;
   constexpr int KV4 = kAttnChunk * HD / 4 / NT;   // float4 of K (and of V) per thread and chunk
@@ -447,12 +454,14 @@ __global__ __launch_bounds__(512) void attn_kernel(const float *__restrict__ qkv
   __shared__ float qs[8][HD];
   __shared__ float pw[8][kAttnChunk];
   __shared__ float knew[HD];
+  __shared__ float qkvb[PARTS ? (8 + 2) * HD : 1];   // PARTS: the summed q (up to 8 heads), k and v rows
   __shared__ unsigned ticket;
   {
     // sequence blockIdx.y of a batch: its q|k|v row, KV cache, partials,
     // tickets and output (the position is shared)
     const size_t b = blockIdx.y;
     qkv += b * qkv_stride;
+    if constexpr (PARTS) qparts += b * size_t(qsplits) * size_t(qnpad);
     kc += b * kv_stride;
     vc += b * kv_stride;
     part += b * size_t(n_heads) * n_chunks * (HD + 4);
@@ -507,28 +516,86 @@ __global__ __launch_bounds__(512) void attn_kernel(const float *__restrict__ qkv
   };
   const float *qin = qkv + size_t(h0 + (wave < hpw ? wave : 0)) * HD;
   float qa[RP], qb[RP], ka[RP], kb[RP], fr[RP], vn[VD];
+  // PARTS: value i < nval of the workgroup's q (hpw heads), k, v rows; thread
+  // t sums values t, t + NT, ... (VPT of them) over the splits
+  constexpr int VPT = PARTS ? ((8 + 2) * HD + NT - 1) / NT : 1;
+  constexpr int NP = PARTS ? kAttnMaxParts : 1;
+  const int nq = hpw * HD, nval = nq + 2 * HD;
+  const auto qkv_row = [&](int i) {   // value i -> its row of the fused q|k|v output
+    return i < nq ? h0 * HD + i : i < nq + HD ? (n_heads + kvh) * HD + (i - nq) : (n_heads + n_kv + kvh) * HD + (i - nq - HD);
+  };
+  float pv[VPT][NP], pb[VPT];
+  if constexpr (PARTS) {
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+      const int r = qkv_row(min(int(threadIdx.x) + j * NT, nval - 1));
+#pragma unroll
+      for (int t = 0; t < NP; ++t) pv[j][t] = t < qsplits ? qparts[size_t(t) * qnpad + r] : 0.0f;
+      pb[j] = qbias ? qbias[r] : 0.0f;
+    }
+  }
 #pragma unroll
   for (int i = 0; i < RP; ++i) {
     const int d = min(lane + i * kWave, HALF - 1);
     fr[i] = freq[d];
-    qa[i] = qin[d];
-    qb[i] = qin[d + HALF];
-    ka[i] = kin[d];
-    kb[i] = kin[d + HALF];
+    if constexpr (!PARTS) {
+      qa[i] = qin[d];
+      qb[i] = qin[d + HALF];
+      ka[i] = kin[d];
+      kb[i] = kin[d + HALF];
+    }
   }
+  if constexpr (!PARTS) {
 #pragma unroll
-  for (int u = 0; u < VD; ++u) vn[u] = vin[u * kWave + lane];
+    for (int u = 0; u < VD; ++u) vn[u] = vin[u * kWave + lane];
+  }
   // One wait for all of them: without a use of every loaded value here the
   // compiler issues the small loads after the K/V waits (a second round trip).
 #pragma unroll
   for (int i = 0; i < KV4; ++i)
     asm volatile("" ::"v"(kr[i].x), "v"(kr[i].y), "v"(kr[i].z), "v"(kr[i].w), "v"(vr[i].x), "v"(vr[i].y),
                  "v"(vr[i].z), "v"(vr[i].w));
+  if constexpr (PARTS) {
 #pragma unroll
-  for (int i = 0; i < RP; ++i) asm volatile("" ::"v"(fr[i]), "v"(qa[i]), "v"(qb[i]), "v"(ka[i]), "v"(kb[i]));
+    for (int i = 0; i < RP; ++i) asm volatile("" ::"v"(fr[i]));
 #pragma unroll
-  for (int u = 0; u < VD; ++u) asm volatile("" ::"v"(vn[u]));
+    for (int j = 0; j < VPT; ++j) {
+#pragma unroll
+      for (int t = 0; t < NP; ++t) asm volatile("" ::"v"(pv[j][t]));
+      asm volatile("" ::"v"(pb[j]));
+    }
+    // split-order sums (+ bias), the batched reduction's expression: one
+    // round of 16 partials from zero, absent splits adding +0
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+      const int i = int(threadIdx.x) + j * NT;
+      float sum = 0.0f;
+#pragma unroll
+      for (int t = 0; t < NP; ++t) sum += pv[j][t];
+      if (qbias) sum += pb[j];
+      if (i < nval) qkvb[i] = sum;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < RP; ++i) asm volatile("" ::"v"(fr[i]), "v"(qa[i]), "v"(qb[i]), "v"(ka[i]), "v"(kb[i]));
+#pragma unroll
+    for (int u = 0; u < VD; ++u) asm volatile("" ::"v"(vn[u]));
+  }
   store_rows();   // the first chunk's rows
+  if constexpr (PARTS) {
+    __syncthreads();   // the summed rows are in qkvb
+    const float *qsrc = qkvb + (wave < hpw ? wave : 0) * HD;
+#pragma unroll
+    for (int i = 0; i < RP; ++i) {
+      const int d = min(lane + i * kWave, HALF - 1);
+      qa[i] = qsrc[d];
+      qb[i] = qsrc[d + HALF];
+      ka[i] = qkvb[nq + d];
+      kb[i] = qkvb[nq + d + HALF];
+    }
+#pragma unroll
+    for (int u = 0; u < VD; ++u) vn[u] = qkvb[nq + HD + u * kWave + lane];
+  }
   const bool live = t0 <= pos;                      // the unit holds positions of the sequence
   const bool own = pos / UNIT == unit;              // the unit holds the new position
   const float pf = float(pos) / pos_div;
@@ -778,7 +845,11 @@ int finish_embed(const lmx_decoder *d, hipStream_t st) {
   return launch_err("finish_embed");
 }
 
-int attention(lmx_decoder *d, size_t layer, hipStream_t st) {
+// qparts: the q|k|v rows as the batched GEMV's split partials
+// [batch][qsplits][qnpad] (kEpiPartials) with the q|k|v bias qbias, summed by
+// the attention kernel itself; nullptr: the rows are in d->qkv.
+int attention(lmx_decoder *d, size_t layer, hipStream_t st, const float *qparts = nullptr, int qsplits = 0,
+              int qnpad = 0, const float *qbias = nullptr) {
   const lmx_decoder_config &c = d->cfg;
   const int group = int(c.n_heads / c.n_kv_heads);
   const int nch = int(attn_chunks(c));
@@ -805,15 +876,23 @@ int attention(lmx_decoder *d, size_t layer, hipStream_t st) {
   }
   const dim3 grid(unsigned(c.n_kv_heads * units * hsplit), unsigned(d->batch));
   const size_t qkv_stride = (c.n_heads + 2 * c.n_kv_heads) * c.head_dim;
-#define LMX_ATTN(HD, CPW)                                                                                          \
-  attn_kernel<HD, CPW><<<grid, dim3(512), 0, st>>>(d->qkv, kc, vc, d->pos, d->freq, d->pos_div, int(c.n_heads),    \
-                                                   int(c.n_kv_heads), group, int(c.max_seq), scale, d->attn_part, \
-                                                   nch, d->attn_tickets, d->attn_out, qkv_stride, d->kv_seq,      \
-                                                   spec_units, hsplit)
-  if (c.head_dim == 64) {
-    if (cpw == 2) LMX_ATTN(64, 2); else LMX_ATTN(64, 1);
+  if (qparts && (qsplits < 1 || qsplits > kAttnMaxParts || qnpad < int(qkv_stride)))
+    return fail(LMX_ERR_INVALID_ARGUMENT, "attention over %d q|k|v partials of %d rows", qsplits, qnpad);
+#define LMX_ATTN(HD, CPW, PARTS)                                                                                    \
+  attn_kernel<HD, CPW, PARTS><<<grid, dim3(512), 0, st>>>(                                                         \
+      d->qkv, kc, vc, d->pos, d->freq, d->pos_div, int(c.n_heads), int(c.n_kv_heads), group, int(c.max_seq), scale, \
+      d->attn_part, nch, d->attn_tickets, d->attn_out, qkv_stride, d->kv_seq, spec_units, hsplit, qparts, qsplits,  \
+      qnpad, qbias)
+  if (qparts) {
+    if (c.head_dim == 64) {
+      if (cpw == 2) LMX_ATTN(64, 2, true); else LMX_ATTN(64, 1, true);
+    } else {
+      if (cpw == 2) LMX_ATTN(128, 2, true); else LMX_ATTN(128, 1, true);
+    }
+  } else if (c.head_dim == 64) {
+    if (cpw == 2) LMX_ATTN(64, 2, false); else LMX_ATTN(64, 1, false);
   } else {
-    if (cpw == 2) LMX_ATTN(128, 2); else LMX_ATTN(128, 1);
+    if (cpw == 2) LMX_ATTN(128, 2, false); else LMX_ATTN(128, 1, false);
   }
 #undef LMX_ATTN
   return launch_err("attention");
@@ -891,6 +970,16 @@ bool rows_fuse(const lmx_decoder *d) {
   return true;
 }
 
+// Whether a layer's qkv projection leaves its split partials to attention
+// (kEpiPartials): the decoder's rows are one batched group whose splits the
+// attention kernel sums (LMX_QKV_PARTS=0: never; the batched reduction then
+// writes the rows first).
+bool qkv_parts(const lmx_decoder *d, const lmx_weight *qkv) {
+  const char *e = std::getenv("LMX_QKV_PARTS");
+  return !(e && std::atoi(e) == 0) && batched_epilogue_ok(qkv, kEpiPartials, d->batch) &&
+         batched_launch_splits(qkv->Npad, qkv->Kp) <= kAttnMaxParts;
+}
+
 int rmsnorm_rows(const lmx_decoder *d, const float *x, const float *wt, float *y, hipStream_t st) {
   rmsnorm_rows_kernel<<<dim3(unsigned(d->batch)), dim3(256), 0, st>>>(x, wt, int(d->cfg.hidden), d->cfg.rms_eps, y);
   return launch_err("rmsnorm_rows");
@@ -966,8 +1055,16 @@ int step_batched(lmx_decoder *d, float *logits_out, hipStream_t st) {
     for (size_t l = 0; l < c.n_layers; ++l) {
       const lmx_decoder::Layer &L = d->layers[l];
       const float *next_norm = l + 1 < c.n_layers ? d->layers[l + 1].in_norm : d->final_norm;
-      if ((r = gemv_rows(d, L.qkv, d->normed, d->qkv, L.qkv_bias, nullptr, st)) || (r = attention(d, l, st)) ||
-          (r = gemv_rows_epi(d, L.o, d->attn_out, d->hidden, d->hidden, kEpiNormOut, L.post_norm, d->normed, st)) ||
+      if (qkv_parts(d, L.qkv)) {
+        // the qkv split sums go straight to attention (no reduction launch)
+        if ((r = gemv_rows_epi(d, L.qkv, d->normed, d->qkv, nullptr, kEpiPartials, nullptr, nullptr, st)) ||
+            (r = attention(d, l, st, L.qkv->d_bpartials, batched_launch_splits(L.qkv->Npad, L.qkv->Kp),
+                           int(L.qkv->Npad), L.qkv_bias)))
+          return r;
+      } else if ((r = gemv_rows(d, L.qkv, d->normed, d->qkv, L.qkv_bias, nullptr, st)) || (r = attention(d, l, st))) {
+        return r;
+      }
+      if ((r = gemv_rows_epi(d, L.o, d->attn_out, d->hidden, d->hidden, kEpiNormOut, L.post_norm, d->normed, st)) ||
           (r = gemv_rows_epi(d, L.gate_up, d->normed, d->act, nullptr, kEpiSiluPair, nullptr, nullptr, st)) ||
           (r = gemv_rows_epi(d, L.down, d->act, d->hidden, d->hidden, kEpiNormOut, next_norm, d->normed, st)))
         return r;

@@ -80,9 +80,15 @@ struct GemvArgs {
 //   kEpiNormOut:   (batched GEMV) y as kEpiStore (+ resid), and y2 = the
 //                  RMSNorm of each y row with weight xw and epsilon eps
 //                  (norm.cpp:18-34), the next linear's input
+//   kEpiPartials:  (batched GEMV, exactly one group of 4/8/16 vectors) no
+//                  reduction: the split sums stay in a.partials
+//                  [nb][splits][Npad] (batched_launch_splits of them) for a
+//                  consumer that sums them in split order itself (the decode
+//                  attention reads its q/k/v rows that way)
 constexpr int kEpiStore = 0;
 constexpr int kEpiSiluPair = 1;
 constexpr int kEpiNormOut = 2;
+constexpr int kEpiPartials = 3;
 constexpr int kNormOutMaxRows = 8192;   // kEpiNormOut keeps a whole row in LDS
 
 // Activation transforms applied while the tables are built:
@@ -175,6 +181,9 @@ inline size_t batched_slice_splits(size_t Npad, size_t Kp) {
   const size_t s256 = Kp / kRotChunk;
   return (Npad / kWave) * s256 < kBatchMinGrid128 ? 2 * s256 : s256;
 }
+// The k-slices a batched launch actually uses: batched_slice_splits, or the
+// 256-wide ones when LMX_BATCH_S128=0 turns the 128-wide slices off.
+int batched_launch_splits(size_t Npad, size_t Kp);
 
 // Exactly 4 vectors (a.x [4][cols], a.y [4][rows], a.resid [4][rows]) in one
 // full-K launch with the transform a.xmode (none or RMSNorm with a.xw) and

@@ -1567,15 +1567,19 @@ static void launch_batch_rg(const GemvArgs &a, int splits, hipStream_t st) {
   lut_gemv_batch_kernel<FMT, NB, VG, RG, kXModeNone, CH><<<grid, block, 0, st>>>(a, row_blocks, splits);
 }
 
-template <int FMT, int NB>
-static int launch_batch_nb(const GemvArgs &a, hipStream_t st) {
+int batched_launch_splits(size_t Npad, size_t Kp) {
   // 128-wide slices (one row group) where 256-wide ones would leave CUs idle
   static const bool s128 = [] {
     const char *e = std::getenv("LMX_BATCH_S128");
     return !(e && std::atoi(e) == 0);
   }();
-  const bool narrow = s128 && batched_slice_splits(size_t(a.Npad), size_t(a.Kp)) != size_t(a.Kp / kRotChunk);
-  const int splits = narrow ? a.Kp / kChunk : a.Kp / kRotChunk;
+  return int(s128 ? batched_slice_splits(Npad, Kp) : Kp / kRotChunk);
+}
+
+template <int FMT, int NB>
+static int launch_batch_nb(const GemvArgs &a, hipStream_t st) {
+  const int splits = batched_launch_splits(size_t(a.Npad), size_t(a.Kp));
+  const bool narrow = splits != a.Kp / kRotChunk;
   // Rows per workgroup: 256 while that leaves a workgroup per CU, else fewer
   // (LMX_BATCH_RG = 1, 2 or 4 forces 64, 128 or 256).
   const auto grid = [&](int rg) { return (a.Npad + rg * kWave - 1) / (rg * kWave) * splits; };
@@ -1592,7 +1596,9 @@ static int launch_batch_nb(const GemvArgs &a, hipStream_t st) {
   else if (rg == 4) launch_batch_rg<FMT, NB, 4>(a, splits, st);
   else if (rg == 2) launch_batch_rg<FMT, NB, 2>(a, splits, st);
   else launch_batch_rg<FMT, NB, 1>(a, splits, st);
-  if (a.epi == kEpiSiluPair) {
+  if (a.epi == kEpiPartials) {
+    // the consumer sums the partials
+  } else if (a.epi == kEpiSiluPair) {
     const int h = a.rows / 2;
     batched_reduce_pair_kernel<<<dim3((h + 4 * kReduceThreads - 1) / (4 * kReduceThreads), NB),
                                  dim3(kReduceThreads), 0, st>>>(a.partials, splits, a.Npad, h, a.bias, a.y);

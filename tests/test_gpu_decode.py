@@ -275,7 +275,10 @@ def test_batched_decoder_matches_oracle(cuda, batch):
 def test_batched_decoder_fused_epilogues(cuda, monkeypatch, batch):
     # o/down reductions writing the normed rows and the gate|up reduction
     # writing SiLU(gate)*up (every row in a batched group) against the row
-    # kernels (LMX_FUSED_ROWS=0): the same bits, and the oracle's logits
+    # kernels (LMX_FUSED_ROWS=0): the same bits, and the oracle's logits.
+    # The qkv split partials summed inside attention (the default for one
+    # group) against the batched reduction writing the rows first
+    # (LMX_QKV_PARTS=0): the same bits as well.
     cfg = D.small_config(hidden=512, n_heads=8, n_kv_heads=2, head_dim=64, ffn=1024, vocab=700, max_seq=64,
                          rope_mode=D.ROPE_REFERENCE, rope_factor=1.0, rope_theta=1e6, qkv_bias=True)
     m = D.SyntheticModel(cfg, seed=35 + batch, group=128, random_norms=True)
@@ -291,10 +294,13 @@ def test_batched_decoder_fused_epilogues(cuda, monkeypatch, batch):
         return out
 
     fused = logits(D.Decoder(m, batch=batch))
+    monkeypatch.setenv("LMX_QKV_PARTS", "0")
+    reduced = logits(D.Decoder(m, batch=batch))
     monkeypatch.setenv("LMX_FUSED_ROWS", "0")
     rows = logits(D.Decoder(m, batch=batch))
     refs = [oracle.OracleDecoder(m) for _ in range(batch)]
     for pos in range(toks.shape[1]):
+        assert np.array_equal(fused[pos].view(np.uint32), reduced[pos].view(np.uint32)), pos
         assert np.array_equal(fused[pos].view(np.uint32), rows[pos].view(np.uint32)), pos
         for b in range(batch):
             assert rel_max_err(fused[pos][b], refs[b].step(toks[b, pos], pos)) < DECODE_TOL, (b, pos)
