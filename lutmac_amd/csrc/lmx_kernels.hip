@@ -1150,8 +1150,10 @@ __global__ __launch_bounds__((kWave * batch_waves<NB, VG, RG>())) void lut_gemv_
 // in split order; resid may be y itself (each element is read and written
 // by one thread).  A thread sums 4 consecutive rows with 16-byte loads (Npad
 // is a multiple of 64, so the 4 rows of any r0 < rows lie inside the padded
-// partials).
+// partials), RL split loads in flight per round: 16, or 48 where K has more
+// than 16 slices (K = 8960: one round trip instead of three).
 constexpr int kReduceThreads = 256;
+template <int RL>
 __global__ __launch_bounds__(kReduceThreads) void batched_reduce_kernel(const float *__restrict__ partials,
                                                                         int splits, int Npad, int rows,
                                                                         const float *__restrict__ bias,
@@ -1161,12 +1163,12 @@ __global__ __launch_bounds__(kReduceThreads) void batched_reduce_kernel(const fl
   const float4 *p = reinterpret_cast<const float4 *>(partials + size_t(n) * splits * Npad + r0);
   const size_t step = size_t(Npad) / 4;
   float4 s = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-  for (int k0 = 0; k0 < splits; k0 += 16) {   // 16 loads in flight, summed in split order
-    float4 v[16];
+  for (int k0 = 0; k0 < splits; k0 += RL) {   // RL loads in flight, summed in split order
+    float4 v[RL];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) v[j] = k0 + j < splits ? p[size_t(k0 + j) * step] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int j = 0; j < RL; ++j) v[j] = k0 + j < splits ? p[size_t(k0 + j) * step] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
-    for (int j = 0; j < 16; ++j) s.x += v[j].x, s.y += v[j].y, s.z += v[j].z, s.w += v[j].w;
+    for (int j = 0; j < RL; ++j) s.x += v[j].x, s.y += v[j].y, s.z += v[j].z, s.w += v[j].w;
   }
   const float t[4] = {s.x, s.y, s.z, s.w};
 #pragma unroll
@@ -1606,8 +1608,13 @@ static int launch_batch_nb(const GemvArgs &a, hipStream_t st) {
     batched_reduce_norm_kernel<<<dim3(NB), dim3(kNormReduceThreads), size_t(a.rows) * sizeof(float), st>>>(
         a.partials, splits, a.Npad, a.rows, a.bias, a.resid, a.y, a.xw, a.eps, a.y2);
   } else {
-    batched_reduce_kernel<<<dim3((a.rows + 4 * kReduceThreads - 1) / (4 * kReduceThreads), NB),
-                            dim3(kReduceThreads), 0, st>>>(a.partials, splits, a.Npad, a.rows, a.bias, a.resid, a.y);
+    const dim3 grid((a.rows + 4 * kReduceThreads - 1) / (4 * kReduceThreads), NB);
+    if (splits > 16)
+      batched_reduce_kernel<48><<<grid, dim3(kReduceThreads), 0, st>>>(a.partials, splits, a.Npad, a.rows, a.bias,
+                                                                       a.resid, a.y);
+    else
+      batched_reduce_kernel<16><<<grid, dim3(kReduceThreads), 0, st>>>(a.partials, splits, a.Npad, a.rows, a.bias,
+                                                                       a.resid, a.y);
   }
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? LMX_OK : fail(LMX_ERR_LAUNCH_FAILED, "batched lut_gemv launch: %s", hipGetErrorString(e));
