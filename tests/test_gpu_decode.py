@@ -347,10 +347,13 @@ def test_batched_decoder_qwen_style(cuda):
     batched_check(D.Decoder(m, batch=4), m, toks)
 
 
-def test_batched_generate_graph_equals_eager_and_oracle(cuda):
+# B = 4: the four-vector step; B = 16: one group of the batched kernel with
+# the qkv partials summed inside attention, captured and replayed
+@pytest.mark.parametrize("B", [4, 16])
+def test_batched_generate_graph_equals_eager_and_oracle(cuda, B):
     cfg = D.small_config(max_seq=96)
     m = D.SyntheticModel(cfg, seed=35, group=128, random_norms=True)
-    B, n_prompt, n_new = 4, 8, 72
+    n_prompt, n_new = 8, 72
     dec = D.Decoder(m, batch=B)
     prompt = np.random.default_rng(36).integers(0, cfg.vocab, (B, n_prompt))
     out, t_pre, t_dec = dec.generate(prompt, n_new)
