@@ -49,10 +49,16 @@ int lmx_quantize_int4(const float *w, size_t rows, size_t cols, size_t group,
  *            [-2, 1] stored as (stage-1, stage-2) bits of q + 2, stage-2
  *            scale 0; with LMX_QUANT_RESIDUAL two residual binary stages;
  *   RRQ3     three residual binary stages (no reference rule);
- *   INT4     lmx_quantize_int4 (no flags).
- * At group 256 the ternary, binary and 2-bit outputs, repacked with
- * lmx_planes_to_blocks, are byte-identical to the reference quantizers'
- * blocks for the same (optionally rotated) weights. */
+ *   INT3     quantize_tensor_int3 (982-1041): s = absmax/4, q = round(w/s)
+ *            in [-4, 3] (0 when s <= 1e-10), code q + 4 (no flags);
+ *   INT4     lmx_quantize_int4 (no flags);
+ *   INT8     quantize_tensor_int8 / Int8Block::set (833-912, types.hpp:441-460):
+ *            s = absmax/127, q = round(w/s) in [-127, 127] (all 0 when s == 0),
+ *            two's-complement code (no flags).
+ * INT3, INT4 and INT8 need a group (a multiple of 8) dividing cols.  At
+ * group 256 the ternary, binary, 2-bit, 3-bit and 8-bit outputs, repacked
+ * with lmx_planes_to_blocks, are byte-identical to the reference
+ * quantizers' blocks for the same (optionally rotated) weights. */
 int lmx_quantize(int format, const float *w, size_t rows, size_t cols,
                  size_t group, unsigned flags, uint8_t *planes, float *scales);
 

@@ -16,7 +16,14 @@
 //            LMX_QUANT_RESIDUAL instead each stage binarises the residual
 //            of the previous ones with the binary rule (real stage-2 scale).
 //   RRQ3     residual binarisation over three stages (no reference rule).
+//   INT3     quantize_tensor_int3 (982-1041): s = absmax / 4, q = round(w * (1/s))
+//            clamped to [-4, 3] (0 when s <= 1e-10), code q + 4 over three
+//            planes (bit p of the code in plane p).
 //   INT4     quantize_tensor_int4 (437-461), as lmx_quantize_int4.
+//   INT8     quantize_tensor_int8 (833-912) with Int8Block::set (types.hpp:441-460):
+//            s = absmax * (1/127) (the -ffast-math build's form of absmax / 127),
+//            q = round(clamp(w * (1/s), -127, 127)), all 0 when s == 0; the
+//            code's two's-complement bits over eight planes.
 // LMX_QUANT_ROTATE first applies the blockwise FWHT-256 to the weights, over
 // the row-major tensor in whole 256-chunks (apply_hadamard_rotation on the
 // tensor's data, as tools/lutmac-quantize.cpp:426-447 does for <= 2-bit
@@ -79,6 +86,46 @@ float binary_group(const float *v, size_t n, uint8_t *plane_row, size_t k0) {
   return s;
 }
 
+// INT3 / INT8: one group's absmax scale and codes, the bits of each code
+// spread over the format's planes (planes [P][rows][cols/8]).
+int quantize_uniform(int format, const float *w, size_t rows, size_t cols, size_t G, uint8_t *planes,
+                     float *scales) {
+  const int P = format == LMX_FMT_INT3 ? 3 : 8;
+  const size_t ng = cols / G, rb = cols / 8;
+  std::memset(planes, 0, size_t(P) * rows * rb);
+  for_rows(rows, [&](size_t r) {
+    const float *v = w + r * cols;
+    for (size_t g = 0; g < ng; ++g) {
+      const size_t k0 = g * G;
+      float absmax = 0.0f;
+      for (size_t i = 0; i < G; ++i) absmax = std::max(absmax, std::abs(v[k0 + i]));
+      float s;
+      if (format == LMX_FMT_INT3) {
+        s = absmax / 4.0f;
+        const float inv = s > 1e-10f ? 1.0f / s : 0.0f;
+        for (size_t i = 0; i < G; ++i) {
+          int q = static_cast<int>(std::round(v[k0 + i] * inv));
+          q = std::max(-4, std::min(3, q));
+          const unsigned code = unsigned(q + 4);
+          for (int p = 0; p < 3; ++p) set_bit(planes + (size_t(p) * rows + r) * rb, k0 + i, (code >> p) & 1u);
+        }
+      } else {
+        s = absmax * (1.0f / 127.0f);
+        if (s != 0.0f) {
+          const float inv = 1.0f / s;
+          for (size_t i = 0; i < G; ++i) {
+            const float val = std::max(-127.0f, std::min(127.0f, v[k0 + i] * inv));
+            const unsigned code = unsigned(uint8_t(int8_t(std::round(val))));
+            for (int p = 0; p < 8; ++p) set_bit(planes + (size_t(p) * rows + r) * rb, k0 + i, (code >> p) & 1u);
+          }
+        }
+      }
+      scales[r * ng + g] = s;
+    }
+  });
+  return LMX_OK;
+}
+
 }  // namespace
 
 extern "C" int lmx_quantize(int format, const float *w, size_t rows, size_t cols, size_t group, unsigned flags,
@@ -92,8 +139,15 @@ extern "C" int lmx_quantize(int format, const float *w, size_t rows, size_t cols
       return fail(LMX_ERR_INVALID_ARGUMENT, "int4 group must be a multiple of 8 dividing cols");
     return lmx_quantize_int4(w, rows, cols, group, planes, scales);
   }
+  if (format == LMX_FMT_INT3 || format == LMX_FMT_INT8) {
+    if (flags) return fail(LMX_ERR_INVALID_ARGUMENT, "int3/int8 take no flags (the tool never rotates them)");
+    if (group == 0 || group % 8 || cols % group)
+      return fail(LMX_ERR_INVALID_ARGUMENT, "int3/int8 group must be a multiple of 8 dividing cols");
+    return quantize_uniform(format, w, rows, cols, group, planes, scales);
+  }
   if (format != LMX_FMT_TERNARY && format != LMX_FMT_BINARY && format != LMX_FMT_RRQ2 && format != LMX_FMT_RRQ3)
-    return fail(LMX_ERR_UNSUPPORTED_FORMAT, "lmx_quantize: format %d (ternary, binary, rrq2, rrq3, int4)", format);
+    return fail(LMX_ERR_UNSUPPORTED_FORMAT, "lmx_quantize: format %d (ternary, binary, rrq2, rrq3, int3, int4, int8)",
+                format);
   if ((flags & LMX_QUANT_RESIDUAL) && format != LMX_FMT_RRQ2)
     return fail(LMX_ERR_INVALID_ARGUMENT, "LMX_QUANT_RESIDUAL applies to rrq2 (rrq3 is always residual)");
   if (group == 0 && format != LMX_FMT_TERNARY)

@@ -98,7 +98,8 @@ def main():
 def quantizer_fixtures(R):
     """The reference quantizers (quantize_tensor, _binary, _int2) on seeded
     N(0, 0.02) weights, plain and after the tool's weight rotation
-    (apply_hadamard_rotation over the tensor, tools/lutmac-quantize.cpp:426-447):
+    (apply_hadamard_rotation over the tensor, tools/lutmac-quantize.cpp:426-447),
+    and _int3 / _int8 on the plain weights (the tool never rotates them):
     inputs and the reference's block bytes (own generator, so the fixtures
     above are unchanged)."""
     rng = np.random.default_rng(20260202)
@@ -115,6 +116,11 @@ def quantizer_fixtures(R):
             blocks = np.zeros(n, np.uint8)
             R.ref_quantize(fmt, P(src), M, K, P(blocks), n)
             out[f"{name}{'_rot' if rot else ''}"] = blocks
+    for fmt, name in [(5, "int3"), (7, "int8")]:
+        n = R.ref_quantize(fmt, P(w), M, K, None, 0)
+        blocks = np.zeros(n, np.uint8)
+        R.ref_quantize(fmt, P(w), M, K, P(blocks), n)
+        out[name] = blocks
     np.savez_compressed(os.path.join(HERE, "quantizers.npz"), **out)
 
 

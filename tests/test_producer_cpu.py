@@ -3,7 +3,9 @@
 Pinned by: the reference quantizers' own block bytes (tests/golden/quantizers.npz,
 written by tests/golden/gen_golden.py from the reference build, and the live
 reference build where it exists) for ternary, binary and 2-bit at group 256,
-plain and with the quantize tool's weight rotation; the FWHT-256 of the
+plain and with the quantize tool's weight rotation, and for 3-bit and 8-bit
+(never rotated) plain; the closed form of the uniform rules (scale =
+absmax / 4 or / 127, codes within half a step of w / scale); the FWHT-256 of the
 activation path (a rotated quantization equals quantizing the oracle-rotated
 weights); and, for the residual stages that have no reference rule, the
 stage definitions (each stage binarises what the earlier ones left: sign
@@ -18,6 +20,8 @@ from conftest import load_golden
 from lutmac_amd import synth
 
 REF_FORMATS = [(L.FMT_TERNARY, "ternary"), (L.FMT_BINARY, "binary"), (L.FMT_RRQ2, "int2")]
+# formats the quantize tool never rotates (tools/lutmac-quantize.cpp:385-425)
+PLAIN_FORMATS = [(L.FMT_INT3, "int3"), (L.FMT_INT8, "int8")]
 
 
 @pytest.mark.parametrize("fmt,name", REF_FORMATS)
@@ -46,6 +50,50 @@ def test_quantizers_match_reference_build(fmt, name, M, K, seed):
         R.ref_quantize(fmt, oracle._ptr(src), M, K, oracle._ptr(ref), n)
         planes, scales, _ = L.quantize(fmt, w, 256, L.QUANT_ROTATE if rot else 0)
         assert np.array_equal(L.planes_to_blocks(fmt, planes, scales, M, K), ref), (name, rot)
+
+
+@pytest.mark.parametrize("fmt,name", PLAIN_FORMATS)
+def test_uniform_quantizers_match_reference_fixtures(fmt, name):
+    g = load_golden("quantizers.npz")
+    w = g["w"]
+    M, K = w.shape
+    planes, scales, _ = L.quantize(fmt, w, 256)
+    assert np.array_equal(L.planes_to_blocks(fmt, planes, scales, M, K), g[name])
+
+
+@pytest.mark.skipif(oracle.ref() is None, reason="oracle/_ref/libref.so not built")
+@pytest.mark.parametrize("fmt,name", PLAIN_FORMATS)
+@pytest.mark.parametrize("M,K,seed", [(300, 2048, 1), (64, 4096, 2), (8, 256, 3)])
+def test_uniform_quantizers_match_reference_build(fmt, name, M, K, seed):
+    R = oracle.ref()
+    w = (np.random.default_rng(seed).standard_normal((M, K)) * 0.02).astype(np.float32)
+    w[M // 2] = 0.0   # an all-zero row: scale 0, every code the format's zero
+    n = R.ref_quantize(fmt, oracle._ptr(w), M, K, None, 0)
+    ref = np.zeros(n, np.uint8)
+    R.ref_quantize(fmt, oracle._ptr(w), M, K, oracle._ptr(ref), n)
+    planes, scales, _ = L.quantize(fmt, w, 256)
+    assert np.array_equal(L.planes_to_blocks(fmt, planes, scales, M, K), ref), name
+
+
+@pytest.mark.parametrize("fmt,qmin,qmax,div", [(L.FMT_INT3, -4, 3, 4.0), (L.FMT_INT8, -127, 127, 127.0)])
+@pytest.mark.parametrize("group", [128, 256])
+def test_uniform_quantizers_closed_form(fmt, qmin, qmax, div, group):
+    # per group: scale = absmax / div, and every weight's code is within half a
+    # step of w / scale (clamped to the format's range); the planes hold the
+    # code's bits, plane p = bit p (int3 code q + 4, int8 two's complement)
+    w = (np.random.default_rng(7).standard_normal((12, 1024)) * 0.02).astype(np.float32)
+    w[3, :group] = 0.0
+    planes, scales, _ = L.quantize(fmt, w, group)
+    P = planes.shape[0]
+    bits = np.unpackbits(planes, axis=2)                       # [P][rows][cols], MSB-first per byte
+    code = sum(bits[p].astype(np.int64) << p for p in range(P))
+    q = code - 4 if fmt == L.FMT_INT3 else np.where(code >= 128, code - 256, code)
+    absmax = np.abs(w).reshape(12, -1, group).max(axis=2)
+    np.testing.assert_allclose(scales[0], absmax / div, rtol=2e-7, atol=0)
+    s = np.repeat(scales[0], group, axis=1)
+    want = np.clip(np.where(s > 0, w / np.where(s > 0, s, 1), 0), qmin, qmax)
+    assert np.all(np.abs(q - want) <= 0.5 + 1e-4)
+    assert np.all(q[3, :group] == 0)
 
 
 @pytest.mark.parametrize("fmt", [L.FMT_TERNARY, L.FMT_BINARY, L.FMT_RRQ2, L.FMT_RRQ3])
@@ -107,7 +155,8 @@ def test_ternary_groups_and_row_scale():
 def test_quantize_rejects_bad_arguments():
     w = np.zeros((4, 256), np.float32)
     for fmt, group, flags in [(L.FMT_BINARY, 0, 0), (L.FMT_INT4, 128, L.QUANT_ROTATE),
-                              (L.FMT_TERNARY, 256, L.QUANT_RESIDUAL), (L.FMT_INT8, 256, 0),
+                              (L.FMT_TERNARY, 256, L.QUANT_RESIDUAL), (L.FMT_INT8, 256, L.QUANT_ROTATE),
+                              (L.FMT_INT3, 96, 0), (L.FMT_INT8, 0, 0),
                               (L.FMT_BINARY, 100, 0), (L.FMT_BINARY, 256, 8)]:
         with pytest.raises(L.LmxError):
             L.quantize(fmt, w, group, flags)
