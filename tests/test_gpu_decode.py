@@ -500,21 +500,30 @@ MIXED = {"q": (L.FMT_TERNARY, 128, 0), "k": (L.FMT_TERNARY, 128, 0), "v": (L.FMT
          "down": (L.FMT_RRQ2, 128, L.QUANT_RESIDUAL), "embed": (L.FMT_INT4, 128, 0)}
 
 
-def test_mixed_format_model_and_lutmac_v2_round_trip(cuda, tmp_path):
-    # linears quantized by lmx_quantize (ternary / binary / RRQ-3 / residual
-    # RRQ-2 at group 128, weights FWHT-rotated as the quantize tool does),
-    # decoded on the device from memory and from a version-2 file, against
-    # the oracle's decode step (which rotates those formats' activations as
+# 3- and 8-bit linears and an 8-bit embedding from the producer's uniform rules
+UNIFORM = {"q": (L.FMT_INT8, 128, 0), "k": (L.FMT_INT8, 128, 0), "v": (L.FMT_INT8, 128, 0),
+           "o": (L.FMT_INT3, 256, 0), "gate": (L.FMT_INT3, 128, 0), "up": (L.FMT_INT3, 128, 0),
+           "down": (L.FMT_INT8, 256, 0), "embed": (L.FMT_INT8, 128, 0)}
+
+
+@pytest.mark.parametrize("formats", [MIXED, UNIFORM], ids=["mixed", "uniform"])
+def test_mixed_format_model_and_lutmac_v2_round_trip(cuda, tmp_path, formats):
+    # linears quantized by lmx_quantize (mixed: ternary / binary / RRQ-3 /
+    # residual RRQ-2 at group 128, weights FWHT-rotated as the quantize tool
+    # does; uniform: 8- and 3-bit at groups 128 and 256), decoded on the
+    # device from memory and from a version-2 file, against the oracle's
+    # decode step (which rotates the 1-2 bit formats' activations as
     # lut_linear does)
     cfg = D.small_config(rope_mode=D.ROPE_REFERENCE, rope_factor=1.0, rope_theta=10000.0, max_seq=64)
-    m = D.QuantizedModel(cfg, MIXED, seed=61)
+    m = D.QuantizedModel(cfg, formats, seed=61)
     toks = np.random.default_rng(62).integers(0, cfg.vocab, 16)
     check_against(D.Decoder(m), oracle.OracleDecoder(m), toks)
     path = tmp_path / "mixed.lutmac"
     m.save_v2(path)
     ours = D.LutmacModel(path, max_seq=64)
-    assert [ours.weight_format(0, w) for w in range(4)] == [L.FMT_TERNARY, L.FMT_BINARY, L.FMT_RRQ3, L.FMT_RRQ2]
-    assert ours.weight_format(-1) == L.FMT_INT4 and ours.weight_format(-2) == L.FMT_INT4
+    want = [formats[n][0] for n in ("q", "o", "gate", "down")]
+    assert [ours.weight_format(0, w) for w in range(4)] == want
+    assert ours.weight_format(-1) == formats["embed"][0] and ours.weight_format(-2) == formats["embed"][0]
     check_against(ours, oracle.OracleDecoder(m), toks)
 
 
