@@ -149,14 +149,16 @@ def test_decoder_matches_reference_model(cuda):
     check_against(D.Decoder(m), oracle.RefDecoder(m), toks)
 
 
-def test_generate_graph_equals_eager_and_oracle(cuda):
-    cfg = D.small_config(max_seq=48)
+# short, and long: 600 positions = 10 attention chunks, past the 8-chunk
+# speculative window, replayed from one captured step
+@pytest.mark.parametrize("n_prompt,n_new,max_seq", [(8, 24, 48), (560, 40, 640)], ids=["short", "long"])
+def test_generate_graph_equals_eager_and_oracle(cuda, n_prompt, n_new, max_seq):
+    cfg = D.small_config(max_seq=max_seq)
     m = D.SyntheticModel(cfg, seed=17, group=128, random_norms=True)
     dec = D.Decoder(m)
-    prompt = np.random.default_rng(18).integers(0, cfg.vocab, 8)
-    n_new = 24
+    prompt = np.random.default_rng(18).integers(0, cfg.vocab, n_prompt)
     out, t_pre, t_dec = dec.generate(prompt, n_new)
-    assert np.array_equal(out[:8], prompt) and t_pre > 0 and t_dec > 0
+    assert np.array_equal(out[:n_prompt], prompt) and t_pre > 0 and t_dec > 0
     # eager steps from the same prompt
     dec.reset(prompt)
     for _ in range(len(prompt) + n_new - 1):
