@@ -458,6 +458,40 @@ def test_decoder_past_4096_positions(cuda):
     check_positions(D.Decoder(m), oracle.OracleDecoder(m), toks, check_from=4030)
 
 
+@pytest.mark.parametrize("batch,hs", [(8, None), (8, "3"), (4, None)])
+def test_batched_qkv_partials_head_dim_128(cuda, monkeypatch, batch, hs):
+    # Qwen attention geometry (head_dim 128, 6 query heads per KV head, QKV
+    # bias) with the qkv split partials summed inside attention: the KV
+    # head's query heads over 2 workgroups (the default for this small
+    # grid) or 3 (LMX_ATTN_HS), batch 8 and 4 (the fused-reduction step,
+    # LMX_QUAD_STEP=0); the same bits as the reduced rows (LMX_QKV_PARTS=0)
+    # and the oracle's logits, across two attention chunks
+    monkeypatch.setenv("LMX_QUAD_STEP", "0")
+    if hs:
+        monkeypatch.setenv("LMX_ATTN_HS", hs)
+    cfg = qwen_small(max_seq=128)
+    m = D.SyntheticModel(cfg, seed=57 + batch, group=128, random_norms=True)
+    toks = np.random.default_rng(58).integers(0, cfg.vocab, (batch, 70))
+
+    def logits(dec):
+        dec.reset(toks)
+        lg = torch.empty(batch * cfg.vocab, dtype=torch.float32, device="cuda")
+        out = []
+        for _ in range(toks.shape[1]):
+            dec.step(lg)
+            out.append(lg.cpu().numpy().reshape(batch, cfg.vocab).copy())
+        return out
+
+    parts = logits(D.Decoder(m, batch=batch))
+    monkeypatch.setenv("LMX_QKV_PARTS", "0")
+    reduced = logits(D.Decoder(m, batch=batch))
+    refs = [oracle.OracleDecoder(m) for _ in range(batch)]
+    for pos in range(toks.shape[1]):
+        assert np.array_equal(parts[pos].view(np.uint32), reduced[pos].view(np.uint32)), pos
+        for b in range(batch):
+            assert rel_max_err(parts[pos][b], refs[b].step(toks[b, pos], pos)) < DECODE_TOL, (b, pos)
+
+
 @pytest.mark.parametrize("cpw", [None, "2"])
 def test_batched_decoder_batch16_past_512(cuda, monkeypatch, cpw):
     # batch 16 = one full group of the batched GEMV, with the attention of every
