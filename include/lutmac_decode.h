@@ -84,6 +84,17 @@ int lmx_decoder_set_layer(lmx_decoder *d, size_t layer, const lmx_weight *qkv,
  * weight (host). */
 int lmx_decoder_set_head(lmx_decoder *d, const lmx_weight *embed,
                          const lmx_weight *head, const float *final_norm);
+/* Repetition penalty of the greedy pick (Model::sample, src/model.cpp:458-469;
+ * GenerationConfig::repetition_penalty, types.hpp:639).  Before each argmax
+ * that picks a token, the logit of every token in the history -- the tokens
+ * given to the next lmx_decoder_reset / lmx_decoder_generate, then every
+ * picked token -- is divided by `penalty` when positive and multiplied by it
+ * otherwise, once per occurrence, as the reference's loop over its
+ * generated_tokens does.  1 (the default) turns it off.  The logits
+ * lmx_decoder_step writes stay unpenalised.  Applies from the next reset or
+ * generate on; the counts live on the device ([batch][vocab] 4-byte words,
+ * allocated by the first call with a penalty other than 1). */
+int lmx_decoder_set_repetition_penalty(lmx_decoder *d, float penalty);
 /* Starts a sequence: position 0, tokens[0..n) = tokens (host).  Positions
  * below n are teacher-forced: their argmax does not overwrite the next
  * token. */

@@ -185,11 +185,15 @@ int lmx_extract_indices(const uint8_t *sign_plane, const uint8_t *zero_plane,
  * y is bit-identical to lmx_gemv's (batches run one vector at a time).  It
  * allocates nothing: the split-K partials, ticket counters and the staging
  * copy of x live in an 8 MiB device array that each GPU holds until the
- * process ends; shapes needing more (counters Npad/64*4 B + staging Kp*4 B +
- * split-K partials (Kp/kslice)*Npad*4 B) return LMX_ERR_INVALID_ARGUMENT.
- * The first call on a device looks the array up and zeroes it (a kernel on
- * `stream`): make it outside graph capture.  Calls on one GPU share the
- * array: calls that overlap in time on one GPU race, so order them. */
+ * process ends: a fixed 64 KiB of split-K ticket counters (one per 64-row
+ * block), then the staging copy of x (Kp*4 B), then the split-K partials
+ * ((Kp/kslice)*Npad*4 B); shapes needing more return
+ * LMX_ERR_INVALID_ARGUMENT.  The first call on a device looks the array up,
+ * zeroes it with a kernel on `stream` and waits for that kernel before it
+ * returns or launches anything else, so make it outside graph capture; every
+ * later call, on any stream or thread, then finds the counters zeroed.  Calls
+ * on one GPU share the array: calls that overlap in time on one GPU race, so
+ * order them (e.g. one stream, or an event between streams). */
 int lmx_gemv_tiles_noalloc(int format, const void *tiles, const float *scales,
                            size_t rows, size_t cols, size_t group,
                            const float *x, float *y, size_t batch,
@@ -204,6 +208,21 @@ int lmx_gemv_tiles_noalloc(int format, const void *tiles, const float *scales,
  * device and no roofline). */
 int lmx_hbm_read_probe(const void *buf, size_t bytes, unsigned *sink,
                        void *stream);
+/* The same read with its launch shape chosen: `workgroups` workgroups of
+ * 1024 lanes, each lane with `loads_in_flight` (1, 2, 4, 8 or 16) 16-byte
+ * loads issued before their data is used (lmx_hbm_read_probe is 2 on 512).
+ * A sweep over shapes gives the fastest plain read at a size. */
+int lmx_hbm_read_probe_shape(const void *buf, size_t bytes, int loads_in_flight,
+                             int workgroups, unsigned *sink, void *stream);
+/* A read of a weight's device tiles and scales (the lmx_tile_planes /
+ * lmx_tile_scales layouts of format x rows x cols x group, K <= 16384) with
+ * the load schedule of the interleaved full-K GEMV: 32 rows per 1024-lane
+ * workgroup, each lane loading its row's plane words of two 128-chunks per
+ * step and their scales -- every step's loads issued at once, so each CU's
+ * whole share of the matrix is requested before any of it is used. */
+int lmx_hbm_read_probe_tiles(const void *tiles, const float *scales, int format,
+                             size_t rows, size_t cols, size_t group,
+                             unsigned *sink, void *stream);
 
 #ifdef __cplusplus
 }

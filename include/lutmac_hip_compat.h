@@ -11,7 +11,9 @@
  * over the array, rechecked on every call: a mismatch re-uploads.  Call
  * lmx_host_forget(blocks) before freeing an array or rewriting part of it
  * (a change the sample cannot see), so no later call reuses stale device
- * weights.  Calls from several threads are safe; calls that share one
+ * weights; or set LMX_HOST_HASH=all in the environment, and every call
+ * hashes the whole array (every rewrite is seen, at a host pass over the
+ * array per call).  Calls from several threads are safe; calls that share one
  * weight are serialised on it.
  *
  * The C++ section maps the reference's names onto them (namespace
@@ -59,6 +61,16 @@ int lmx_host_apply_hadamard_rotation(float *data, size_t n);
 /* precompute_luts (lut_gemm.hpp:53-58): luts[n/4][16]. */
 int lmx_host_precompute_luts(const float *activations, size_t n, float *luts);
 
+/* precompute_lut (lut_gemm.hpp:30-44): the 16-entry table of one group of
+ * 4 activations, lut[m] = sum of a_j over the set bits (3-j) of m. */
+int lmx_host_precompute_lut(const float *activations, float *lut);
+
+/* extract_indices (lut_gemm.hpp:79-99): group group_idx of a ternary
+ * block's sign/zero planes (byte group_idx/2, high nibble for even groups)
+ * -> pos_idx = non-zero and positive, neg_idx = non-zero and negative. */
+int lmx_host_extract_indices(const uint8_t *sign_plane, const uint8_t *zero_plane, size_t group_idx,
+                             uint8_t *pos_idx, uint8_t *neg_idx);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 
@@ -104,6 +116,14 @@ inline void apply_hadamard_rotation(float *data, size_t n) {
 inline void fwht_256(float *data) { apply_hadamard_rotation(data, 256); }
 inline void precompute_luts(const float *activations, size_t n, float *luts) {
   check_or_abort(lmx_host_precompute_luts(activations, n, luts), "precompute_luts");
+}
+inline void precompute_lut(const float *activations, float *lut) {
+  check_or_abort(lmx_host_precompute_lut(activations, lut), "precompute_lut");
+}
+inline void extract_indices(const uint8_t *sign_plane, const uint8_t *zero_plane, size_t group_idx,
+                            uint8_t &pos_idx, uint8_t &neg_idx) {
+  check_or_abort(lmx_host_extract_indices(sign_plane, zero_plane, group_idx, &pos_idx, &neg_idx),
+                 "extract_indices");
 }
 
 /* lut_linear over the reference's PackedTensor (or any type with the same

@@ -33,13 +33,16 @@ EXPORTS = [
     "lmx_tile_bytes", "lmx_tile_planes", "lmx_untile_planes", "lmx_tile_scales", "lmx_gemv_tiles_noalloc",
     "lmx_weight_create", "lmx_weight_from_blocks", "lmx_weight_destroy", "lmx_weight_info",
     "lmx_weight_kernel_config", "lmx_weight_read_tiles", "lmx_gemv", "lmx_linear", "lmx_fwht256",
-    "lmx_precompute_luts", "lmx_extract_indices", "lmx_hbm_read_probe",
+    "lmx_precompute_luts", "lmx_extract_indices", "lmx_hbm_read_probe", "lmx_hbm_read_probe_shape",
+    "lmx_hbm_read_probe_tiles",
     # include/lutmac_hip_compat.h
     "lmx_host_gemv", "lmx_host_lut_linear", "lmx_host_apply_hadamard_rotation",
-    "lmx_host_precompute_luts", "lmx_host_forget", "lmx_host_cache_clear",
+    "lmx_host_precompute_luts", "lmx_host_precompute_lut", "lmx_host_extract_indices", "lmx_host_forget",
+    "lmx_host_cache_clear",
     # include/lutmac_decode.h
     "lmx_decoder_create", "lmx_decoder_create_batched", "lmx_decoder_destroy", "lmx_decoder_set_layer", "lmx_decoder_set_head",
     "lmx_decoder_reset", "lmx_decoder_step", "lmx_decoder_tokens", "lmx_decoder_generate",
+    "lmx_decoder_set_repetition_penalty",
     # include/lutmac_synth.h
     "lmx_quantize_int4", "lmx_quantize", "lmx_synth_int4_normal", "lmx_synth_normal",
     # include/lutmac_model.h
@@ -98,6 +101,8 @@ _SIGS = {
     "lmx_host_apply_hadamard_rotation": ([_p, _sz], _i),
     "lmx_host_forget": ([_p], _i),
     "lmx_hbm_read_probe": ([_p, _sz, _p, _p], _i),
+    "lmx_hbm_read_probe_shape": ([_p, _sz, _i, _i, _p, _p], _i),
+    "lmx_hbm_read_probe_tiles": ([_p, _p, _i, _sz, _sz, _sz, _p, _p], _i),
     "lmx_tile_scales": ([_i, _p, _sz, _sz, _sz, _p, ctypes.POINTER(_sz)], _i),
     "lmx_gemv_tiles_noalloc": ([_i, _p, _p, _sz, _sz, _sz, _p, _p, _sz, _u, _p], _i),
     "lmx_host_cache_clear": ([], _i),
@@ -121,6 +126,9 @@ _SIGS = {
     "lmx_decoder_generate": ([_p, _p, _sz, _sz, _p, ctypes.POINTER(ctypes.c_float),
                               ctypes.POINTER(ctypes.c_float), _p], _i),
     "lmx_host_precompute_luts": ([_p, _sz, _p], _i),
+    "lmx_host_precompute_lut": ([_p, _p], _i),
+    "lmx_decoder_set_repetition_penalty": ([_p, ctypes.c_float], _i),
+    "lmx_host_extract_indices": ([_p, _p, _sz, _p, _p], _i),
 }
 
 _LIB = None
@@ -198,10 +206,16 @@ def planes_to_blocks(fmt, planes, scales, rows, cols):
     return out
 
 
-def tile_scales(fmt, scales, rows, cols, group):
-    """Canonical scales [S, rows, groups] -> the device scale layout (lmx_tile_scales)."""
+def tile_scales_bytes(fmt, rows, cols, group):
+    """Bytes of the device scale layout (lmx_tile_scales with no buffers)."""
     n = ctypes.c_size_t()
     check(lib().lmx_tile_scales(fmt, None, rows, cols, group, None, ctypes.byref(n)))
+    return n.value
+
+
+def tile_scales(fmt, scales, rows, cols, group):
+    """Canonical scales [S, rows, groups] -> the device scale layout (lmx_tile_scales)."""
+    n = ctypes.c_size_t(tile_scales_bytes(fmt, rows, cols, group))
     out = np.zeros(n.value // 4, np.float32)
     sc = np.ascontiguousarray(scales, np.float32)
     check(lib().lmx_tile_scales(fmt, _np_ptr(sc), rows, cols, group, _np_ptr(out), ctypes.byref(n)))
@@ -210,7 +224,19 @@ def tile_scales(fmt, scales, rows, cols, group):
 
 def gemv_tiles_noalloc(fmt, tiles, scales, rows, cols, group, x, y, batch=1, flags=ROTATE_NONE, stream=None):
     """lmx_gemv_tiles_noalloc on device tensors (tiles uint8, scales fp32 in the
-    device layouts, x [batch*cols], y [batch*rows])."""
+    device layouts, x [batch*cols], y [batch*rows]).  The C entry point takes no
+    buffer sizes, so every buffer is checked against the shape here first: an
+    undersized one raises LmxError instead of reaching the device."""
+    need = {
+        "tiles": (tiles.numel() * tiles.element_size(), tile_bytes(fmt, rows, cols)),
+        "scales": (scales.numel() * scales.element_size(), tile_scales_bytes(fmt, rows, cols, group)),
+        "x": (x.numel() * x.element_size(), 4 * batch * cols),
+        "y": (y.numel() * y.element_size(), 4 * batch * rows),
+    }
+    for name, (have, want) in need.items():
+        if have < want:
+            raise LmxError(ERR_INVALID_ARGUMENT, f"{name} holds {have} bytes, {rows} x {cols} x batch {batch} "
+                                                 f"needs {want}")
     check(lib().lmx_gemv_tiles_noalloc(fmt, _dev_ptr(tiles), _dev_ptr(scales), rows, cols, group, _dev_ptr(x),
                                        _dev_ptr(y), batch, flags, _stream_ptr(stream)))
     return y
@@ -369,6 +395,22 @@ def hbm_read_probe(buf, sink, stream=None):
                                    _stream_ptr(stream)))
 
 
+def hbm_read_probe_shape(buf, sink, loads_in_flight, workgroups, stream=None):
+    """The plain read with a chosen launch shape (lmx_hbm_read_probe_shape)."""
+    check(lib().lmx_hbm_read_probe_shape(_dev_ptr(buf), buf.numel() * buf.element_size(), loads_in_flight,
+                                         workgroups, _dev_ptr(sink), _stream_ptr(stream)))
+
+
+def hbm_read_probe_tiles(tiles, scales, fmt, rows, cols, group, sink, stream=None):
+    """A read of device tiles + scales with the interleaved GEMV's load schedule
+    (lmx_hbm_read_probe_tiles); buffer sizes are checked against the shape."""
+    if tiles.numel() * tiles.element_size() < tile_bytes(fmt, rows, cols) or \
+            scales.numel() * scales.element_size() < tile_scales_bytes(fmt, rows, cols, group):
+        raise LmxError(ERR_INVALID_ARGUMENT, "tiles or scales smaller than the shape's layouts")
+    check(lib().lmx_hbm_read_probe_tiles(_dev_ptr(tiles), _dev_ptr(scales), fmt, rows, cols, group,
+                                         _dev_ptr(sink), _stream_ptr(stream)))
+
+
 def precompute_luts(x, rotate=False, stream=None):
     import torch
     n = x.numel()
@@ -430,3 +472,24 @@ def host_precompute_luts(x):
     out = np.zeros((x.size // 4) * 16, np.float32)
     check(lib().lmx_host_precompute_luts(_np_ptr(x), x.size, _np_ptr(out)))
     return out
+
+
+def host_precompute_lut(a4):
+    """precompute_lut on 4 host activations -> the 16-entry table."""
+    a = np.ascontiguousarray(a4, np.float32)
+    if a.size != 4:
+        raise ValueError("precompute_lut takes 4 activations")
+    out = np.zeros(16, np.float32)
+    check(lib().lmx_host_precompute_lut(_np_ptr(a), _np_ptr(out)))
+    return out
+
+
+def host_extract_indices(sign_plane, zero_plane, group_idx):
+    """extract_indices on host plane bytes -> (pos_idx, neg_idx)."""
+    s = np.ascontiguousarray(sign_plane, np.uint8)
+    z = np.ascontiguousarray(zero_plane, np.uint8)
+    if group_idx // 2 >= min(s.size, z.size):
+        raise ValueError("group_idx past the plane bytes")
+    pos, neg = ctypes.c_uint8(), ctypes.c_uint8()
+    check(lib().lmx_host_extract_indices(_np_ptr(s), _np_ptr(z), group_idx, ctypes.byref(pos), ctypes.byref(neg)))
+    return pos.value, neg.value

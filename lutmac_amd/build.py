@@ -44,16 +44,23 @@ def _run(cmd, verbose):
 
 
 def build(verbose=True):
+    """Compiles every translation unit (in parallel, one hipcc per file) and
+    links the library."""
+    from concurrent.futures import ThreadPoolExecutor
     os.makedirs(OUT_DIR, exist_ok=True)
-    objs = []
+    jobs = []
     for src, device in SOURCES:
         path = os.path.join(CSRC, src)
         if not os.path.exists(path):
             continue
         obj = os.path.join(OUT_DIR, src + ".o")
         flags = COMMON + (DEVICE if device else ["-D__HIP_PLATFORM_AMD__"])
-        _run([HIPCC] + flags + ["-c", path, "-o", obj], verbose)
-        objs.append(obj)
+        jobs.append(([HIPCC] + flags + ["-c", path, "-o", obj], obj))
+    workers = max(1, min(len(jobs), int(os.environ.get("MAX_JOBS", "8"))))
+    with ThreadPoolExecutor(workers) as pool:
+        for f in [pool.submit(_run, cmd, verbose) for cmd, _ in jobs]:
+            f.result()
+    objs = [obj for _, obj in jobs]
     tmp = LIB + ".tmp"
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp] + objs, verbose)
     os.replace(tmp, LIB)

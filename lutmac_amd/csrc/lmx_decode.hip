@@ -38,6 +38,7 @@
 #include <cstring>
 #include <vector>
 
+#include "lmx_device.hpp"
 #include "lmx_internal.hpp"
 #include "lmx_lanes.hpp"
 #include "lutmac_decode.h"
@@ -146,15 +147,18 @@ __global__ __launch_bounds__(1024) void argmax_rows_kernel(const float *__restri
                                                            int *__restrict__ pos_p, int n_forced, int max_pos,
                                                            unsigned *__restrict__ ticket_p,
                                                            unsigned long long *__restrict__ slots,
-                                                           unsigned *__restrict__ seq_tickets) {
+                                                           unsigned *__restrict__ seq_tickets,
+                                                           unsigned *__restrict__ pcount, float penalty) {
   constexpr int NT = 1024, IN = 4;   // threads, loads in flight per thread
   __shared__ unsigned long long best[16];
   const int part = blockIdx.x, parts = gridDim.x, b = blockIdx.y;
   const float *lg = logits + size_t(b) * vocab;
+  unsigned *pc = pcount ? pcount + size_t(b) * vocab : nullptr;   // repetition penalty: token counts
   unsigned long long key = 0;
   // key = orderable value bits << 32 | ~index: the largest value, the lowest
   // index among equal values; NaN never wins, -0 counts as +0
-  const auto fold = [&key](float v, int i) {
+  const auto fold = [&key, pc, penalty](float v, int i) {
+    if (pc) v = penalised_logit(v, pc[i], penalty);
     if (__builtin_isnan(v)) return;
     uint32_t u = __float_as_uint(v + 0.0f);
     u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
@@ -202,7 +206,10 @@ __global__ __launch_bounds__(1024) void argmax_rows_kernel(const float *__restri
   }
   const int idx = key ? int(0xFFFFFFFFu - uint32_t(key)) : 0;
   const int pos = *pos_p;
-  if (pos + 1 >= n_forced && pos + 1 <= max_pos) tokens[size_t(b) * tstride + pos + 1] = idx;
+  if (pos + 1 >= n_forced && pos + 1 <= max_pos) {
+    tokens[size_t(b) * tstride + pos + 1] = idx;
+    if (pc) pc[idx] += 1u;   // the sampled token joins the history
+  }
   __builtin_amdgcn_s_waitcnt(0);
   const unsigned t = __hip_atomic_fetch_add(ticket_p, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   if (t == gridDim.y - 1) {   // every sequence has read the position
@@ -224,7 +231,7 @@ __global__ __launch_bounds__(1024) void finish_embed_kernel(const unsigned long 
                                                             const uint8_t *__restrict__ planes,
                                                             const float *__restrict__ scales, int Npad, int rows,
                                                             int n_groups, int group_chunks, int cols,
-                                                            float *__restrict__ out) {
+                                                            float *__restrict__ out, unsigned *__restrict__ pcount) {
   constexpr int P = EmbFmt<FMT>::P, S = EmbFmt<FMT>::S;
   __shared__ unsigned long long best[16];
   __shared__ int next;
@@ -239,10 +246,12 @@ __global__ __launch_bounds__(1024) void finish_embed_kernel(const unsigned long 
     const int pos = *pos_p;
     int t = idx;
     if (pos + 1 <= max_pos) {
-      if (pos + 1 >= n_forced)
+      if (pos + 1 >= n_forced) {
         tokens[pos + 1] = idx;
-      else
+        if (pcount) pcount[idx] += 1u;   // the sampled token joins the penalty's history
+      } else {
         t = tokens[pos + 1];   // the prompt's token
+      }
     }
     *pos_p = pos + 1;
     next = t;
@@ -739,6 +748,12 @@ struct lmx_decoder {
   unsigned long long *amax = nullptr;    // per-wave argmax keys of the head GEMV
   size_t amax_slots = 0;
   int *tokens = nullptr, *pos = nullptr;
+  // Repetition penalty (Model::sample, model.cpp:458-469): off at 1; else
+  // pcount [batch][vocab] counts each token's occurrences in the history
+  // (the prompt, then every sampled token), kept on the device.
+  float penalty = 1.0f;
+  unsigned *pcount = nullptr;
+  unsigned *penalty_counts() const { return penalty != 1.0f ? pcount : nullptr; }
   int n_forced = 0;
   size_t host_pos = 0;
   float pos_div = 1.0f;
@@ -782,10 +797,13 @@ bool gate_up_pairs(const lmx_weight *gate_up) {
 }
 
 int gemv(const lmx_weight *w, const float *x, float *y, const float *bias, int xmode, const float *xw, float eps,
-         hipStream_t st, unsigned long long *amax = nullptr, int epi = kEpiStore) {
+         hipStream_t st, unsigned long long *amax = nullptr, int epi = kEpiStore, const unsigned *pcount = nullptr,
+         float penalty = 1.0f) {
   GemvArgs a = weight_args(w);
   a.epi = epi;
   a.amax = amax;
+  a.pcount = pcount;
+  a.penalty = penalty;
   a.x = x;
   a.y = y;
   a.bias = bias;
@@ -827,7 +845,7 @@ void launch_finish_embed(const lmx_decoder *d, hipStream_t st) {
   finish_embed_kernel<FMT><<<dim3(1), dim3(1024), 0, st>>>(
       d->amax, int(d->amax_slots), d->tokens, d->pos, d->n_forced, int(d->cfg.max_seq),
       static_cast<const uint8_t *>(w->d_planes), w->d_scales, int(w->Npad), int(w->rows), int(w->n_groups),
-      int(w->group / kChunk), int(w->cols), d->hidden);
+      int(w->group / kChunk), int(w->cols), d->hidden, d->penalty_counts());
 }
 
 // Greedy finish of a batch-1 step and the embedding of the next token.
@@ -1079,7 +1097,7 @@ int step_batched(lmx_decoder *d, float *logits_out, hipStream_t st) {
   const int parts = std::max(1, std::min(kArgmaxParts, ap ? std::atoi(ap) : int(256 / B)));
   argmax_rows_kernel<<<dim3(unsigned(parts), unsigned(B)), dim3(1024), 0, st>>>(
       lg, int(c.vocab), d->tokens, int(c.max_seq + 1), d->pos, d->n_forced, int(c.max_seq), d->argmax_ticket,
-      d->argmax_slots, d->argmax_seq_tickets);
+      d->argmax_slots, d->argmax_seq_tickets, d->penalty_counts(), d->penalty);
   return launch_err("argmax_rows");
 }
 
@@ -1130,7 +1148,9 @@ int step(lmx_decoder *d, float *logits_out, hipStream_t st) {
     }
   }
   float *lg = logits_out ? logits_out : d->logits;
-  if ((r = gemv(d->head, d->hidden, lg, nullptr, kXModeRmsNorm, d->final_norm, c.rms_eps, st, d->amax))) return r;
+  if ((r = gemv(d->head, d->hidden, lg, nullptr, kXModeRmsNorm, d->final_norm, c.rms_eps, st, d->amax, kEpiStore,
+                d->penalty_counts(), d->penalty)))
+    return r;
   return finish_embed(d, st);
 }
 
@@ -1156,6 +1176,14 @@ int set_position(lmx_decoder *d, const int32_t *tokens, size_t n, hipStream_t st
   if (d->batch == 1) {   // a batch-1 step starts from the embedding of the token at its position
     const int r = embed(d->embed, d->tokens, d->pos, d->hidden, 1, int(d->cfg.max_seq + 1), st);
     if (r) return r;
+  }
+  std::vector<unsigned> hist;   // the penalty's history starts as the whole prompt (inference.cpp:264-268)
+  if (d->penalty_counts()) {
+    hist.assign(d->batch * d->cfg.vocab, 0u);
+    for (size_t b = 0; b < d->batch; ++b)
+      for (size_t i = 0; i < n; ++i) hist[b * d->cfg.vocab + size_t(tokens[b * n + i])] += 1u;
+    e = hipMemcpyAsync(d->pcount, hist.data(), hist.size() * sizeof(unsigned), hipMemcpyHostToDevice, st);
+    if (e != hipSuccess) return hip_err(e, "decoder reset (penalty counts)");
   }
   e = hipStreamSynchronize(st);
   if (e != hipSuccess) return hip_err(e, "decoder reset");
@@ -1286,6 +1314,18 @@ int lmx_decoder_set_head(lmx_decoder *d, const lmx_weight *embed, const lmx_weig
   d->amax_slots = slots;
   d->embed = embed;
   d->head = head;
+  return LMX_OK;
+}
+
+int lmx_decoder_set_repetition_penalty(lmx_decoder *d, float penalty) {
+  if (!d) return fail(LMX_ERR_INVALID_ARGUMENT, "decoder is NULL");
+  if (!(penalty > 0.0f) || !std::isfinite(penalty))
+    return fail(LMX_ERR_INVALID_ARGUMENT, "repetition penalty %g must be positive and finite", double(penalty));
+  if (penalty != 1.0f && !d->pcount) {
+    const int st = d->alloc(reinterpret_cast<void **>(&d->pcount), d->batch * d->cfg.vocab * sizeof(unsigned));
+    if (st) return st;
+  }
+  d->penalty = penalty;
   return LMX_OK;
 }
 

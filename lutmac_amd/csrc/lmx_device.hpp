@@ -306,6 +306,21 @@ __device__ __forceinline__ unsigned long long wave_argmax_key(float v, int row, 
   return wave_max_key(key, threadIdx.x & (kWave - 1));
 }
 
+// Repetition penalty of Model::sample (model.cpp:458-469): once per
+// occurrence of the token in the history, a positive logit is divided by the
+// penalty and any other multiplied by it; the sign never changes, so n
+// occurrences are n of the same step, applied one after another as there.
+__device__ __forceinline__ float penalised_logit(float v, unsigned n, float penalty) {
+  for (unsigned i = 0; i < n; ++i) v = v > 0.0f ? v / penalty : v * penalty;
+  return v;
+}
+
+// The value the greedy pick ranks for row `row` of a GEMV with an argmax
+// epilogue: y itself, or y penalised when the launch carries token counts.
+__device__ __forceinline__ float argmax_value(const GemvArgs &a, float v, int row, bool valid) {
+  return a.pcount && valid ? penalised_logit(v, a.pcount[row], a.penalty) : v;
+}
+
 // Writes the wave's key into its slot: one slot per wave of the launch
 // (every slot is written on every launch, so the reader sees no stale keys).
 __device__ __forceinline__ void wave_argmax(unsigned long long *slots, int slot, float v, int row, bool valid) {

@@ -66,6 +66,9 @@ struct GemvArgs {
   const float *xw;         // kXModeRmsNorm: norm weight [cols]
   float eps;               // kXModeRmsNorm: epsilon
   unsigned long long *amax;  // when set: per-wave argmax keys of y (gemv_argmax_slots of them)
+  const unsigned *pcount;  // with amax, or null: occurrences of each row's token in the history; the
+                           // argmax keys then rank repetition-penalised values (penalised_logit)
+  float penalty;           // repetition penalty applied pcount[row] times
   int epi;                 // output epilogue (kEpi*)
   float *y2;               // kEpiNormOut: RMSNorm of y with weight xw [rows] (batched GEMV only)
 };

@@ -146,7 +146,9 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_kernel(GemvArgs a, int
   if (splits == 1) {
     const float out = a.bias && active && row < a.rows ? acc + a.bias[row] : acc;
     if (active && row < a.rows) a.y[row] = out;
-    if (a.amax) wave_argmax(a.amax, blockIdx.x * WAVES + wave, out, row, active && row < a.rows);
+    if (a.amax)
+      wave_argmax(a.amax, blockIdx.x * WAVES + wave, argmax_value(a, out, row, active && row < a.rows), row,
+                  active && row < a.rows);
     return;
   }
   float *part = a.partials + size_t(split) * a.Npad;
@@ -198,7 +200,7 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_kernel(GemvArgs a, int
     out = a.bias ? s + a.bias[r] : s;
     a.y[r] = out;
   }
-  if (a.amax) wave_argmax(a.amax, rb * WAVES + wave, out, r, r < a.rows);
+  if (a.amax) wave_argmax(a.amax, rb * WAVES + wave, argmax_value(a, out, r, r < a.rows), r, r < a.rows);
   if (threadIdx.x == 0) __hip_atomic_store(a.counters + rb, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -208,7 +210,8 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_kernel(GemvArgs a, int
 // in a fixed order.
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restrict__ partials, int splits, int Npad,
                                                             int rows, const float *__restrict__ bias,
-                                                            float *__restrict__ y, unsigned long long *amax) {
+                                                            float *__restrict__ y, unsigned long long *amax,
+                                                            const unsigned *__restrict__ pcount, float penalty) {
   __shared__ float q[4][kWave];
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
   const int r = blockIdx.x * kWave + lane;
@@ -223,7 +226,8 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restr
       t = bias ? t + bias[r] : t;
       y[r] = t;
     }
-    if (amax) wave_argmax(amax, blockIdx.x, t, r, r < rows);
+    if (amax)
+      wave_argmax(amax, blockIdx.x, pcount && r < rows ? penalised_logit(t, pcount[r], penalty) : t, r, r < rows);
   }
 }
 
@@ -400,7 +404,9 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_fullk_kernel(GemvArgs 
       a.y[r] = t;
     }
   }
-  if (a.amax && threadIdx.x < kWave) wave_argmax(a.amax, blockIdx.x, t, r, threadIdx.x < RW && r < a.rows);
+  if (a.amax && threadIdx.x < kWave)
+    wave_argmax(a.amax, blockIdx.x, argmax_value(a, t, r, threadIdx.x < RW && r < a.rows), r,
+                threadIdx.x < RW && r < a.rows);
 }
 
 // Full-K kernel with a lean front end: the same geometry, lookups and
@@ -881,7 +887,8 @@ static int launch_fmt(const GemvArgs &a, hipStream_t st) {
   const int splits = a.Kp / a.kslice;
   if (splits > 1 && a.reduce == kReduceTwoPass)
     splitk_reduce_kernel<<<dim3((a.rows + kWave - 1) / kWave), dim3(256), 0, st>>>(a.partials, splits, a.Npad,
-                                                                                  a.rows, a.bias, a.y, a.amax);
+                                                                                  a.rows, a.bias, a.y, a.amax,
+                                                                                  a.pcount, a.penalty);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(LMX_ERR_LAUNCH_FAILED, "lut_gemv launch: %s", hipGetErrorString(e));
   return LMX_OK;

@@ -9,14 +9,17 @@
 // hipMalloc, hipFree or any allocating routine.
 //
 // Scratch layout (byte offsets, each region 256-byte aligned):
-//   [0, C)        ticket counters, one per 64-row block   C = Npad/64 * 4
-//   [C, C+X)      staging copy of x (unaligned x, length-K FWHT)   X = Kp * 4
-//   [C+X, ...)    split-K partials [Kp/kslice][Npad] fp32 (split-K plans only)
+//   [0, 64 KiB)   ticket counters, one per 64-row block of a split-K plan: a
+//                 fixed region, so no other call's staging or partials ever
+//                 land on a counter (up to 16384 row blocks, Npad <= 1 Mi rows)
+//   [64 KiB, +X)  staging copy of x (unaligned x, length-K FWHT)   X = Kp * 4
+//   [.., ...)     split-K partials [Kp/kslice][Npad] fp32 (split-K plans only)
 // The counters must read zero when a call starts: the first call on a
-// device zeroes the whole array with a fill kernel, and every split-K
-// launch leaves each counter it used at zero again (its last workgroup
-// resets it).  Calls on one GPU share the array, so calls that overlap in
-// time on one GPU (two streams, two threads) race; order them.
+// device zeroes the whole array with a fill kernel and waits for it before
+// any call may use the array, and every split-K launch leaves each counter
+// it used at zero again (its last workgroup resets it).  Calls on one GPU
+// share the array, so calls that overlap in time on one GPU (two streams,
+// two threads) race; order them.
 #include <hip/hip_runtime.h>
 
 #include <mutex>
@@ -24,6 +27,7 @@
 #include "lmx_internal.hpp"
 
 constexpr size_t kScratchBytes = size_t(8) << 20;   // 8 MiB per GPU
+constexpr size_t kCounterBytes = size_t(64) << 10;  // fixed ticket-counter region at offset 0
 
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
@@ -40,7 +44,9 @@ std::mutex g_mu;
 void *g_ptr[kMaxDevices] = {};   // each device's address of `scratch`, set once
 
 // The device address of this device's `scratch` (never the host-side name),
-// set up on the first call on the device.
+// set up on the first call on the device: the zero fill is waited for before
+// the address is published, so a call on any stream or thread that starts
+// after this one returned finds zeroed counters.
 int scratch_ptr(int dev, void *stream, unsigned char **out) {
   if (dev < 0 || dev >= kMaxDevices) return fail(LMX_ERR_NO_DEVICE, "device %d outside 0..%d", dev, kMaxDevices - 1);
   std::lock_guard<std::mutex> lock(g_mu);
@@ -49,10 +55,12 @@ int scratch_ptr(int dev, void *stream, unsigned char **out) {
     hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (e != hipSuccess || !p)
       return fail(LMX_ERR_HIP, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
-    zero_scratch_kernel<<<dim3(1024), dim3(256), 0, static_cast<hipStream_t>(stream)>>>(static_cast<uint32_t *>(p),
-                                                                                      kScratchBytes / 4);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    zero_scratch_kernel<<<dim3(1024), dim3(256), 0, st>>>(static_cast<uint32_t *>(p), kScratchBytes / 4);
     e = hipGetLastError();
     if (e != hipSuccess) return fail(LMX_ERR_LAUNCH_FAILED, "scratch zero fill: %s", hipGetErrorString(e));
+    e = hipStreamSynchronize(st);
+    if (e != hipSuccess) return fail(LMX_ERR_HIP, "scratch zero fill: %s", hipGetErrorString(e));
     g_ptr[dev] = p;
   }
   *out = static_cast<unsigned char *>(g_ptr[dev]);
@@ -81,14 +89,15 @@ extern "C" int lmx_gemv_tiles_noalloc(int format, const void *tiles, const float
   lmx_weight w;   // the plan lmx_weight_create would choose, over the caller's buffers
   plan_weight(&w, format, rows, cols, group);
   w.batched = false;   // one vector at a time: the batched kernel's partials would not fit
-  const size_t counters = round_up(w.Npad / kWave * sizeof(unsigned), 256);
+  const size_t row_blocks = w.Npad / kWave;
   const size_t staging = round_up(w.Kp * sizeof(float), 256);
   const size_t partials = w.fullk ? 0 : (w.Kp / size_t(w.kslice)) * w.Npad * sizeof(float);
-  if (counters + staging + partials > kScratchBytes)
+  if ((!w.fullk && row_blocks * sizeof(unsigned) > kCounterBytes) || kCounterBytes + staging + partials > kScratchBytes)
     return fail(LMX_ERR_INVALID_ARGUMENT,
-                "%zu x %zu needs %zu B of scratch (ticket counters, x staging, split-K partials); "
+                "%zu x %zu needs %zu B of scratch (ticket counters %zu B of %zu, x staging, split-K partials); "
                 "lmx_gemv_tiles_noalloc holds %zu B per GPU: use a weight handle (lmx_gemv)",
-                rows, cols, counters + staging + partials, kScratchBytes);
+                rows, cols, kCounterBytes + staging + partials, w.fullk ? size_t(0) : row_blocks * sizeof(unsigned),
+                kCounterBytes, kScratchBytes);
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return fail(LMX_ERR_NO_DEVICE, "hipGetDevice: %s", hipGetErrorString(e));
@@ -99,7 +108,7 @@ extern "C" int lmx_gemv_tiles_noalloc(int format, const void *tiles, const float
   w.d_planes = const_cast<void *>(tiles);
   w.d_scales = const_cast<float *>(scales);
   w.d_counters = reinterpret_cast<unsigned *>(base);
-  w.d_xrot = reinterpret_cast<float *>(base + counters);
-  w.d_partials = reinterpret_cast<float *>(base + counters + staging);
+  w.d_xrot = reinterpret_cast<float *>(base + kCounterBytes);
+  w.d_partials = reinterpret_cast<float *>(base + kCounterBytes + staging);
   return gemv_impl(&w, x, y, batch, flags, stream);
 }

@@ -1,9 +1,19 @@
-// lmx_probe.hip -- achievable-bandwidth yardstick: a plain streaming read of
-// a device buffer (16-byte non-temporal loads, 512 workgroups of 1024
-// threads, two loads in flight per thread; the fastest plain-read shape
-// measured on MI355X at the 16-70 MB GEMV sizes).  It does no arithmetic
-// beyond an XOR that keeps the loads live, so its time is what the memory
-// system needs to deliver the same bytes a GEMV streams.
+// lmx_probe.hip -- achievable-bandwidth yardsticks: plain streaming reads of
+// device buffers that do no arithmetic beyond an XOR keeping the loads live,
+// so their time is what the memory system needs to deliver the bytes a GEMV
+// streams.
+//   read_probe_kernel<IN>   linear read, 16-byte non-temporal loads, IN
+//                           loads in flight per lane before the XOR
+//                           (lmx_hbm_read_probe: IN = 2 on 512 workgroups of
+//                           1024 lanes; lmx_hbm_read_probe_shape: any IN of
+//                           1/2/4/8/16 and any grid)
+//   tile_probe_kernel<CPS,P,S>  the interleaved full-K GEMV's own loads
+//                           (lmx_hbm_read_probe_tiles): 32 rows per 1024-lane
+//                           workgroup, wave w's half-waves reading 128-chunks
+//                           2(w*CPS + c) and 2(w*CPS + c) + 1 of their row
+//                           for every plane, plus the row's scales -- every
+//                           load of a lane issued before the first is used,
+//                           so the CU's whole share is requested at once
 #include <hip/hip_runtime.h>
 
 #include "lmx_internal.hpp"
@@ -13,14 +23,18 @@ namespace {
 
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
+template <int IN>
 __global__ __launch_bounds__(1024) void read_probe_kernel(const u32x4 *__restrict__ p, size_t n16,
                                                           unsigned *__restrict__ sink) {
   const size_t nt = size_t(gridDim.x) * blockDim.x;
   size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
   unsigned acc = 0;
-  for (; i + nt < n16; i += 2 * nt) {
-    const u32x4 a = __builtin_nontemporal_load(p + i), b = __builtin_nontemporal_load(p + i + nt);
-    acc ^= a.x ^ a.y ^ a.z ^ a.w ^ b.x ^ b.y ^ b.z ^ b.w;
+  for (; i + (IN - 1) * nt < n16; i += IN * nt) {
+    u32x4 v[IN];
+#pragma unroll
+    for (int j = 0; j < IN; ++j) v[j] = __builtin_nontemporal_load(p + i + j * nt);
+#pragma unroll
+    for (int j = 0; j < IN; ++j) acc ^= v[j].x ^ v[j].y ^ v[j].z ^ v[j].w;
   }
   for (; i < n16; i += nt) {
     const u32x4 a = p[i];
@@ -29,17 +43,114 @@ __global__ __launch_bounds__(1024) void read_probe_kernel(const u32x4 *__restric
   if (acc == 0x9E3779B9u) sink[0] = acc;   // practically never: keeps the loads
 }
 
+// Tiles [Kc][P][Npad][16 B], scales [S][n_groups][Npad] fp32 (the device
+// layouts of lmx_tile_planes / lmx_tile_scales).
+template <int CPS, int P, int S>
+__global__ __launch_bounds__(1024) void tile_probe_kernel(const u32x4 *__restrict__ tiles,
+                                                          const float *__restrict__ scales, int Npad, int Kc,
+                                                          int n_groups, int group_chunks,
+                                                          unsigned *__restrict__ sink) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5;
+  const int row = blockIdx.x * 32 + (lane & 31);
+  u32x4 w[CPS][P];
+  float sc[CPS][S];
+#pragma unroll
+  for (int c = 0; c < CPS; ++c) {
+    const int ch = min(2 * (wave * CPS + c) + h, Kc - 1);
+#pragma unroll
+    for (int p = 0; p < P; ++p) w[c][p] = __builtin_nontemporal_load(tiles + (size_t(ch) * P + p) * Npad + row);
+#pragma unroll
+    for (int t = 0; t < S; ++t) sc[c][t] = scales[(size_t(t) * n_groups + ch / group_chunks) * Npad + row];
+  }
+  unsigned acc = 0;
+#pragma unroll
+  for (int c = 0; c < CPS; ++c) {
+#pragma unroll
+    for (int p = 0; p < P; ++p) acc ^= w[c][p].x ^ w[c][p].y ^ w[c][p].z ^ w[c][p].w;
+#pragma unroll
+    for (int t = 0; t < S; ++t) acc ^= __float_as_uint(sc[c][t]);
+  }
+  if (acc == 0x9E3779B9u) sink[0] = acc;
+}
+
+int launch_read(const void *buf, size_t bytes, int in_flight, int workgroups, unsigned *sink, hipStream_t st) {
+  const u32x4 *p = static_cast<const u32x4 *>(buf);
+  const dim3 grid{unsigned(workgroups)}, block{1024u};
+  switch (in_flight) {
+  case 1: read_probe_kernel<1><<<grid, block, 0, st>>>(p, bytes / 16, sink); break;
+  case 2: read_probe_kernel<2><<<grid, block, 0, st>>>(p, bytes / 16, sink); break;
+  case 4: read_probe_kernel<4><<<grid, block, 0, st>>>(p, bytes / 16, sink); break;
+  case 8: read_probe_kernel<8><<<grid, block, 0, st>>>(p, bytes / 16, sink); break;
+  case 16: read_probe_kernel<16><<<grid, block, 0, st>>>(p, bytes / 16, sink); break;
+  default: return fail(LMX_ERR_INVALID_ARGUMENT, "loads in flight %d: use 1, 2, 4, 8 or 16", in_flight);
+  }
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? LMX_OK : fail(LMX_ERR_LAUNCH_FAILED, "read probe launch: %s", hipGetErrorString(e));
+}
+
+template <int CPS, int P, int S>
+void launch_tiles(const void *tiles, const float *scales, int Npad, int Kc, int n_groups, int group_chunks,
+                  unsigned *sink, hipStream_t st) {
+  tile_probe_kernel<CPS, P, S><<<dim3(unsigned(Npad / 32)), dim3(1024), 0, st>>>(
+      static_cast<const u32x4 *>(tiles), scales, Npad, Kc, n_groups, group_chunks, sink);
+}
+
+template <int CPS>
+int launch_tiles_fmt(int planes, int stages, const void *tiles, const float *scales, int Npad, int Kc, int n_groups,
+                     int group_chunks, unsigned *sink, hipStream_t st) {
+#define LMX_TP(PP, SS)                                                                          \
+  if (planes == PP && stages == SS) {                                                           \
+    launch_tiles<CPS, PP, SS>(tiles, scales, Npad, Kc, n_groups, group_chunks, sink, st);       \
+    return LMX_OK;                                                                              \
+  }
+  LMX_TP(1, 1) LMX_TP(2, 1) LMX_TP(2, 2) LMX_TP(3, 1) LMX_TP(3, 3) LMX_TP(4, 1) LMX_TP(8, 1)
+#undef LMX_TP
+  return fail(LMX_ERR_UNSUPPORTED_FORMAT, "%d planes with %d scale stages", planes, stages);
+}
+
 }  // namespace
 }  // namespace lmx
 
 extern "C" int lmx_hbm_read_probe(const void *buf, size_t bytes, unsigned *sink, void *stream) {
+  return lmx_hbm_read_probe_shape(buf, bytes, 2, 512, sink, stream);
+}
+
+extern "C" int lmx_hbm_read_probe_shape(const void *buf, size_t bytes, int loads_in_flight, int workgroups,
+                                        unsigned *sink, void *stream) {
   using namespace lmx;
   if (!buf || !sink) return fail(LMX_ERR_INVALID_ARGUMENT, "NULL argument");
   if (reinterpret_cast<size_t>(buf) % 16 || bytes % 16)
     return fail(LMX_ERR_INVALID_ARGUMENT, "buffer and size must be 16-byte multiples");
+  if (workgroups < 1 || workgroups > 65536) return fail(LMX_ERR_INVALID_ARGUMENT, "workgroups %d", workgroups);
   if (bytes == 0) return LMX_OK;
-  read_probe_kernel<<<dim3(512), dim3(1024), 0, static_cast<hipStream_t>(stream)>>>(
-      static_cast<const u32x4 *>(buf), bytes / 16, sink);
+  return launch_read(buf, bytes, loads_in_flight, workgroups, sink, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int lmx_hbm_read_probe_tiles(const void *tiles, const float *scales, int format, size_t rows, size_t cols,
+                                        size_t group, unsigned *sink, void *stream) {
+  using namespace lmx;
+  FormatInfo fi;
+  if (!format_info(format, &fi)) return fail(LMX_ERR_UNSUPPORTED_FORMAT, "unknown format %d", format);
+  if (!tiles || !scales || !sink) return fail(LMX_ERR_INVALID_ARGUMENT, "NULL argument");
+  if (reinterpret_cast<size_t>(tiles) % 16 || reinterpret_cast<size_t>(scales) % 4)
+    return fail(LMX_ERR_INVALID_ARGUMENT, "tiles must be 16-byte and scales 4-byte aligned");
+  if (rows == 0 || cols == 0 || rows > (1u << 24)) return fail(LMX_ERR_INVALID_ARGUMENT, "shape %zu x %zu", rows, cols);
+  if (group >= round_up(cols, kRotChunk)) group = 0;
+  if (group && group % kChunk) return fail(LMX_ERR_INVALID_ARGUMENT, "group %zu", group);
+  lmx_weight w;   // the layouts lmx_tile_planes / lmx_tile_scales produce for this shape
+  plan_weight(&w, format, rows, cols, group);
+  const size_t Npad = w.Npad, Kc = w.Kp / kChunk, gc = w.group / kChunk, n_groups = w.n_groups;
+  const size_t cps = (Kc + 31) / 32;   // 16 waves x 2 half-waves per step
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  int r;
+  switch (cps) {
+  case 1: r = launch_tiles_fmt<1>(fi.planes, fi.stages, tiles, scales, int(Npad), int(Kc), int(n_groups), int(gc), sink, st); break;
+  case 2: r = launch_tiles_fmt<2>(fi.planes, fi.stages, tiles, scales, int(Npad), int(Kc), int(n_groups), int(gc), sink, st); break;
+  case 3: r = launch_tiles_fmt<3>(fi.planes, fi.stages, tiles, scales, int(Npad), int(Kc), int(n_groups), int(gc), sink, st); break;
+  case 4: r = launch_tiles_fmt<4>(fi.planes, fi.stages, tiles, scales, int(Npad), int(Kc), int(n_groups), int(gc), sink, st); break;
+  default: return fail(LMX_ERR_INVALID_ARGUMENT, "K = %zu: the tile probe covers K <= 16384", cols);
+  }
+  if (r) return r;
   hipError_t e = hipGetLastError();
-  return e == hipSuccess ? LMX_OK : fail(LMX_ERR_LAUNCH_FAILED, "read probe launch: %s", hipGetErrorString(e));
+  return e == hipSuccess ? LMX_OK : fail(LMX_ERR_LAUNCH_FAILED, "tile probe launch: %s", hipGetErrorString(e));
 }

@@ -32,6 +32,7 @@
 // fallback).
 #include <hip/hip_runtime.h>
 
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <memory>
@@ -52,6 +53,17 @@ constexpr size_t kSampleBlocks = 256;
 // block count and up to kSampleBlocks whole blocks: ~10 us for 256 blocks of
 // 132 bytes on one host core, where a byte-wise pass took ~49 us of every
 // call.
+// LMX_HOST_HASH=all (read once) hashes every block instead of the sample,
+// for callers that rewrite weights in place without lmx_host_forget: every
+// call then pays a pass over the whole array (~1 ms per 2 MB on one core).
+bool hash_all_blocks() {
+  static const bool all = [] {
+    const char *e = std::getenv("LMX_HOST_HASH");
+    return e && std::strcmp(e, "all") == 0;
+  }();
+  return all;
+}
+
 uint64_t fingerprint(const void *blocks, size_t num_blocks, size_t block_bytes) {
   uint64_t h = 1469598103934665603ull;
   auto mix = [&h](const uint8_t *p, size_t n) {
@@ -66,7 +78,7 @@ uint64_t fingerprint(const void *blocks, size_t num_blocks, size_t block_bytes) 
   };
   mix(reinterpret_cast<const uint8_t *>(&num_blocks), sizeof num_blocks);
   const uint8_t *b = static_cast<const uint8_t *>(blocks);
-  const size_t n = num_blocks < kSampleBlocks ? num_blocks : kSampleBlocks;
+  const size_t n = num_blocks < kSampleBlocks || hash_all_blocks() ? num_blocks : kSampleBlocks;
   for (size_t i = 0; i < n; ++i) {
     const size_t j = n > 1 ? i * (num_blocks - 1) / (n - 1) : 0;
     mix(b + j * block_bytes, block_bytes);
@@ -239,6 +251,32 @@ int lmx_host_precompute_luts(const float *activations, size_t n, float *luts) {
       (st = lmx_precompute_luts(g_stage.d_in, n, LMX_ROTATE_NONE, g_stage.d_out, g_stage.stream)))
     return st;
   return d2h_sync(luts, g_stage.d_out, groups * 16);
+}
+
+int lmx_host_precompute_lut(const float *activations, float *lut) {
+  return lmx_host_precompute_luts(activations, 4, lut);
+}
+
+int lmx_host_extract_indices(const uint8_t *sign_plane, const uint8_t *zero_plane, size_t group_idx,
+                             uint8_t *pos_idx, uint8_t *neg_idx) {
+  if (!sign_plane || !zero_plane || !pos_idx || !neg_idx) return lmx::fail(LMX_ERR_INVALID_ARGUMENT, "NULL pointer");
+  // The device kernel reads group g from byte g/2 (high nibble for even g):
+  // pass the group's byte and ask for groups 0..group_idx%2 of it.
+  const size_t n = group_idx % 2 + 1;
+  uint8_t in[8] = {sign_plane[group_idx / 2], 0, 0, 0, zero_plane[group_idx / 2], 0, 0, 0};
+  uint8_t out[8] = {};
+  int st;
+  if ((st = stage_stream()) || (st = ensure(&g_stage.d_in, &g_stage.n_in, 2)) ||
+      (st = ensure(&g_stage.d_out, &g_stage.n_out, 2)) ||
+      (st = h2d(g_stage.d_in, reinterpret_cast<const float *>(in), 2)))
+    return st;
+  uint8_t *d_in = reinterpret_cast<uint8_t *>(g_stage.d_in), *d_out = reinterpret_cast<uint8_t *>(g_stage.d_out);
+  if ((st = lmx_extract_indices(d_in, d_in + 4, n, d_out, d_out + 4, g_stage.stream)) ||
+      (st = d2h_sync(reinterpret_cast<float *>(out), g_stage.d_out, 2)))
+    return st;
+  *pos_idx = out[n - 1];
+  *neg_idx = out[4 + n - 1];
+  return LMX_OK;
 }
 
 }  // extern "C"

@@ -218,6 +218,11 @@ class _DecoderOps:
         t = np.ascontiguousarray(tokens, np.int32)
         check(lib().lmx_decoder_reset(self._h, _np_ptr(t), t.size // self.batch))
 
+    def set_repetition_penalty(self, penalty):
+        """The reference's repetition penalty in the greedy pick (1 = off), from the
+        next reset or generate on (lmx_decoder_set_repetition_penalty)."""
+        check(lib().lmx_decoder_set_repetition_penalty(self._h, penalty))
+
     def step(self, logits=None, stream=None):
         """One forward step at the current position; logits (device float32 tensor of
         vocab entries, batch x vocab for a batched decoder) receives the step's logits

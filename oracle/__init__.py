@@ -220,6 +220,32 @@ class OracleDecoder:
         return logits
 
 
+def greedy_pick(logits, history, penalty=1.0):
+    """Greedy Model::sample (src/model.cpp:455-490 with temperature 0): the
+    repetition penalty of :458-469 -- for every token of the history, once per
+    occurrence, a positive logit is divided by the penalty and any other
+    multiplied by it -- then the first maximum (:480-490).  Returns (token,
+    penalised logits).  Pinned to the reference's own sample() by
+    tests/test_decode_cpu.py."""
+    v = f32(logits).copy()
+    if penalty != 1.0:
+        p = np.float32(penalty)
+        for t in history:
+            if 0 <= t < v.size:
+                v[t] = v[t] / p if v[t] > 0 else v[t] * p
+    return int(np.argmax(v)), v
+
+
+def ref_greedy_pick(logits, history, penalty):
+    """The reference's own Model::sample, greedy (oracle/_ref): (token, penalised logits)."""
+    R = RefDecoder._bind()
+    lg = f32(logits)
+    h = np.ascontiguousarray(history, np.int32)
+    out = np.zeros_like(lg)
+    t = R.ref_greedy_sample(_ptr(lg), lg.size, _ptr(h), h.size, penalty, _ptr(out))
+    return t, out
+
+
 _SPREAD = None
 
 
@@ -261,6 +287,7 @@ class RefDecoder:
             ("ref_model_load", [ctypes.c_char_p], _p),
             ("ref_model_forward", [_p, ctypes.c_int, _sz, _p], None),
             ("ref_model_destroy", [_p], None),
+            ("ref_greedy_sample", [_p, _sz, _p, _sz, ctypes.c_float, _p], ctypes.c_int),
         ]:
             f = getattr(R, name)
             f.argtypes, f.restype = args, res

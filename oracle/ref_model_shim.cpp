@@ -7,6 +7,7 @@
 // (src/model.cpp:576-701): 4-bit linears as Int4Block vectors, the tied
 // lm_head as a copy of the 4-bit embedding (model.cpp:667-689), norms, and
 // Model::allocate() for the KV cache and buffers.
+#include <algorithm>
 #include <cstring>
 #include <memory>
 
@@ -159,5 +160,22 @@ void ref_model_forward(void *mp, int token, size_t pos, float *logits) {
 }
 
 void ref_model_destroy(void *mp) { delete static_cast<Model *>(mp); }
+
+// Model::sample (model.cpp:455-490) in its greedy form (temperature 0) over
+// the given logits and token history: the repetition penalty, then the first
+// maximum.  logits_out receives the penalised logits the pick ranked.
+int ref_greedy_sample(const float *logits, size_t vocab, const int *history, size_t n_hist, float penalty,
+                      float *logits_out) {
+  Model m;
+  m.config.vocab_size = vocab;
+  m.logits.assign(logits, logits + vocab);
+  m.generated_tokens.assign(history, history + n_hist);
+  GenerationConfig g;
+  g.repetition_penalty = penalty;
+  g.temperature = 0.0f;
+  const int t = m.sample(g);
+  std::copy(m.logits.begin(), m.logits.end(), logits_out);
+  return t;
+}
 
 }  // extern "C"

@@ -96,6 +96,21 @@ int main() {
     bool ok = true;
     for (int i = 0; i < 16; ++i) ok = ok && t[i] == want[i];
     report("precompute_luts KAT", ok, t[15], 10.0);
+    float t1[16];
+    lutmac_hip::precompute_lut(a, t1);   // one group (lut_gemm.hpp:30-44)
+    ok = true;
+    for (int i = 0; i < 16; ++i) ok = ok && t1[i] == want[i];
+    report("precompute_lut KAT", ok, t1[15], 10.0);
+  }
+  // test_lut_gemm.cpp:57-88 restated: weights [+1, -1, 0, +1] -> pos 0b1001,
+  // neg 0b0100; the same nibbles in group 1 (low nibble of byte 0).
+  {
+    const uint8_t sign[4] = {0b01000100, 0, 0, 0}, zero[4] = {0b00100010, 0, 0, 0};
+    uint8_t pos = 0, neg = 0;
+    lutmac_hip::extract_indices(sign, zero, 0, pos, neg);
+    uint8_t pos1 = 0, neg1 = 0;
+    lutmac_hip::extract_indices(sign, zero, 1, pos1, neg1);
+    report("extract_indices KAT", pos == 0b1001 && neg == 0b0100 && pos1 == 0b1001 && neg1 == 0b0100, pos, 9.0);
   }
   std::printf("%d failure(s)\n", failures);
   return failures ? 1 : 0;

@@ -7,6 +7,8 @@
   fixes (unchanged high frequencies, low frequencies / factor, continuity).
 * The 4-bit producer (lmx_quantize_int4) against the reference's own
   quantize_tensor_int4 (quantize.hpp:437-461) and a numpy restatement.
+* The greedy pick with the repetition penalty (oracle.greedy_pick) against
+  the reference's own Model::sample (src/model.cpp:455-490).
 """
 import ctypes
 
@@ -189,3 +191,38 @@ def test_lutmac_loader_rejects_bad_files(tmp_path):
     raw = b"LUTMAC01" + (3).to_bytes(4, "little") + (2).to_bytes(4, "little") + b"{}"
     p.write_bytes(raw)                                                        # version 3
     assert L.lib().lmx_model_load(str(p).encode(), 0, ctypes.byref(h)) == L.ERR_UNSUPPORTED_FORMAT
+
+
+@needs_ref
+@pytest.mark.parametrize("penalty", [1.0, 1.1, 1.7])
+def test_greedy_pick_matches_reference_sample(penalty):
+    # The reference's sample() penalises the history's tokens (once per
+    # occurrence, sign-dependent) before its first-maximum scan; the oracle's
+    # restatement must rank the same values and pick the same token.  The
+    # reference is built with -ffast-math, which may turn the division into a
+    # multiplication by 1/penalty: 1 ulp per application is allowed.
+    rng = np.random.default_rng(int(penalty * 10))
+    for trial in range(40):
+        vocab = 300
+        lg = rng.standard_normal(vocab).astype(np.float32) * 3
+        lg[rng.integers(0, vocab, 5)] = 0.0
+        hist = rng.integers(0, vocab, rng.integers(0, 60))
+        top = int(np.argmax(lg))
+        hist = np.r_[hist, [top] * int(rng.integers(0, 4))].astype(np.int32)   # the raw maximum repeats
+        t_ref, v_ref = oracle.ref_greedy_pick(lg, hist, penalty)
+        t_orc, v_orc = oracle.greedy_pick(lg, hist, penalty)
+        counts = np.bincount(hist, minlength=vocab)
+        assert np.allclose(v_orc, v_ref, rtol=2e-7 * (1 + counts), atol=0)
+        assert t_orc == t_ref or abs(v_orc[t_orc] - v_orc[t_ref]) <= 1e-6 * abs(v_orc[t_orc])
+    # the closed form on one token: 3 occurrences of a positive and a negative logit
+    lg = np.array([2.0, -2.0, 1.0], np.float32)
+    _, v = oracle.greedy_pick(lg, [0, 0, 0, 1, 1, 1], 2.0)
+    assert v.tolist() == [0.25, -16.0, 1.0]
+    assert oracle.greedy_pick(lg, [0, 0, 0, 1, 1, 1], 2.0)[0] == 2
+
+
+def test_greedy_pick_penalty_one_is_argmax():
+    rng = np.random.default_rng(3)
+    lg = rng.standard_normal(500).astype(np.float32)
+    lg[10] = lg[20] = lg.max() + 1   # tie: the first maximum
+    assert oracle.greedy_pick(lg, rng.integers(0, 500, 30), 1.0)[0] == 10

@@ -25,6 +25,29 @@ def test_lut_precomputation(cuda):
     assert t.tolist() == [0, 4, 3, 7, 2, 6, 5, 9, 1, 5, 4, 8, 3, 7, 6, 10]
 
 
+def test_precompute_lut_kat(cuda):
+    # test_lut_gemm.cpp:17-55 through the single-group drop-in (lut_gemm.hpp:30-44)
+    t = L.host_precompute_lut(np.array([1, 2, 3, 4], np.float32))
+    assert t.tolist() == [0, 4, 3, 7, 2, 6, 5, 9, 1, 5, 4, 8, 3, 7, 6, 10]
+    a = np.array([0.1, -2.5, 3e-3, 7.0], np.float32)
+    assert np.array_equal(L.host_precompute_lut(a), oracle.precompute_luts(a))
+
+
+def test_extract_indices_kat(cuda):
+    # test_lut_gemm.cpp:57-88: weights [+1, -1, 0, +1] -> pos 0b1001, neg 0b0100
+    sign = np.array([0b01000000, 0, 0, 0], np.uint8)
+    zero = np.array([0b00100000, 0, 0, 0], np.uint8)
+    assert L.host_extract_indices(sign, zero, 0) == (0b1001, 0b0100)
+    # every nibble pair, even and odd groups, against the closed form
+    rng = np.random.default_rng(5)
+    s, z = rng.integers(0, 256, 8, dtype=np.uint8), rng.integers(0, 256, 8, dtype=np.uint8)
+    for g in range(16):
+        sh = 4 if g % 2 == 0 else 0
+        sn, zn = (int(s[g // 2]) >> sh) & 0xF, (int(z[g // 2]) >> sh) & 0xF
+        nz = ~zn & 0xF
+        assert L.host_extract_indices(s, z, g) == (nz & ~sn & 0xF, nz & sn), g
+
+
 def test_gemv_correctness_ternary_all_ones(cuda):
     # test_lut_gemm.cpp:135-165: +1 weights, x = [1,2,3,4] -> 10 (scale 1)
     blk = np.zeros(68, np.uint8)
