@@ -632,7 +632,7 @@ def main():
         r["frac_of_achievable"] = round(r["GB_per_s"] / a["achievable_GB_per_s"], 4)
     print("# achievable (plain reads of the same bytes): " + ", ".join(
         f"{k} {v['us_per_read']} us (best shape {v['best_shape']} {v['best_us']} us, tile schedule "
-        f"{v.get('tile_schedule_us')} us)" for k, v in achievable.items() if "us_per_read" in v),
+        f"{v.get('tile_schedule_us')} us)" for k, v in achievable.items() if isinstance(v, dict) and "us_per_read" in v),
         file=sys.stderr, flush=True)
     del flush
     decode = None
