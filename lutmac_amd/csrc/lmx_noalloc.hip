@@ -91,12 +91,15 @@ extern "C" int lmx_gemv_tiles_noalloc(int format, const void *tiles, const float
   w.batched = false;   // one vector at a time: the batched kernel's partials would not fit
   const size_t row_blocks = w.Npad / kWave;
   const size_t staging = round_up(w.Kp * sizeof(float), 256);
-  const size_t partials = w.fullk ? 0 : (w.Kp / size_t(w.kslice)) * w.Npad * sizeof(float);
-  if ((!w.fullk && row_blocks * sizeof(unsigned) > kCounterBytes) || kCounterBytes + staging + partials > kScratchBytes)
+  // split-K plans, and the layered full-K plan (which runs the split-K
+  // kernel where it has no kernel form), need partials and ticket counters
+  const bool splitk = !w.fullk || w.fullk == kFullK_8x8x2L;
+  const size_t partials = splitk ? (w.Kp / size_t(w.kslice)) * w.Npad * sizeof(float) : 0;
+  if ((splitk && row_blocks * sizeof(unsigned) > kCounterBytes) || kCounterBytes + staging + partials > kScratchBytes)
     return fail(LMX_ERR_INVALID_ARGUMENT,
                 "%zu x %zu needs %zu B of scratch (ticket counters %zu B of %zu, x staging, split-K partials); "
                 "lmx_gemv_tiles_noalloc holds %zu B per GPU: use a weight handle (lmx_gemv)",
-                rows, cols, kCounterBytes + staging + partials, w.fullk ? size_t(0) : row_blocks * sizeof(unsigned),
+                rows, cols, kCounterBytes + staging + partials, splitk ? row_blocks * sizeof(unsigned) : size_t(0),
                 kCounterBytes, kScratchBytes);
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
