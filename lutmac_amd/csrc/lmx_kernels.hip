@@ -766,7 +766,8 @@ template <int FMT, int WAVES, int H, int CPS, bool LAY = false>
 static int launch_plain_cfg(const GemvArgs &a, hipStream_t st) {
   // Interleaved where it measured faster: two k-slices per wave and at least
   // two steps per wave (one step has nothing to interleave; 17920 x 1536
-  // ran 40% slower that way), RRQ-3 excepted (4% slower at 8192^2).
+  // ran 40% slower that way).  RRQ-3 too since the first-step priority
+  // (8192^2 -1.6 %; it had been 4 % slower).
   if (a.epi == kEpiSiluPair) {
     // gate|up of the decode step: RMSNorm in, SiLU(gate)*up out (4-bit, unrotated)
     if constexpr (FMT == LMX_FMT_INT4)
@@ -787,7 +788,7 @@ static int launch_plain_cfg(const GemvArgs &a, hipStream_t st) {
     }
     return 1;
   }
-  if constexpr (!LAY && H == 2 && CPS >= 2 && FMT != LMX_FMT_RRQ3) {
+  if constexpr (!LAY && H == 2 && CPS >= 2) {
     if (a.kfamily != kKernelLean) {
       const int r = a.rotate == LMX_ROTATE_FWHT256 ? launch_ipl_kernel<FMT, true, WAVES, CPS>(a, st)
                                                    : launch_ipl_kernel<FMT, false, WAVES, CPS>(a, st);
