@@ -631,7 +631,16 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_ipl_kernel(GemvArgs a)
   // first step last and only then requested the rest: its late loads and a
   // tail of lookups alone on the SIMD ended the kernel (measured: int4 8192^2
   // -4.5 %, ternary -8.7 %, binary -5 %, same bits).
-  __builtin_amdgcn_s_setprio(1);
+  // AGE: past the first step the younger waves outrank the older ones
+  // (priority wave / 4, the first step at 3), so the wave whose weights
+  // came last is not also served last; measured int4 -1.1 %, int8 -1.6 %,
+  // RRQ-2 -1.9 %, RRQ-3 -2.5 %, but ternary +1.3 % and binary +2.2 %.
+  constexpr bool AGE = FMT != LMX_FMT_TERNARY && FMT != LMX_FMT_BINARY;
+  if constexpr (AGE)
+    __builtin_amdgcn_s_setprio(3);
+  else
+    __builtin_amdgcn_s_setprio(1);
+  const int wave_s = __builtin_amdgcn_readfirstlane(wave);
   float4 xr[CPS];
 #pragma unroll
   for (int c = 0; c < CPS; ++c) xr[c] = load_x4_raw(a.x, min(c2base + c, C2n - 1) * kRotChunk, a.cols, lane);
@@ -703,7 +712,25 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_ipl_kernel(GemvArgs a)
 #pragma unroll
       for (int cc = 1; cc < CPS; ++cc) load_planes(cc);
       __builtin_amdgcn_sched_barrier(0);
-      __builtin_amdgcn_s_setprio(0);
+      if constexpr (AGE) {
+        // priority wave / 4, in one asm block: a branch on the wave index
+        // here splits the unrolled step loop and the compiler spills
+        asm volatile(
+            "s_setprio 0\n"
+            "s_cmp_ge_u32 %0, 4\n"
+            "s_cbranch_scc0 1f\n"
+            "s_setprio 1\n"
+            "s_cmp_ge_u32 %0, 8\n"
+            "s_cbranch_scc0 1f\n"
+            "s_setprio 2\n"
+            "s_cmp_ge_u32 %0, 12\n"
+            "s_cbranch_scc0 1f\n"
+            "s_setprio 3\n"
+            "1:" ::"s"(wave_s)
+            : "scc");
+      } else {
+        __builtin_amdgcn_s_setprio(0);
+      }
     }
     float xs = 0.0f;
     if constexpr (Fmt<FMT>::XS) xs = xsum[min(ch, Kc - 1)];
