@@ -421,10 +421,13 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_fullk_kernel(GemvArgs 
 // consecutive ones), and chunk ch keeps its tables at ch * kIplChunkBytes,
 // back to back: the last layer may be ragged (K = 8960 = 70 chunks on 64
 // slices: 6 slices do two chunks), and 70 chunks' tables fit the LDS.
-template <int FMT, bool ROT, int WAVES, int H, int CPS, int XM, int EPI = kEpiStore, bool LAY = false>
+template <int FMT, bool ROT, int WAVES, int H, int CPS, int XM, int EPI = kEpiStore, bool LAY = false, bool PS = false>
 __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_plain_kernel(GemvArgs a) {
   constexpr int P = Fmt<FMT>::P, NA = Fmt<FMT>::NA, S = Fmt<FMT>::S;
-  constexpr int RW = kWave / H;
+  // PS (4-bit): the four planes of a row's chunk split over two lanes, planes
+  // 0-1 and 2-3 (half the lookups per lane, half the rows per workgroup)
+  static_assert(!PS || (FMT == LMX_FMT_INT4 && !LAY && EPI == kEpiStore), "plane split: 4-bit, plain store");
+  constexpr int RW = kWave / H / (PS ? 2 : 1);
   constexpr bool PAIR = EPI == kEpiSiluPair;
   constexpr int HR = RW / 2;   // PAIR: gate rows (then as many up rows) per workgroup
   constexpr int NS = WAVES * H;
@@ -442,7 +445,8 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_plain_kernel(GemvArgs 
 
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
-  const int s = wave * H + lane / RW;
+  const int s = wave * H + (PS ? (lane / RW) >> 1 : lane / RW);
+  const int part = PS ? (lane / RW) & 1 : 0;   // PS: planes 2*part, 2*part + 1
   const int rl = lane % RW;
   // PAIR: the workgroup's rows are gate rows blockIdx.x*HR + [0, HR) and the
   // up rows rows/2 + blockIdx.x*HR + [0, HR) (the host checks rows/2 % HR == 0)
@@ -469,14 +473,16 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_plain_kernel(GemvArgs 
   __builtin_amdgcn_s_barrier();   // every wave's x requests ahead of the weight stream
 
   // ---- weights (chunk 0 now, the rest after the prologue) and scales ----
-  u32x4 w[CPS][P];
+  constexpr int PL = PS ? 2 : P;   // planes a lane loads
+  u32x4 w[CPS][PL];
   float sc[CPS][S];
   const u32x4 *__restrict__ pl = reinterpret_cast<const u32x4 *>(a.planes);
   const uint32_t Npad = uint32_t(a.Npad);
   auto load_planes = [&](int c) {
     const uint32_t ch = uint32_t(min(chunk_of(c), Kc - 1));
 #pragma unroll
-    for (int p = 0; p < P; ++p) w[c][p] = __builtin_nontemporal_load(pl + ((ch * P + p) * Npad + uint32_t(lr)));
+    for (int p = 0; p < PL; ++p)
+      w[c][p] = __builtin_nontemporal_load(pl + ((ch * P + uint32_t(PS ? 2 * part + p : p)) * Npad + uint32_t(lr)));
   };
   load_planes(0);
 #pragma unroll
@@ -546,21 +552,38 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_plain_kernel(GemvArgs 
     const uint32_t shift = slice_shift<H>(s) * 0x01010101u;
 #pragma unroll
     for (int c = 0; c < CPS; ++c) {
-      float A[NA];
-#pragma unroll
-      for (int i = 0; i < NA; ++i) A[i] = 0.0f;
-      if constexpr (LAY)
-        chunk_lookups<FMT, true>(w[c], tbase + uint32_t(min(chunk_of(c), Kc - 1)) * kIplChunkBytes, shift, A);
-      else
-        chunk_lookups<FMT, true>(w[c], tbase, shift, A, c * kStagChunkBytes);
       const int ch = chunk_of(c);
-      float xs = 0.0f;
-      if constexpr (Fmt<FMT>::XS) xs = xsum[min(ch, Kc - 1)];
       float scl[S];
 #pragma unroll
       for (int t = 0; t < S; ++t) scl[t] = sc[c][t] * kScale;
-      const float nacc = finish_chunk<FMT>(A, xs, scl, acc);
-      acc = ch < Kc ? nacc : acc;
+      if constexpr (PS) {
+        // two planes as a 2-plane format; the third plane of the 4-bit
+        // identity enters inverted, and the part's terms of
+        // ((A0 + 2 A1) + 4 A2) - 8 A3 weight its two sums
+        u32x4 wl[2] = {w[c][0], w[c][1]};
+        const uint32_t inv = part ? 0xFFFFFFFFu : 0u;
+        wl[1].x ^= inv;
+        wl[1].y ^= inv;
+        wl[1].z ^= inv;
+        wl[1].w ^= inv;
+        float A2[2] = {0.0f, 0.0f};
+        chunk_lookups<LMX_FMT_RRQ2, true>(wl, tbase, shift, A2, c * kStagChunkBytes);
+        const float c0 = part ? 4.0f : 1.0f, c1 = part ? -8.0f : 2.0f;
+        const float nacc = fmaf(scl[0], c0 * A2[0] + c1 * A2[1], acc);
+        acc = ch < Kc ? nacc : acc;
+      } else {
+        float A[NA];
+#pragma unroll
+        for (int i = 0; i < NA; ++i) A[i] = 0.0f;
+        if constexpr (LAY)
+          chunk_lookups<FMT, true>(w[c], tbase + uint32_t(min(chunk_of(c), Kc - 1)) * kIplChunkBytes, shift, A);
+        else
+          chunk_lookups<FMT, true>(w[c], tbase, shift, A, c * kStagChunkBytes);
+        float xs = 0.0f;
+        if constexpr (Fmt<FMT>::XS) xs = xsum[min(ch, Kc - 1)];
+        const float nacc = finish_chunk<FMT>(A, xs, scl, acc);
+        acc = ch < Kc ? nacc : acc;
+      }
     }
   }
 
@@ -763,18 +786,32 @@ constexpr size_t plain_lds_bytes(size_t Kc) {
          (LAY ? Kc * kIplChunkBytes : (Kc + CPS - 1) / CPS * stag_slice_bytes(CPS));
 }
 
-template <int FMT, bool ROT, int WAVES, int H, int CPS, int XM, int EPI = kEpiStore, bool LAY = false>
+template <int FMT, bool ROT, int WAVES, int H, int CPS, int XM, int EPI = kEpiStore, bool LAY = false, bool PS = false>
 static int launch_plain_kernel(const GemvArgs &a, hipStream_t st) {
   const size_t lds = plain_lds_bytes<WAVES, H, CPS, LAY>(size_t(a.Kp / kChunk));
   if (lds > kMaxLdsBytes) return 1;   // staggered tables do not fit: the generic kernel serves it
   static const hipError_t attr = hipFuncSetAttribute(
-      reinterpret_cast<const void *>(&lut_gemv_plain_kernel<FMT, ROT, WAVES, H, CPS, XM, EPI, LAY>),
+      reinterpret_cast<const void *>(&lut_gemv_plain_kernel<FMT, ROT, WAVES, H, CPS, XM, EPI, LAY, PS>),
       hipFuncAttributeMaxDynamicSharedMemorySize, int(kMaxLdsBytes));
   if (attr != hipSuccess) return fail(LMX_ERR_LAUNCH_FAILED, "hipFuncSetAttribute: %s", hipGetErrorString(attr));
-  constexpr int RW = kWave / H;
+  constexpr int RW = kWave / H / (PS ? 2 : 1);
   const int blocks = EPI == kEpiSiluPair ? a.rows / RW : (a.Npad + RW - 1) / RW;
-  lut_gemv_plain_kernel<FMT, ROT, WAVES, H, CPS, XM, EPI, LAY><<<dim3(blocks), dim3(WAVES * kWave), lds, st>>>(a);
+  lut_gemv_plain_kernel<FMT, ROT, WAVES, H, CPS, XM, EPI, LAY, PS><<<dim3(blocks), dim3(WAVES * kWave), lds, st>>>(a);
   return LMX_OK;
+}
+
+// 4-bit launches that split each chunk's planes over two lanes (LMX_PS: 0
+// none, 1 the 4 x 4 x 1 plan (default), 2 also 8 x 8 x 1).
+static int plane_split() {
+  const char *e = std::getenv("LMX_PS");
+  return e ? std::atoi(e) : 1;
+}
+template <int WAVES, int H, int CPS, bool LAY>
+static bool plane_split_plan() {
+  if constexpr (LAY || CPS != 1) return false;
+  if constexpr (WAVES == 4 && H == 4) return plane_split() >= 1;
+  if constexpr (WAVES == 8 && H == 8) return plane_split() >= 2;
+  return false;
 }
 
 template <int FMT, bool ROT, int WAVES, int CPS>
@@ -807,6 +844,9 @@ static int launch_plain_cfg(const GemvArgs &a, hipStream_t st) {
     // unrotated); other formats take the generic kernel.
     if constexpr (FMT == LMX_FMT_INT4) {
       if (a.rotate == LMX_ROTATE_NONE) {
+        if constexpr (!LAY && CPS == 1)
+          if (a.xmode == kXModeRmsNorm && plane_split_plan<WAVES, H, CPS, LAY>())
+            return launch_plain_kernel<FMT, false, WAVES, H, CPS, kXModeRmsNorm, kEpiStore, LAY, true>(a, st);
         switch (a.xmode) {
         case kXModeRmsNorm: return launch_plain_kernel<FMT, false, WAVES, H, CPS, kXModeRmsNorm, kEpiStore, LAY>(a, st);
         case kXModeSiluMul: return launch_plain_kernel<FMT, false, WAVES, H, CPS, kXModeSiluMul, kEpiStore, LAY>(a, st);
@@ -823,6 +863,9 @@ static int launch_plain_cfg(const GemvArgs &a, hipStream_t st) {
     }
   }
   if (a.rotate == LMX_ROTATE_FWHT256) return launch_plain_kernel<FMT, true, WAVES, H, CPS, kXModeNone, kEpiStore, LAY>(a, st);
+  if constexpr (FMT == LMX_FMT_INT4 && !LAY && CPS == 1)
+    if (plane_split_plan<WAVES, H, CPS, LAY>())
+      return launch_plain_kernel<FMT, false, WAVES, H, CPS, kXModeNone, kEpiStore, LAY, true>(a, st);
   return launch_plain_kernel<FMT, false, WAVES, H, CPS, kXModeNone, kEpiStore, LAY>(a, st);
 }
 

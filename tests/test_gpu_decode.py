@@ -42,8 +42,12 @@ def check_against(dec, ref, tokens, tol=DECODE_TOL):
         assert err < tol, f"step {pos}: rel err {err:.3e}"
 
 
+@pytest.mark.parametrize("ps", ["0", "1"])
 @pytest.mark.parametrize("rope_mode", [D.ROPE_LLAMA3, D.ROPE_REFERENCE])
-def test_decoder_matches_oracle_small(cuda, rope_mode):
+def test_decoder_matches_oracle_small(cuda, monkeypatch, rope_mode, ps):
+    # LMX_PS: the 4 x 4 x 1 linears (RMSNorm fused) with and without the
+    # plane split
+    monkeypatch.setenv("LMX_PS", ps)
     cfg = D.small_config(rope_mode=rope_mode, rope_factor=32.0 if rope_mode == D.ROPE_LLAMA3 else 4.0,
                          rope_orig_max_pos=64, rope_theta=10000.0)
     m = D.SyntheticModel(cfg, seed=11, group=128, random_norms=True)

@@ -248,6 +248,23 @@ def test_forced_kernel_plans(cuda, monkeypatch, fmt, cfg, staged, family):
     assert rel_max_err(y, ref) < TOL
 
 
+# The 4 x 4 x 1 plan of an unrotated 4-bit GEMV splits each chunk's four
+# planes over two lanes (LMX_PS=1, the default; 0 keeps one lane per row and
+# chunk): both forms against the oracle, ragged and full workgroups.
+@pytest.mark.parametrize("ps", ["0", "1"])
+@pytest.mark.parametrize("rows,cols", [(33, 2048), (300, 640), (2048, 2048), (3072, 2048), (1536, 1536)])
+def test_int4_plane_split(cuda, monkeypatch, ps, rows, cols):
+    monkeypatch.setenv("LMX_PS", ps)
+    planes, scales, g = synth.make_weights(L.FMT_INT4, rows, cols, seed=rows + cols, group=128)
+    x = synth.make_activations(cols, seed=7, outliers=True)
+    w = L.Weight.from_planes(L.FMT_INT4, planes, scales, rows, cols, g)
+    assert w.kernel_config()[0] == 6, "the 4 x 4 x 1 plan"
+    y = w.gemv(dev(x), flags=L.ROTATE_NONE).cpu().numpy()
+    ref = oracle_planes_gemv(L.FMT_INT4, planes, scales, rows, cols, g, x, L.ROTATE_NONE)
+    assert rel_max_err(y, ref) < TOL
+    w.close()
+
+
 # ---- split-K reductions: last-workgroup ticket and two-pass ----------------
 @pytest.mark.parametrize("reduce", [0, 2])
 @pytest.mark.parametrize("kslice", [256, 512])
