@@ -53,6 +53,7 @@ int env_int(const char *name, int dflt) {
   return s ? std::atoi(s) : dflt;
 }
 
+
 int choose_waves() {
   const int env = env_int("LMX_WAVES", 4);
   return (env == 1 || env == 2 || env == 4) ? env : 4;
@@ -94,7 +95,13 @@ int choose_fullk(int fmt, size_t Npad, size_t Kp, int kfamily) {
   };
   if (env >= 0) return (env == 0 || !fits(env)) ? kFullK_None : env;
   const bool wide = env_int("LMX_FULLK_WIDE", 1) != 0;   // 0: auto never picks 8 rows x 64 slices
-  auto workgroups = [&](int cfg) { return Npad / size_t(kWave / fullk_shape(cfg).h); };
+  // 4-bit: the 16 x 4 x 1 plan splits its planes over two lanes (unrotated
+  // launches), 8 rows per workgroup
+  const bool ps16 = fmt == LMX_FMT_INT4 && plane_split_level() == 1;
+  auto workgroups = [&](int cfg) {
+    const size_t rows = size_t(kWave / fullk_shape(cfg).h) / (ps16 && cfg == kFullK_16x4x1 ? 2 : 1);
+    return Npad / rows;
+  };
   // Measured on MI355X (4-bit, decode shapes):
   //  * K <= 2048: 4 waves x 16 rows per workgroup wins from N = 256 up to
   //    ~8k rows (latency-bound small GEMVs want many small workgroups); up
@@ -133,6 +140,8 @@ int choose_reduce() {
 }
 
 }  // namespace
+
+int plane_split_level() { return env_int("LMX_PS", 1); }
 
 void plan_weight(lmx_weight *w, int fmt, size_t rows, size_t cols, size_t group) {
   FormatInfo fi;

@@ -170,6 +170,10 @@ constexpr int kReduceFenceAll = 1;  // same, with a device fence in every thread
 constexpr int kReduceTwoPass = 2;   // partials, then a separate reduce kernel
 
 int launch_gemv(int fmt, const GemvArgs &a, void *stream);
+// Plane split of unrotated 4-bit lean launches (LMX_PS, read per call): 1
+// the 4 x 4 x 1 and 16 x 4 x 1 plans (default), 2 the 4 x 4 x 1 plan only,
+// 0 neither.
+int plane_split_level();
 // Rows of one output half a workgroup covers with kEpiSiluPair for these
 // arguments (format, plan, transform), 0 when that epilogue is not served.
 int silu_pair_rows(int fmt, const GemvArgs &a);

@@ -800,17 +800,17 @@ static int launch_plain_kernel(const GemvArgs &a, hipStream_t st) {
   return LMX_OK;
 }
 
-// 4-bit launches that split each chunk's planes over two lanes (LMX_PS: 0
-// none, 1 the 4 x 4 x 1 plan (default), 2 also 8 x 8 x 1).
-static int plane_split() {
-  const char *e = std::getenv("LMX_PS");
-  return e ? std::atoi(e) : 1;
-}
+// Unrotated 4-bit launches of the 4 x 4 x 1 and 16 x 4 x 1 plans split each
+// chunk's planes over two lanes (plane_split_level(): 1, the default; 2 the
+// 4 x 4 x 1 plan only; 0 neither).  Splitting the 8 x 8 x 1 plan as well
+// (4 rows per workgroup, each building the whole K's tables) measured 9 %
+// slower in Llama decode, so the plan chooser takes 16 x 4 x 1 with 8 rows
+// per workgroup there instead (choose_fullk).
 template <int WAVES, int H, int CPS, bool LAY>
 static bool plane_split_plan() {
   if constexpr (LAY || CPS != 1) return false;
-  if constexpr (WAVES == 4 && H == 4) return plane_split() >= 1;
-  if constexpr (WAVES == 8 && H == 8) return plane_split() >= 2;
+  if constexpr (WAVES == 4 && H == 4) return plane_split_level() >= 1;
+  if constexpr (WAVES == 16 && H == 4) return plane_split_level() == 1;
   return false;
 }
 

@@ -100,19 +100,22 @@ def test_decoder_layered_head_takes_split_k(cuda):
             assert lg[out[pos + 1]] >= lg.max() - DECODE_TOL * np.linalg.norm(lg)
 
 
-@pytest.mark.parametrize("ffn", [768, 4096])
-def test_decoder_silu_pair_epilogue(cuda, monkeypatch, ffn):
+@pytest.mark.parametrize("ffn,ps", [(768, "1"), (4096, "1"), (4096, "2")])
+def test_decoder_silu_pair_epilogue(cuda, monkeypatch, ffn, ps):
     # gate|up writing SiLU(gate)*up itself (the 4-bit batch-1 step) against
     # the down projection forming it (LMX_SILU_PAIR=0): the same values, and
     # both within the bar of the oracle.  ffn 4096 gives down (512 x 4096)
-    # the 8-row x 64-slice plan
+    # 8 rows per workgroup: the 16 x 4 x 1 plan with its planes split over
+    # two lanes (the default), or the 8-row x 64-slice plan (LMX_PS=2: only
+    # the 4 x 4 x 1 plan splits)
+    monkeypatch.setenv("LMX_PS", ps)
     cfg = D.small_config(hidden=512, ffn=ffn, vocab=900, rope_mode=D.ROPE_REFERENCE, rope_factor=1.0,
                          rope_theta=1e6)
     m = D.SyntheticModel(cfg, seed=41 + ffn, group=128, random_norms=True)
     toks = np.random.default_rng(42).integers(0, cfg.vocab, 10)
     dec = D.Decoder(m)
     if ffn == 4096:
-        assert dec.weights[3].kernel_config()[0] == 7
+        assert dec.weights[3].kernel_config()[0] == (5 if ps == "1" else 7)
     paired = device_logits(dec, toks)
     monkeypatch.setenv("LMX_SILU_PAIR", "0")
     unpaired = device_logits(D.Decoder(m), toks)
