@@ -1379,10 +1379,13 @@ constexpr uint32_t quad_prefix_bytes(int waves, int h) {
   return (uint32_t(waves * h * 4 + waves * (kWave / h) * 4 + waves * 4) * 4 + 255) / 256 * 256;
 }
 
-template <int FMT, bool ROT, int WAVES, int H, int XM, int EPI>
+template <int FMT, bool ROT, int WAVES, int H, int XM, int EPI, bool PS = false>
 __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_quad_kernel(GemvArgs a) {
   constexpr int P = Fmt<FMT>::P, NA = Fmt<FMT>::NA, S = Fmt<FMT>::S;
-  constexpr int RW = kWave / H;
+  // PS (4-bit, unrotated): a row's chunk split over two lanes by planes, as
+  // in the lean kernel
+  static_assert(!PS || (FMT == LMX_FMT_INT4 && !ROT && EPI == kEpiStore), "plane split: 4-bit, plain store");
+  constexpr int RW = kWave / H / (PS ? 2 : 1);
   constexpr int NS = WAVES * H;
   constexpr int XJ = H / 2;
   constexpr bool PAIR = EPI == kEpiSiluPair;
@@ -1397,7 +1400,8 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_quad_kernel(GemvArgs a
   const int Kc = a.Kp / kChunk;
   const int C2n = a.Kp / kRotChunk;
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
-  const int s = wave * H + lane / RW;     // this lane's 128-chunk
+  const int s = wave * H + (PS ? (lane / RW) >> 1 : lane / RW);   // this lane's 128-chunk
+  const int part = PS ? (lane / RW) & 1 : 0;                       // PS: planes 2*part, 2*part + 1
   const int rl = lane % RW;
   const int row = PAIR ? (rl < HR ? 0 : a.rows / 2 - HR) + blockIdx.x * HR + rl : blockIdx.x * RW + rl;
   const int lr = min(row, a.Npad - 1);
@@ -1414,14 +1418,16 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_quad_kernel(GemvArgs a
   }
   __builtin_amdgcn_sched_barrier(0);
   __builtin_amdgcn_s_barrier();   // every wave's x requests ahead of the weight stream
-  u32x4 w[P];
+  constexpr int PL = PS ? 2 : P;   // planes a lane loads
+  u32x4 w[PL];
   float sc[S];
   {
     const u32x4 *__restrict__ pl = reinterpret_cast<const u32x4 *>(a.planes);
     const uint32_t Npad = uint32_t(a.Npad);
     const uint32_t ch = uint32_t(min(s, Kc - 1));
 #pragma unroll
-    for (int p = 0; p < P; ++p) w[p] = __builtin_nontemporal_load(pl + ((ch * P + p) * Npad + uint32_t(lr)));
+    for (int p = 0; p < PL; ++p)
+      w[p] = __builtin_nontemporal_load(pl + ((ch * P + uint32_t(PS ? 2 * part + p : p)) * Npad + uint32_t(lr)));
     const int g = a.gshift >= 0 ? int(ch) >> a.gshift : int(ch) / a.group_chunks;
 #pragma unroll
     for (int t = 0; t < S; ++t) sc[t] = a.scales[(uint32_t(t * a.n_groups + g)) * Npad + uint32_t(lr)];
@@ -1485,7 +1491,32 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_quad_kernel(GemvArgs a
 
   // ---- lookups over this lane's chunk for the 4 vectors ----
   float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  {
+  if constexpr (PS) {
+    // the two planes of this lane's part; the 4-bit identity's third plane
+    // enters inverted, and the part's terms of ((A0 + 2 A1) + 4 A2) - 8 A3
+    // weight the two sums
+    const int ch = min(s, Kc - 1);
+    const uint32_t cbase = lds_addr(lds) + PREFIX + uint32_t(ch) * kQuadChunkBytes;
+    const uint32_t inv = part ? 0xFFFFFFFFu : 0u;
+    float A[2][4];
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+#pragma unroll
+      for (int n = 0; n < 4; ++n) A[q][n] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t v[2] = {w[0][i], w[1][i] ^ inv};
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        word_lookups_batch<4>(v[q], i, cbase, A[q]);
+#pragma unroll
+        for (int n = 0; n < 4; ++n) asm volatile("" : "+v"(A[q][n]));
+      }
+    }
+    const float c0 = part ? 4.0f : 1.0f, c1 = part ? -8.0f : 2.0f;
+#pragma unroll
+    for (int n = 0; n < 4; ++n) acc[n] = s < Kc ? fmaf(sc[0], c0 * A[0][n] + c1 * A[1][n], 0.0f) : 0.0f;
+  } else {
     const int ch = min(s, Kc - 1);
     const uint32_t cbase = lds_addr(lds) + PREFIX + uint32_t(ch) * kQuadChunkBytes;   // 256-byte aligned
     float A[NA][4];
@@ -1555,22 +1586,37 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_quad_kernel(GemvArgs a
   }
 }
 
-template <int FMT, bool ROT, int WAVES, int H, int XM, int EPI>
+template <int FMT, bool ROT, int WAVES, int H, int XM, int EPI, bool PS = false>
 static int launch_quad_kernel(const GemvArgs &a, hipStream_t st) {
   const size_t lds = quad_prefix_bytes(WAVES, H) + size_t(a.Kp / kChunk) * kQuadChunkBytes;
   static const hipError_t attr =
-      hipFuncSetAttribute(reinterpret_cast<const void *>(&lut_gemv_quad_kernel<FMT, ROT, WAVES, H, XM, EPI>),
+      hipFuncSetAttribute(reinterpret_cast<const void *>(&lut_gemv_quad_kernel<FMT, ROT, WAVES, H, XM, EPI, PS>),
                           hipFuncAttributeMaxDynamicSharedMemorySize, int(kMaxLdsBytes));
   if (attr != hipSuccess) return fail(LMX_ERR_LAUNCH_FAILED, "hipFuncSetAttribute: %s", hipGetErrorString(attr));
-  constexpr int RW = kWave / H;
+  constexpr int RW = kWave / H / (PS ? 2 : 1);
   const int blocks = EPI == kEpiSiluPair ? a.rows / RW : (a.Npad + RW - 1) / RW;
-  lut_gemv_quad_kernel<FMT, ROT, WAVES, H, XM, EPI><<<dim3(blocks), dim3(WAVES * kWave), lds, st>>>(a);
+  lut_gemv_quad_kernel<FMT, ROT, WAVES, H, XM, EPI, PS><<<dim3(blocks), dim3(WAVES * kWave), lds, st>>>(a);
   return LMX_OK;
+}
+
+static int quad_max_blocks() {
+  const char *e = std::getenv("LMX_QUAD_MAX_BLOCKS");
+  return e ? std::atoi(e) : kQuadMaxBlocks;
 }
 
 template <int FMT, int WAVES, int H>
 static int launch_quad_cfg(const GemvArgs &a, hipStream_t st) {   // quad_serves(a) holds
   const bool rot = a.rotate == LMX_ROTATE_FWHT256;
+  // 4-bit 4 x 4 x 1, unrotated, store: the plane split where twice the
+  // workgroups still make one round (LMX_QPS=0 turns it off)
+  if constexpr (FMT == LMX_FMT_INT4 && WAVES == 4 && H == 4) {
+    const char *qe = std::getenv("LMX_QPS");
+    const int rw = kWave / H;
+    if ((!qe || std::atoi(qe) != 0) && !rot && a.epi == kEpiStore && 2 * ((a.Npad + rw - 1) / rw) <= quad_max_blocks()) {
+      if (a.xmode == kXModeRmsNorm) return launch_quad_kernel<FMT, false, WAVES, H, kXModeRmsNorm, kEpiStore, true>(a, st);
+      return launch_quad_kernel<FMT, false, WAVES, H, kXModeNone, kEpiStore, true>(a, st);
+    }
+  }
 #define LMX_QUAD(R, XMV, EPV) return launch_quad_kernel<FMT, R, WAVES, H, XMV, EPV>(a, st)
   if (a.xmode == kXModeRmsNorm) {
     if (rot) {
@@ -1620,10 +1666,8 @@ bool quad_serves(const GemvArgs &a) {
   // round of workgroups costs more than the batched kernel's per-slice
   // tables and reduce (Qwen gate|up 17920 x 1536, 560 workgroups: batch 4
   // decode 2222 -> 2285 tokens/s with the limit).
-  const char *e = std::getenv("LMX_QUAD_MAX_BLOCKS");
-  const int max_blocks = e ? std::atoi(e) : kQuadMaxBlocks;
   const int blocks = a.epi == kEpiSiluPair ? a.rows / rw : (a.Npad + rw - 1) / rw;
-  return blocks <= max_blocks;
+  return blocks <= quad_max_blocks();
 }
 
 int launch_gemv_quad(int fmt, const GemvArgs &a, void *stream) {

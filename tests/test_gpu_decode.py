@@ -472,8 +472,11 @@ def test_batched_qkv_partials_head_dim_128(cuda, monkeypatch, batch, hs):
     # head's query heads over 2 workgroups (the default for this small
     # grid) or 3 (LMX_ATTN_HS), batch 8 and 4 (the fused-reduction step,
     # LMX_QUAD_STEP=0); the same bits as the reduced rows (LMX_QKV_PARTS=0)
-    # and the oracle's logits, across two attention chunks
+    # and the oracle's logits, across two attention chunks.  At batch 4 the
+    # reduced path's qkv takes the four-vector kernel, unsplit here
+    # (LMX_QPS=0): its chunk sums are then the batched reduction's bits.
     monkeypatch.setenv("LMX_QUAD_STEP", "0")
+    monkeypatch.setenv("LMX_QPS", "0")
     if hs:
         monkeypatch.setenv("LMX_ATTN_HS", hs)
     cfg = qwen_small(max_seq=128)

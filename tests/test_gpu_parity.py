@@ -365,6 +365,25 @@ def test_four_vector_full_k(cuda, monkeypatch, fmt, cfg, rows, cols, flags):
         assert rel_max_err(y[b], yb[b]) < TOL, f"vector {b}"
 
 
+@pytest.mark.parametrize("qps", ["0", "1"])
+@pytest.mark.parametrize("rows,cols", [(70, 2048), (2048, 1536), (1536, 1536), (33, 640)])
+def test_four_vector_plane_split(cuda, monkeypatch, qps, rows, cols):
+    # 4 unrotated 4-bit vectors on the 4x4x1 plan: the four-vector kernel
+    # with a chunk's planes split over two lanes (where twice its workgroups
+    # still make one round; LMX_QPS=0 keeps one lane per row and chunk),
+    # against the oracle for each vector
+    monkeypatch.setenv("LMX_QPS", qps)
+    planes, scales, g = synth.make_weights(L.FMT_INT4, rows, cols, seed=rows + 5 * cols, group=128)
+    xs = np.stack([synth.make_activations(cols, seed=4000 + s, outliers=True) for s in range(4)])
+    w = L.Weight.from_planes(L.FMT_INT4, planes, scales, rows, cols, g)
+    assert w.kernel_config()[0] == 6
+    y = w.gemv(dev(xs.ravel()), flags=L.ROTATE_NONE).cpu().numpy().reshape(4, rows)
+    for b in range(4):
+        ref = oracle_planes_gemv(L.FMT_INT4, planes, scales, rows, cols, g, xs[b], L.ROTATE_NONE)
+        assert rel_max_err(y[b], ref) < TOL, f"vector {b}"
+    w.close()
+
+
 @pytest.mark.parametrize("fmt", [L.FMT_INT4, L.FMT_TERNARY])
 def test_four_vector_linear_bias(cuda, fmt):
     # lmx_linear on exactly 4 vectors of a 4 x 4 x 1 plan: the four-vector
