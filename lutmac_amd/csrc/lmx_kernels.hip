@@ -247,6 +247,15 @@ constexpr uint32_t fullk_prefix_bytes() {
   return (uint32_t(WAVES * H * CPS + WAVES * kWave) * 4 + 255) / 256 * 256;
 }
 
+// The lean kernel's prefix: as fullk_prefix_bytes, or with a plane split
+// only the WAVES x (rows per workgroup) slice sums it writes (the layered
+// plan's 70 chunk blocks leave 2.5 KB of the 160 KB)
+template <int WAVES, int H, int CPS, bool PS>
+constexpr uint32_t plain_prefix_bytes() {
+  if constexpr (PS) return (uint32_t(WAVES * H * CPS + WAVES * (kWave / H / 2)) * 4 + 255) / 256 * 256;
+  return fullk_prefix_bytes<WAVES, H, CPS>();
+}
+
 template <int H>
 __device__ __forceinline__ uint32_t slice_shift(int s) {
   return ((H == 4 || H == 8) && (s & 1)) ? 64u : 0u;
@@ -426,7 +435,7 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_plain_kernel(GemvArgs 
   constexpr int P = Fmt<FMT>::P, NA = Fmt<FMT>::NA, S = Fmt<FMT>::S;
   // PS (4-bit): the four planes of a row's chunk split over two lanes, planes
   // 0-1 and 2-3 (half the lookups per lane, half the rows per workgroup)
-  static_assert(!PS || (FMT == LMX_FMT_INT4 && !LAY && EPI == kEpiStore), "plane split: 4-bit, plain store");
+  static_assert(!PS || (FMT == LMX_FMT_INT4 && EPI == kEpiStore), "plane split: 4-bit, plain store");
   constexpr int RW = kWave / H / (PS ? 2 : 1);
   constexpr bool PAIR = EPI == kEpiSiluPair;
   constexpr int HR = RW / 2;   // PAIR: gate rows (then as many up rows) per workgroup
@@ -435,7 +444,7 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_plain_kernel(GemvArgs 
   constexpr int XJ = H * CPS / 2;
   static_assert(!LAY || H % 2 == 0, "layered: whole 256-chunks per wave and layer");
   static_assert(H * CPS % 2 == 0, "whole 256-chunks per wave");
-  constexpr uint32_t PREFIX = fullk_prefix_bytes<WAVES, H, CPS>();
+  constexpr uint32_t PREFIX = plain_prefix_bytes<WAVES, H, CPS, PS>();
   extern __shared__ __attribute__((aligned(256))) float lds[];
   const int Kc = a.Kp / kChunk;
   const int used = (Kc + CPS - 1) / CPS;
@@ -567,7 +576,10 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_plain_kernel(GemvArgs 
         wl[1].z ^= inv;
         wl[1].w ^= inv;
         float A2[2] = {0.0f, 0.0f};
-        chunk_lookups<LMX_FMT_RRQ2, true>(wl, tbase, shift, A2, c * kStagChunkBytes);
+        if constexpr (LAY)
+          chunk_lookups<LMX_FMT_RRQ2, true>(wl, tbase + uint32_t(min(chunk_of(c), Kc - 1)) * kIplChunkBytes, shift, A2);
+        else
+          chunk_lookups<LMX_FMT_RRQ2, true>(wl, tbase, shift, A2, c * kStagChunkBytes);
         const float c0 = part ? 4.0f : 1.0f, c1 = part ? -8.0f : 2.0f;
         const float nacc = fmaf(scl[0], c0 * A2[0] + c1 * A2[1], acc);
         acc = ch < Kc ? nacc : acc;
@@ -780,15 +792,15 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_ipl_kernel(GemvArgs a)
   }
 }
 
-template <int WAVES, int H, int CPS, bool LAY = false>
+template <int WAVES, int H, int CPS, bool LAY = false, bool PS = false>
 constexpr size_t plain_lds_bytes(size_t Kc) {
-  return fullk_prefix_bytes<WAVES, H, CPS>() +
+  return plain_prefix_bytes<WAVES, H, CPS, PS>() +
          (LAY ? Kc * kIplChunkBytes : (Kc + CPS - 1) / CPS * stag_slice_bytes(CPS));
 }
 
 template <int FMT, bool ROT, int WAVES, int H, int CPS, int XM, int EPI = kEpiStore, bool LAY = false, bool PS = false>
 static int launch_plain_kernel(const GemvArgs &a, hipStream_t st) {
-  const size_t lds = plain_lds_bytes<WAVES, H, CPS, LAY>(size_t(a.Kp / kChunk));
+  const size_t lds = plain_lds_bytes<WAVES, H, CPS, LAY, PS>(size_t(a.Kp / kChunk));
   if (lds > kMaxLdsBytes) return 1;   // staggered tables do not fit: the generic kernel serves it
   static const hipError_t attr = hipFuncSetAttribute(
       reinterpret_cast<const void *>(&lut_gemv_plain_kernel<FMT, ROT, WAVES, H, CPS, XM, EPI, LAY, PS>),
@@ -881,7 +893,19 @@ static int launch_plain(const GemvArgs &a, hipStream_t st) {
   case kFullK_4x4x1: return launch_plain_cfg<FMT, 4, 4, 1>(a, st);
   case kFullK_8x8x1: return launch_plain_cfg<FMT, 8, 8, 1>(a, st);
   case kFullK_8x8x2L:
-    if constexpr (FMT == LMX_FMT_INT4) return launch_plain_cfg<FMT, 8, 8, 2, true>(a, st);
+    if constexpr (FMT == LMX_FMT_INT4) {
+      // unrotated, plain store: 16 waves x 4 slices x 2 layered chunks with
+      // the planes split over two lanes (the same 8 rows per workgroup and
+      // chunk tables; four waves per SIMD, half the lookups per lane)
+      if (a.rotate == LMX_ROTATE_NONE && a.epi == kEpiStore && plane_split_level() == 1) {
+        switch (a.xmode) {
+        case kXModeNone: return launch_plain_kernel<FMT, false, 16, 4, 2, kXModeNone, kEpiStore, true, true>(a, st);
+        case kXModeRmsNorm: return launch_plain_kernel<FMT, false, 16, 4, 2, kXModeRmsNorm, kEpiStore, true, true>(a, st);
+        case kXModeSiluMul: return launch_plain_kernel<FMT, false, 16, 4, 2, kXModeSiluMul, kEpiStore, true, true>(a, st);
+        }
+      }
+      return launch_plain_cfg<FMT, 8, 8, 2, true>(a, st);
+    }
     return 1;
   }
   return 1;

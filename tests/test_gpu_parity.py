@@ -248,20 +248,21 @@ def test_forced_kernel_plans(cuda, monkeypatch, fmt, cfg, staged, family):
     assert rel_max_err(y, ref) < TOL
 
 
-# The 4 x 4 x 1 and 16 x 4 x 1 plans of an unrotated 4-bit GEMV split each
-# chunk's four planes over two lanes (LMX_PS=1, the default; 2 splits only
-# the 4 x 4 x 1 plan, 0 neither): every form against the oracle, ragged and
-# full workgroups.  (K > 2048 with at most 2048 rows: 16 x 4 x 1 at 8 rows
-# per workgroup when it splits, else the 8 x 8 x 1 plan.)
+# The 4 x 4 x 1, 16 x 4 x 1 and layered plans of an unrotated 4-bit GEMV
+# split each chunk's four planes over two lanes (LMX_PS=1, the default; 2
+# splits only the 4 x 4 x 1 plan, 0 neither): every form against the oracle,
+# ragged and full workgroups.  (K > 2048 with at most 2048 rows: 16 x 4 x 1
+# at 8 rows per workgroup when it splits, else the 8 x 8 x 1 plan; K = 8960:
+# the layered plan, launched as 16 waves x 4 slices x 2 chunks when split.)
 @pytest.mark.parametrize("ps", ["0", "1", "2"])
 @pytest.mark.parametrize("rows,cols", [(33, 2048), (300, 640), (2048, 2048), (3072, 2048), (1536, 1536),
-                                       (2048, 8192), (300, 4096), (45, 7936)])
+                                       (2048, 8192), (300, 4096), (45, 7936), (1536, 8960), (40, 8960)])
 def test_int4_plane_split(cuda, monkeypatch, ps, rows, cols):
     monkeypatch.setenv("LMX_PS", ps)
     planes, scales, g = synth.make_weights(L.FMT_INT4, rows, cols, seed=rows + cols, group=128)
     x = synth.make_activations(cols, seed=7, outliers=True)
     w = L.Weight.from_planes(L.FMT_INT4, planes, scales, rows, cols, g)
-    want_plan = 6 if cols <= 2048 else (5 if ps == "1" else 7)
+    want_plan = 6 if cols <= 2048 else 8 if cols > 8192 else (5 if ps == "1" else 7)
     assert w.kernel_config()[0] == want_plan
     y = w.gemv(dev(x), flags=L.ROTATE_NONE).cpu().numpy()
     ref = oracle_planes_gemv(L.FMT_INT4, planes, scales, rows, cols, g, x, L.ROTATE_NONE)
