@@ -285,6 +285,21 @@ bool rotates(int fmt) {   // lut_gemm_scalar.cpp:88-96: ternary and 1/2-bit inpu
   return fmt == LMX_FMT_TERNARY || fmt == LMX_FMT_BINARY || fmt == LMX_FMT_RRQ2 || fmt == LMX_FMT_RRQ3;
 }
 
+// The rotation table of every position the cache holds: tab[p * half + d] =
+// (cos, sin) of (p / pos_div) * freq[d] (embedding.cpp:36-75), written once
+// when the decoder is created, so that attention reads a position's angles
+// with its K/V rows instead of reducing large arguments for sincosf.
+__global__ __launch_bounds__(256) void rope_table_kernel(const float *__restrict__ freq, float pos_div, int half,
+                                                         size_t n, float2 *__restrict__ tab) {
+  const size_t i = size_t(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= n) return;
+  const int p = int(i / size_t(half)), d = int(i % size_t(half));
+  const float pf = float(p) / pos_div;
+  float sn, cs;
+  sincosf(pf * freq[d], &sn, &cs);
+  tab[i] = make_float2(cs, sn);
+}
+
 // Frequencies theta^(-2d/hd) for d < hd/2, Llama-3 scaled when asked.
 std::vector<float> rope_freqs(const lmx_decoder_config &c) {
   const int hd = int(c.head_dim);
@@ -381,15 +396,29 @@ __device__ __forceinline__ void chunk_attend(const float (*ks)[HD + 4], const fl
   if (valid) {
     const float *kv = lane == jnew ? knew : ks[lane];
     float acc = 0.0f;
-    constexpr int kUnrollD = LEAN ? 8 : HD / 4;
-#pragma unroll kUnrollD
-    for (int d4 = 0; d4 < HD / 4; ++d4) {
-      const float4 k4 = *reinterpret_cast<const float4 *>(kv + 4 * d4);
-      const float4 q4 = *reinterpret_cast<const float4 *>(qrow + 4 * d4);
-      acc += q4.x * k4.x;
-      acc += q4.y * k4.y;
-      acc += q4.z * k4.z;
-      acc += q4.w * k4.w;
+    // Stages of SB float4 pairs: a stage's LDS reads are all requested
+    // before its multiply-adds (the scheduler otherwise keeps two reads in
+    // flight and the one wave per SIMD waits out the LDS latency on every
+    // pair); the sum runs in the same order as one read at a time.
+    constexpr int SB = LEAN ? 4 : 8;
+    static_assert((HD / 4) % SB == 0, "whole stages");
+#pragma unroll
+    for (int d0 = 0; d0 < HD / 4; d0 += SB) {
+      float4 k4[SB], q4[SB];
+#pragma unroll
+      for (int b = 0; b < SB; ++b) {
+        k4[b] = *reinterpret_cast<const float4 *>(kv + 4 * (d0 + b));
+        q4[b] = *reinterpret_cast<const float4 *>(qrow + 4 * (d0 + b));
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int b = 0; b < SB; ++b) {
+        acc += q4[b].x * k4[b].x;
+        acc += q4[b].y * k4[b].y;
+        acc += q4[b].z * k4[b].z;
+        acc += q4[b].w * k4[b].w;
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
     sc = acc * scale;
   }
@@ -446,7 +475,7 @@ __device__ __forceinline__ void chunk_attend(const float (*ks)[HD + 4], const fl
 template <int HD, int CPW, bool PARTS>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void attn_kernel(const float *__restrict__ qkv, float *__restrict__ kc,
                                                    float *__restrict__ vc, const int *__restrict__ pos_p,
-                                                   const float *__restrict__ freq, float pos_div, int n_heads,
+                                                   const float2 *__restrict__ rope, int n_heads,
                                                    int n_kv, int group, int max_seq, float scale,
                                                    float *__restrict__ part, int n_chunks,
                                                    unsigned *__restrict__ tickets, float *__restrict__ out,
@@ -465,6 +494,14 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void a
   __shared__ float knew[HD];
   __shared__ float qkvb[PARTS ? (8 + 2) * HD : 1];   // PARTS: the summed q (up to 8 heads), k and v rows
   __shared__ unsigned ticket;
+  // Every argument in SGPRs before the first wait: their loads then take one
+  // round trip (left to the compiler they came in three batches, each waited
+  // for, ahead of the K/V requests).
+  asm volatile("" ::"s"(qkv), "s"(kc), "s"(vc), "s"(pos_p), "s"(rope), "s"(part), "s"(tickets), "s"(out));
+  asm volatile("" ::"s"(n_heads), "s"(n_kv), "s"(group), "s"(max_seq), "s"(scale), "s"(n_chunks), "s"(qkv_stride),
+               "s"(kv_stride), "s"(spec_units), "s"(hsplit));
+  if constexpr (PARTS) asm volatile("" ::"s"(qparts), "s"(qsplits), "s"(qnpad), "s"(qbias));
+  __builtin_amdgcn_sched_barrier(0);
   {
     // sequence blockIdx.y of a batch: its q|k|v row, KV cache, partials,
     // tickets and output (the position is shared)
@@ -486,13 +523,15 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void a
   const int t0 = unit * UNIT;
   const float *kin = qkv + size_t(n_heads) * HD + kvh * HD;
   const float *vin = kin + row;
-  const int pos = min(*pos_p, max_seq - 1);
   // Past the speculative window a unit learns the position first (an
   // atomic load: never hoisted above this uniform branch, so the window's
   // units issue their loads without waiting for it).
+  int pos = 0;
   bool skip = false;
-  if (unit >= spec_units)
-    skip = t0 > min(__hip_atomic_load(pos_p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), max_seq - 1);
+  if (unit >= spec_units) {
+    pos = min(__hip_atomic_load(pos_p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), max_seq - 1);
+    skip = t0 > pos;
+  }
   if (!skip) {   // uniform over the workgroup
 
   // ---- every global operand requested before the first wait (one round
@@ -513,6 +552,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void a
       vr[i] = *reinterpret_cast<const float4 *>(vc + size_t(tq + r) * row + kvh * HD + 4 * c4);
     }
   };
+  // The position (for the rotation table's row) is requested first and the
+  // rows, q, k and v right after it, so that its wait (the loads return in
+  // order) leaves them in flight.
+  const int praw = __hip_atomic_load(pos_p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __builtin_amdgcn_sched_barrier(0);
   load_rows(0);
   const auto store_rows = [&]() {
 #pragma unroll
@@ -524,7 +568,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void a
     }
   };
   const float *qin = qkv + size_t(h0 + (wave < hpw ? wave : 0)) * HD;
-  float qa[RP], qb[RP], ka[RP], kb[RP], fr[RP], vn[VD];
+  float qa[RP], qb[RP], ka[RP], kb[RP], vn[VD];
+  float2 rt[RP];   // (cos, sin) of the position's rotation angles
   // PARTS: value i < nval of the workgroup's q (hpw heads), k, v rows; thread
   // t sums values t, t + NT, ... (VPT of them) over the splits
   constexpr int VPT = PARTS ? ((8 + 2) * HD + NT - 1) / NT : 1;
@@ -543,21 +588,22 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void a
       pb[j] = qbias ? qbias[r] : 0.0f;
     }
   }
+  if constexpr (!PARTS) {
 #pragma unroll
-  for (int i = 0; i < RP; ++i) {
-    const int d = min(lane + i * kWave, HALF - 1);
-    fr[i] = freq[d];
-    if constexpr (!PARTS) {
+    for (int i = 0; i < RP; ++i) {
+      const int d = min(lane + i * kWave, HALF - 1);
       qa[i] = qin[d];
       qb[i] = qin[d + HALF];
       ka[i] = kin[d];
       kb[i] = kin[d + HALF];
     }
-  }
-  if constexpr (!PARTS) {
 #pragma unroll
     for (int u = 0; u < VD; ++u) vn[u] = vin[u * kWave + lane];
   }
+  __builtin_amdgcn_sched_barrier(0);
+  pos = min(__builtin_amdgcn_readfirstlane(praw), max_seq - 1);
+#pragma unroll
+  for (int i = 0; i < RP; ++i) rt[i] = rope[size_t(pos) * HALF + min(lane + i * kWave, HALF - 1)];
   // One wait for all of them: without a use of every loaded value here the
   // compiler issues the small loads after the K/V waits (a second round trip).
 #pragma unroll
@@ -566,7 +612,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void a
                  "v"(vr[i].z), "v"(vr[i].w));
   if constexpr (PARTS) {
 #pragma unroll
-    for (int i = 0; i < RP; ++i) asm volatile("" ::"v"(fr[i]));
+    for (int i = 0; i < RP; ++i) asm volatile("" ::"v"(rt[i].x), "v"(rt[i].y));
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
 #pragma unroll
@@ -586,7 +632,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void a
     }
   } else {
 #pragma unroll
-    for (int i = 0; i < RP; ++i) asm volatile("" ::"v"(fr[i]), "v"(qa[i]), "v"(qb[i]), "v"(ka[i]), "v"(kb[i]));
+    for (int i = 0; i < RP; ++i)
+      asm volatile("" ::"v"(rt[i].x), "v"(rt[i].y), "v"(qa[i]), "v"(qb[i]), "v"(ka[i]), "v"(kb[i]));
 #pragma unroll
     for (int u = 0; u < VD; ++u) asm volatile("" ::"v"(vn[u]));
   }
@@ -607,14 +654,16 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void a
   }
   const bool live = t0 <= pos;                      // the unit holds positions of the sequence
   const bool own = pos / UNIT == unit;              // the unit holds the new position
-  const float pf = float(pos) / pos_div;
-  // RoPE: pairs (d, d + HD/2) rotated by pf * freq[d] (embedding.cpp:36-75),
-  // computed by every lane so that no load sinks into a branch
+  // RoPE: pairs (d, d + HD/2) rotated by the position's angle for d
+  // (embedding.cpp:36-75), its cosine and sine read from the decoder's
+  // table; computed by every lane so that no load sinks into a branch
 #pragma unroll
   for (int i = 0; i < RP; ++i) {
+    // each product rounded, then the sum (no fused multiply-add): the
+    // reference's a*c - b*s, the same bits in every instantiation
+#pragma clang fp contract(off)
     const int d = lane + i * kWave;
-    float sn, cs;
-    sincosf(pf * fr[i], &sn, &cs);
+    const float cs = rt[i].x, sn = rt[i].y;
     const float q0 = qa[i] * cs - qb[i] * sn, q1 = qa[i] * sn + qb[i] * cs;
     const float k0 = ka[i] * cs - kb[i] * sn, k1 = ka[i] * sn + kb[i] * cs;
     if (live && wave < hpw && d < HALF) {
@@ -736,6 +785,7 @@ struct lmx_decoder {
   float *final_norm = nullptr;
   float *hidden = nullptr, *qkv = nullptr, *gate_up = nullptr, *logits = nullptr;
   float *kcache = nullptr, *vcache = nullptr, *freq = nullptr;
+  float2 *rope = nullptr;                // [max_seq][head_dim / 2] (cos, sin) of each position's angles
   float *attn_part = nullptr;            // [n_heads][chunks][m, l, -, -, o[head_dim]]
   float *attn_out = nullptr;             // [n_heads * head_dim] merged attention output
   unsigned *attn_tickets = nullptr;      // [n_kv_heads][kAttnMaxSplit] unit tickets (zero between steps)
@@ -898,7 +948,7 @@ int attention(lmx_decoder *d, size_t layer, hipStream_t st, const float *qparts 
     return fail(LMX_ERR_INVALID_ARGUMENT, "attention over %d q|k|v partials of %d rows", qsplits, qnpad);
 #define LMX_ATTN(HD, CPW, PARTS)                                                                                    \
   attn_kernel<HD, CPW, PARTS><<<grid, dim3(512), 0, st>>>(                                                         \
-      d->qkv, kc, vc, d->pos, d->freq, d->pos_div, int(c.n_heads), int(c.n_kv_heads), group, int(c.max_seq), scale, \
+      d->qkv, kc, vc, d->pos, d->rope, int(c.n_heads), int(c.n_kv_heads), group, int(c.max_seq), scale, \
       d->attn_part, nch, d->attn_tickets, d->attn_out, qkv_stride, d->kv_seq, spec_units, hsplit, qparts, qsplits,  \
       qnpad, qbias)
   if (qparts) {
@@ -1258,9 +1308,24 @@ int lmx_decoder_create_batched(const lmx_decoder_config *cfg, size_t batch, lmx_
       (B > 1 && (st = d->alloc(reinterpret_cast<void **>(&d->argmax_slots), B * kArgmaxParts * 8))) ||
       (B > 1 && (st = d->alloc(reinterpret_cast<void **>(&d->argmax_seq_tickets),
                                B * kTicketPad * sizeof(unsigned)))) ||
-      (st = upload(d, &d->freq, fr.data(), fr.size()))) {
+      (st = upload(d, &d->freq, fr.data(), fr.size())) ||
+      (st = d->alloc(reinterpret_cast<void **>(&d->rope), c.max_seq * (c.head_dim / 2) * sizeof(float2)))) {
     delete d;
     return st;
+  }
+  {
+    const size_t n = c.max_seq * (c.head_dim / 2);
+    rope_table_kernel<<<dim3(unsigned((n + 255) / 256)), dim3(256)>>>(d->freq, d->pos_div, int(c.head_dim / 2), n,
+                                                                      d->rope);
+    if ((st = launch_err("rope table"))) {
+      delete d;
+      return st;
+    }
+    e = hipStreamSynchronize(nullptr);
+    if (e != hipSuccess) {
+      delete d;
+      return hip_err(e, "rope table");
+    }
   }
   e = hipStreamCreateWithFlags(&d->stream, hipStreamNonBlocking);
   if (e != hipSuccess) {
