@@ -142,6 +142,7 @@ int choose_reduce() {
 }  // namespace
 
 int plane_split_level() { return env_int("LMX_PS", 1); }
+int mfma_batched() { return env_int("LMX_MFMA", 1); }
 
 void plan_weight(lmx_weight *w, int fmt, size_t rows, size_t cols, size_t group) {
   FormatInfo fi;

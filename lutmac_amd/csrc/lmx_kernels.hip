@@ -1256,6 +1256,142 @@ __global__ __launch_bounds__((kWave * batch_waves<NB, VG, RG>())) void lut_gemv_
   for (int n = 0; n < VG; ++n) a.partials[(size_t(n0 + n) * splits + split) * a.Npad + row] = acc[n];
 }
 
+// Batched 4-bit GEMV on the matrix cores (int4, unrotated, up to 16
+// vectors): the same k-slices, grid and partials as lut_gemv_batch_kernel,
+// so its reductions and epilogues consume them unchanged.  A wave owns 16
+// rows of the slice; v_mfma_f32_16x16x16_bf16 takes A = the 16 rows' codes
+// plus 16 (16..31: bf16 0x4180 | q << 3, exact) and B = the vectors split
+// into three bf16 parts (x = hi + mid + lo exactly: each part the
+// round-to-nearest-even bf16 of what the earlier parts leave), so every
+// product is exact and the sums accumulate in fp32; each 128-chunk's sum
+// less 24 times the chunk's sum of x is scaled by its group scale in fp32
+// (int4_gemv, lut_gemm_scalar.cpp:186-222: y = sum_b s_b sum_i (q_i - 8) x_i).  Lane (i, kq) of a 16 x 16 x 16 step
+// holds row i's codes of 4 k (A) and vector i's 4 activations (B), lane
+// layout A[i][k] -> lane i + 16 (k / 4), item k % 4; B[k][j] -> lane
+// j + 16 (k / 4); D[i][j] -> lane j + 16 (i / 4), item i % 4.  k-block
+// kb = 2m + h of a slice takes the 4-groups g = 8m + 2kq + h: lane kq's
+// byte kq of word m of each plane holds its nibbles of both h, and item e
+// is k = 4g + 3 - e (the nibble's bit e, MSB-first planes).
+template <int NB, int CH, int NW>
+__global__ __launch_bounds__(kWave * NW) void lut_gemv_mfma_kernel(GemvArgs a, int row_blocks, int splits) {
+  typedef short v4s __attribute__((ext_vector_type(4)));
+  typedef float v4f __attribute__((ext_vector_type(4)));
+  constexpr int KB = 8 * CH;   // 16-k blocks per slice
+  static_assert(NB >= 1 && NB <= 16 && (CH == 1 || CH == 2), "up to 16 vectors, 128- or 256-wide slices");
+  __shared__ uint2 bfrag[KB * 3][kWave];   // B fragments: [k-block][part][lane], 4 bf16 each
+  __shared__ float xsb[KB][16];            // sum of each k-block's activations per vector
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  const int rb = blockIdx.x % row_blocks, split = blockIdx.x / row_blocks;
+  const int c0 = split * CH;
+  const int kq = lane >> 4, li = lane & 15;
+  const int row0 = min(rb * 16 * NW + wave * 16, a.Npad - 16);   // tiles past Npad redo the last one, unstored
+  const bool active = rb * 16 * NW + wave * 16 < a.Npad;           // wave-uniform
+  const uint32_t Npad = uint32_t(a.Npad);
+
+  // ---- the rows' planes (row li of the tile) and the D rows' scales ----
+  u32x4 w[CH][4];
+  {
+    const u32x4 *__restrict__ pl = reinterpret_cast<const u32x4 *>(a.planes);
+#pragma unroll
+    for (int c = 0; c < CH; ++c)
+#pragma unroll
+      for (int p = 0; p < 4; ++p)
+        w[c][p] = __builtin_nontemporal_load(pl + (uint32_t((c0 + c) * 4 + p) * Npad + uint32_t(row0 + li)));
+  }
+  float4 sc[CH];
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int g = a.gshift >= 0 ? (c0 + c) >> a.gshift : (c0 + c) / a.group_chunks;
+    sc[c] = *reinterpret_cast<const float4 *>(a.scales + uint32_t(g) * Npad + uint32_t(row0 + 4 * kq));
+  }
+
+  // ---- B fragments of the slice: wave w splits k-blocks w, w + NW, ... ----
+#pragma unroll
+  for (int kb = wave; kb < KB; kb += NW) {
+    const int g = 8 * (kb >> 1) + 2 * kq + (kb & 1);
+    const int k = c0 * kChunk + 4 * g;
+    float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (li < NB && k < a.cols) v = *reinterpret_cast<const float4 *>(a.x + size_t(li) * a.cols + k);
+    const float xe[4] = {v.w, v.z, v.y, v.x};   // item e: k = 4g + 3 - e
+    {
+      float xs = (v.x + v.y) + (v.z + v.w);
+      xs += __shfl_xor(xs, 16, kWave);
+      xs += __shfl_xor(xs, 32, kWave);
+      if (kq == 0) xsb[kb][li] = xs;
+    }
+    uint32_t part[3][4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float r = xe[e];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const uint32_t u = __float_as_uint(r);
+        const uint32_t h = (u + 0x7FFFu + ((u >> 16) & 1u)) & 0xFFFF0000u;   // bf16, nearest even
+        part[t][e] = h;
+        r -= __uint_as_float(h);   // exact
+      }
+      part[2][e] = __float_as_uint(r);   // at most 8 significant bits left: exact in bf16
+    }
+#pragma unroll
+    for (int t = 0; t < 3; ++t)
+      bfrag[kb * 3 + t][lane] = make_uint2(__builtin_amdgcn_perm(part[t][1], part[t][0], 0x07060302u),
+                                           __builtin_amdgcn_perm(part[t][3], part[t][2], 0x07060302u));
+  }
+  __syncthreads();
+
+  // ---- the tile: per 128-chunk, 8 k-blocks of 3 products, then the scale ----
+  const uint32_t sel01 = uint32_t(kq) | uint32_t(4 + kq) << 8 | 0x0C0C0000u;
+  const uint32_t sel23 = 0x00000C0Cu | uint32_t(kq) << 16 | uint32_t(4 + kq) << 24;
+  if (!active) return;   // after the barrier; no barrier follows
+  v4f y = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    // one accumulator per activation part: three independent product chains
+    v4f acc[3] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
+#pragma unroll
+    for (int mm = 0; mm < 4; ++mm) {
+      // byte kq of word mm of planes 0..3 -> bytes 0..3
+      const uint32_t wb = __builtin_amdgcn_perm(w[c][1][mm], w[c][0][mm], sel01) |
+                          __builtin_amdgcn_perm(w[c][3][mm], w[c][2][mm], sel23);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        // group 8m + 2kq + h: the high nibble of each byte for h = 0
+        uint32_t M = h == 0 ? (wb >> 4) & 0x0F0F0F0Fu : wb & 0x0F0F0F0Fu;
+        // 4 x 4 bit transpose: bit e of byte p (plane p, item e) -> bit p of byte e
+        uint32_t t1 = ((M >> 14) ^ M) & 0x00000C0Cu;
+        M ^= t1 ^ (t1 << 14);
+        uint32_t t2 = ((M >> 7) ^ M) & 0x000A000Au;
+        M ^= t2 ^ (t2 << 7);
+        // byte e = code q of item e; A item = bf16(q + 16) = 0x4180 | q << 3
+        const uint32_t a01 = (__builtin_amdgcn_perm(0u, M, 0x0C010C00u) << 3) | 0x41804180u;
+        const uint32_t a23 = (__builtin_amdgcn_perm(0u, M, 0x0C030C02u) << 3) | 0x41804180u;
+        const v4s av = __builtin_bit_cast(v4s, make_uint2(a01, a23));
+        const int kb = 2 * (4 * c + mm) + h;
+#pragma unroll
+        for (int t = 0; t < 3; ++t) {
+          const v4s bv = __builtin_bit_cast(v4s, bfrag[kb * 3 + t][lane]);
+          acc[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(av, bv, acc[t], 0, 0, 0);
+        }
+      }
+    }
+    const int ch = c0 + c;
+    if (ch < a.Kp / kChunk) {
+      float xs = 0.0f;   // the chunk's sum of vector li's activations
+#pragma unroll
+      for (int kb = 8 * c; kb < 8 * c + 8; ++kb) xs += xsb[kb][li];
+      const v4f s = ((acc[0] + acc[1]) + acc[2]) - 24.0f * xs;
+      y[0] = fmaf(sc[c].x, s[0], y[0]);
+      y[1] = fmaf(sc[c].y, s[1], y[1]);
+      y[2] = fmaf(sc[c].z, s[2], y[2]);
+      y[3] = fmaf(sc[c].w, s[3], y[3]);
+    }
+  }
+  // D[i][j]: lane j + 16 (i / 4), item i % 4 -> rows row0 + 4 kq + e of vector li
+  if (li < NB)
+    *reinterpret_cast<float4 *>(a.partials + (size_t(li) * splits + split) * Npad + uint32_t(row0 + 4 * kq)) =
+        make_float4(y[0], y[1], y[2], y[3]);
+}
+
 // y[n*rows + r] = sum_s partials[n][s][r] (+ bias[r]) (+ resid[n*rows + r])
 // in split order; resid may be y itself (each element is read and written
 // by one thread).  A thread sums 4 consecutive rows with 16-byte loads (Npad
@@ -1748,10 +1884,31 @@ static int launch_batch_nb(const GemvArgs &a, hipStream_t st) {
                  : grid(4) >= kBatchMinGrid ? 4
                  : grid(2) >= kBatchMinGrid ? 2
                                             : 1;
-  if (narrow) launch_batch_rg<FMT, NB, 1, 1>(a, splits, st);
-  else if (rg == 4) launch_batch_rg<FMT, NB, 4>(a, splits, st);
-  else if (rg == 2) launch_batch_rg<FMT, NB, 2>(a, splits, st);
-  else launch_batch_rg<FMT, NB, 1>(a, splits, st);
+  bool mfma = false;
+  if constexpr (FMT == LMX_FMT_INT4 && NB >= 8) mfma = a.rotate == LMX_ROTATE_NONE && mfma_batched() && a.xmode == kXModeNone;
+  if (mfma) {
+    // 8 waves (128 rows) per workgroup, the slice's activation fragments
+    // built once for them (LMX_MFMA=4: 4 waves)
+    const bool w4 = mfma_batched() == 4;
+    const int nw = w4 ? 4 : 8;
+    const int row_blocks = (a.Npad + 16 * nw - 1) / (16 * nw);
+    const dim3 grid(row_blocks * splits), block(kWave * nw);
+    if (w4) {
+      if (narrow) lut_gemv_mfma_kernel<NB, 1, 4><<<grid, block, 0, st>>>(a, row_blocks, splits);
+      else lut_gemv_mfma_kernel<NB, 2, 4><<<grid, block, 0, st>>>(a, row_blocks, splits);
+    } else {
+      if (narrow) lut_gemv_mfma_kernel<NB, 1, 8><<<grid, block, 0, st>>>(a, row_blocks, splits);
+      else lut_gemv_mfma_kernel<NB, 2, 8><<<grid, block, 0, st>>>(a, row_blocks, splits);
+    }
+  } else if (narrow) {
+    launch_batch_rg<FMT, NB, 1, 1>(a, splits, st);
+  } else if (rg == 4) {
+    launch_batch_rg<FMT, NB, 4>(a, splits, st);
+  } else if (rg == 2) {
+    launch_batch_rg<FMT, NB, 2>(a, splits, st);
+  } else {
+    launch_batch_rg<FMT, NB, 1>(a, splits, st);
+  }
   if (a.epi == kEpiPartials) {
     // the consumer sums the partials
   } else if (a.epi == kEpiSiluPair) {

@@ -328,6 +328,29 @@ def test_batched_gemv(cuda, fmt, batch, rows, cols):
         assert rel_max_err(y[b], ref) < TOL, f"vector {b}"
 
 
+# Unrotated 4-bit groups of 8 and 16 vectors run on the matrix cores
+# (LMX_MFMA=1, the default: 8 waves per workgroup; 4: four waves; 0 the
+# lookup-table kernel): 128- and 256-wide
+# k-slices, K past the last whole 256 (640), group scales of 128 and 256
+# and one per row, a last group of fewer vectors (9, 21), against the oracle.
+@pytest.mark.parametrize("mfma", ["1", "4", "0"])
+@pytest.mark.parametrize("group", [128, 256, 0])
+@pytest.mark.parametrize("batch", [8, 16, 9, 21])
+@pytest.mark.parametrize("rows,cols", [(300, 640), (513, 1536), (2048, 2048), (4160, 4096)])
+def test_batched_int4_matrix_cores(cuda, monkeypatch, mfma, group, batch, rows, cols):
+    monkeypatch.setenv("LMX_MFMA", mfma)
+    planes, scales, g = synth.make_weights(L.FMT_INT4, rows, cols, seed=batch * 31 + rows, group=group or 128)
+    if group == 0:
+        scales = np.ascontiguousarray(scales[:, :, :1])
+    xs = np.stack([synth.make_activations(cols, seed=3000 + s, outliers=True) for s in range(batch)])
+    w = L.Weight.from_planes(L.FMT_INT4, planes, scales, rows, cols, group)
+    y = w.gemv(dev(xs.ravel()), flags=L.ROTATE_NONE).cpu().numpy().reshape(batch, rows)
+    for b in range(batch):
+        ref = oracle_planes_gemv(L.FMT_INT4, planes, scales, rows, cols, group, xs[b], L.ROTATE_NONE)
+        assert rel_max_err(y[b], ref) < TOL, f"vector {b}"
+    w.close()
+
+
 @pytest.mark.parametrize("fmt", [1, 3, 5, 6])
 @pytest.mark.parametrize("batch", [7, 8, 16])
 @pytest.mark.parametrize("rows,cols", [(4160, 4096), (2112, 4096)])
