@@ -1261,8 +1261,8 @@ __global__ __launch_bounds__((kWave * batch_waves<NB, VG, RG>())) void lut_gemv_
 // so its reductions and epilogues consume them unchanged.  A wave owns 16
 // rows of the slice; v_mfma_f32_16x16x16_bf16 takes A = the 16 rows' codes
 // plus 16 (16..31: bf16 0x4180 | q << 3, exact) and B = the vectors split
-// into three bf16 parts (x = hi + mid + lo exactly: each part the
-// round-to-nearest-even bf16 of what the earlier parts leave), so every
+// into three bf16 parts (x = hi + mid + lo exactly: hi and mid the top 8
+// significant bits of x and of x - hi, lo the at most 8 bits left), so every
 // product is exact and the sums accumulate in fp32; each 128-chunk's sum
 // less 24 times the chunk's sum of x is scaled by its group scale in fp32
 // (int4_gemv, lut_gemm_scalar.cpp:186-222: y = sum_b s_b sum_i (q_i - 8) x_i).  Lane (i, kq) of a 16 x 16 x 16 step
@@ -1272,37 +1272,50 @@ __global__ __launch_bounds__((kWave * batch_waves<NB, VG, RG>())) void lut_gemv_
 // kb = 2m + h of a slice takes the 4-groups g = 8m + 2kq + h: lane kq's
 // byte kq of word m of each plane holds its nibbles of both h, and item e
 // is k = 4g + 3 - e (the nibble's bit e, MSB-first planes).
-template <int NB, int CH, int NW>
+template <int NB, int CH, int NW, int RT>
 __global__ __launch_bounds__(kWave * NW) void lut_gemv_mfma_kernel(GemvArgs a, int row_blocks, int splits) {
   typedef short v4s __attribute__((ext_vector_type(4)));
   typedef float v4f __attribute__((ext_vector_type(4)));
   constexpr int KB = 8 * CH;   // 16-k blocks per slice
-  static_assert(NB >= 1 && NB <= 16 && (CH == 1 || CH == 2), "up to 16 vectors, 128- or 256-wide slices");
+  static_assert(NB >= 1 && NB <= 16 && (CH == 1 || CH == 2) && (RT == 1 || RT == 2),
+                "up to 16 vectors, 128- or 256-wide slices, 1 or 2 row tiles per wave");
   __shared__ uint2 bfrag[KB * 3][kWave];   // B fragments: [k-block][part][lane], 4 bf16 each
   __shared__ float xsb[KB][16];            // sum of each k-block's activations per vector
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
   const int rb = blockIdx.x % row_blocks, split = blockIdx.x / row_blocks;
   const int c0 = split * CH;
   const int kq = lane >> 4, li = lane & 15;
-  const int row0 = min(rb * 16 * NW + wave * 16, a.Npad - 16);   // tiles past Npad redo the last one, unstored
-  const bool active = rb * 16 * NW + wave * 16 < a.Npad;           // wave-uniform
+  // tile t of the wave: rows row0[t] .. + 15; tiles past Npad redo the last
+  // one and are not stored
+  int row0[RT];
+  bool live[RT];
+#pragma unroll
+  for (int t = 0; t < RT; ++t) {
+    const int r = (rb * NW + wave) * 16 * RT + 16 * t;
+    row0[t] = min(r, a.Npad - 16);
+    live[t] = r < a.Npad;   // wave-uniform
+  }
   const uint32_t Npad = uint32_t(a.Npad);
 
-  // ---- the rows' planes (row li of the tile) and the D rows' scales ----
-  u32x4 w[CH][4];
+  // ---- the rows' planes (row li of each tile) and the D rows' scales ----
+  u32x4 w[RT][CH][4];
   {
     const u32x4 *__restrict__ pl = reinterpret_cast<const u32x4 *>(a.planes);
 #pragma unroll
-    for (int c = 0; c < CH; ++c)
+    for (int t = 0; t < RT; ++t)
 #pragma unroll
-      for (int p = 0; p < 4; ++p)
-        w[c][p] = __builtin_nontemporal_load(pl + (uint32_t((c0 + c) * 4 + p) * Npad + uint32_t(row0 + li)));
+      for (int c = 0; c < CH; ++c)
+#pragma unroll
+        for (int p = 0; p < 4; ++p)
+          w[t][c][p] = __builtin_nontemporal_load(pl + (uint32_t((c0 + c) * 4 + p) * Npad + uint32_t(row0[t] + li)));
   }
-  float4 sc[CH];
+  float4 sc[RT][CH];
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
     const int g = a.gshift >= 0 ? (c0 + c) >> a.gshift : (c0 + c) / a.group_chunks;
-    sc[c] = *reinterpret_cast<const float4 *>(a.scales + uint32_t(g) * Npad + uint32_t(row0 + 4 * kq));
+#pragma unroll
+    for (int t = 0; t < RT; ++t)
+      sc[t][c] = *reinterpret_cast<const float4 *>(a.scales + uint32_t(g) * Npad + uint32_t(row0[t] + 4 * kq));
   }
 
   // ---- B fragments of the slice: wave w splits k-blocks w, w + NW, ... ----
@@ -1325,8 +1338,7 @@ __global__ __launch_bounds__(kWave * NW) void lut_gemv_mfma_kernel(GemvArgs a, i
       float r = xe[e];
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
-        const uint32_t u = __float_as_uint(r);
-        const uint32_t h = (u + 0x7FFFu + ((u >> 16) & 1u)) & 0xFFFF0000u;   // bf16, nearest even
+        const uint32_t h = __float_as_uint(r) & 0xFFFF0000u;   // the top 8 significant bits
         part[t][e] = h;
         r -= __uint_as_float(h);   // exact
       }
@@ -1339,38 +1351,50 @@ __global__ __launch_bounds__(kWave * NW) void lut_gemv_mfma_kernel(GemvArgs a, i
   }
   __syncthreads();
 
-  // ---- the tile: per 128-chunk, 8 k-blocks of 3 products, then the scale ----
+  // ---- the tiles: per 128-chunk, 8 k-blocks of 3 products, then the scale ----
   const uint32_t sel01 = uint32_t(kq) | uint32_t(4 + kq) << 8 | 0x0C0C0000u;
   const uint32_t sel23 = 0x00000C0Cu | uint32_t(kq) << 16 | uint32_t(4 + kq) << 24;
-  if (!active) return;   // after the barrier; no barrier follows
-  v4f y = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (!live[0]) return;   // after the barrier; no barrier follows
+  v4f y[RT];
+#pragma unroll
+  for (int t = 0; t < RT; ++t) y[t] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
-    // one accumulator per activation part: three independent product chains
-    v4f acc[3] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
+    // one accumulator per tile and activation part: independent product chains
+    v4f acc[RT][3];
+#pragma unroll
+    for (int t = 0; t < RT; ++t)
+#pragma unroll
+      for (int u = 0; u < 3; ++u) acc[t][u] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int mm = 0; mm < 4; ++mm) {
       // byte kq of word mm of planes 0..3 -> bytes 0..3
-      const uint32_t wb = __builtin_amdgcn_perm(w[c][1][mm], w[c][0][mm], sel01) |
-                          __builtin_amdgcn_perm(w[c][3][mm], w[c][2][mm], sel23);
+      uint32_t wb[RT];
+#pragma unroll
+      for (int t = 0; t < RT; ++t)
+        wb[t] = __builtin_amdgcn_perm(w[t][c][1][mm], w[t][c][0][mm], sel01) |
+                __builtin_amdgcn_perm(w[t][c][3][mm], w[t][c][2][mm], sel23);
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        // group 8m + 2kq + h: the high nibble of each byte for h = 0
-        uint32_t M = h == 0 ? (wb >> 4) & 0x0F0F0F0Fu : wb & 0x0F0F0F0Fu;
-        // 4 x 4 bit transpose: bit e of byte p (plane p, item e) -> bit p of byte e
-        uint32_t t1 = ((M >> 14) ^ M) & 0x00000C0Cu;
-        M ^= t1 ^ (t1 << 14);
-        uint32_t t2 = ((M >> 7) ^ M) & 0x000A000Au;
-        M ^= t2 ^ (t2 << 7);
-        // byte e = code q of item e; A item = bf16(q + 16) = 0x4180 | q << 3
-        const uint32_t a01 = (__builtin_amdgcn_perm(0u, M, 0x0C010C00u) << 3) | 0x41804180u;
-        const uint32_t a23 = (__builtin_amdgcn_perm(0u, M, 0x0C030C02u) << 3) | 0x41804180u;
-        const v4s av = __builtin_bit_cast(v4s, make_uint2(a01, a23));
         const int kb = 2 * (4 * c + mm) + h;
+        v4s bv[3];
 #pragma unroll
-        for (int t = 0; t < 3; ++t) {
-          const v4s bv = __builtin_bit_cast(v4s, bfrag[kb * 3 + t][lane]);
-          acc[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(av, bv, acc[t], 0, 0, 0);
+        for (int u = 0; u < 3; ++u) bv[u] = __builtin_bit_cast(v4s, bfrag[kb * 3 + u][lane]);
+#pragma unroll
+        for (int t = 0; t < RT; ++t) {
+          // group 8m + 2kq + h: the high nibble of each byte for h = 0
+          uint32_t M = h == 0 ? (wb[t] >> 4) & 0x0F0F0F0Fu : wb[t] & 0x0F0F0F0Fu;
+          // 4 x 4 bit transpose: bit e of byte p (plane p, item e) -> bit p of byte e
+          const uint32_t t1 = ((M >> 14) ^ M) & 0x00000C0Cu;
+          M ^= t1 ^ (t1 << 14);
+          const uint32_t t2 = ((M >> 7) ^ M) & 0x000A000Au;
+          M ^= t2 ^ (t2 << 7);
+          // byte e = code q of item e; A item = bf16(q + 16) = 0x4180 | q << 3
+          const uint32_t a01 = (__builtin_amdgcn_perm(0u, M, 0x0C010C00u) << 3) | 0x41804180u;
+          const uint32_t a23 = (__builtin_amdgcn_perm(0u, M, 0x0C030C02u) << 3) | 0x41804180u;
+          const v4s av = __builtin_bit_cast(v4s, make_uint2(a01, a23));
+#pragma unroll
+          for (int u = 0; u < 3; ++u) acc[t][u] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(av, bv[u], acc[t][u], 0, 0, 0);
         }
       }
     }
@@ -1379,17 +1403,22 @@ __global__ __launch_bounds__(kWave * NW) void lut_gemv_mfma_kernel(GemvArgs a, i
       float xs = 0.0f;   // the chunk's sum of vector li's activations
 #pragma unroll
       for (int kb = 8 * c; kb < 8 * c + 8; ++kb) xs += xsb[kb][li];
-      const v4f s = ((acc[0] + acc[1]) + acc[2]) - 24.0f * xs;
-      y[0] = fmaf(sc[c].x, s[0], y[0]);
-      y[1] = fmaf(sc[c].y, s[1], y[1]);
-      y[2] = fmaf(sc[c].z, s[2], y[2]);
-      y[3] = fmaf(sc[c].w, s[3], y[3]);
+#pragma unroll
+      for (int t = 0; t < RT; ++t) {
+        const v4f s = ((acc[t][0] + acc[t][1]) + acc[t][2]) - 24.0f * xs;
+        y[t][0] = fmaf(sc[t][c].x, s[0], y[t][0]);
+        y[t][1] = fmaf(sc[t][c].y, s[1], y[t][1]);
+        y[t][2] = fmaf(sc[t][c].z, s[2], y[t][2]);
+        y[t][3] = fmaf(sc[t][c].w, s[3], y[t][3]);
+      }
     }
   }
   // D[i][j]: lane j + 16 (i / 4), item i % 4 -> rows row0 + 4 kq + e of vector li
-  if (li < NB)
-    *reinterpret_cast<float4 *>(a.partials + (size_t(li) * splits + split) * Npad + uint32_t(row0 + 4 * kq)) =
-        make_float4(y[0], y[1], y[2], y[3]);
+#pragma unroll
+  for (int t = 0; t < RT; ++t)
+    if (li < NB && live[t])
+      *reinterpret_cast<float4 *>(a.partials + (size_t(li) * splits + split) * Npad + uint32_t(row0[t] + 4 * kq)) =
+          make_float4(y[t][0], y[t][1], y[t][2], y[t][3]);
 }
 
 // y[n*rows + r] = sum_s partials[n][s][r] (+ bias[r]) (+ resid[n*rows + r])
@@ -1887,19 +1916,21 @@ static int launch_batch_nb(const GemvArgs &a, hipStream_t st) {
   bool mfma = false;
   if constexpr (FMT == LMX_FMT_INT4 && NB >= 8) mfma = a.rotate == LMX_ROTATE_NONE && mfma_batched() && a.xmode == kXModeNone;
   if (mfma) {
-    // 8 waves (128 rows) per workgroup, the slice's activation fragments
-    // built once for them (LMX_MFMA=4: 4 waves)
-    const bool w4 = mfma_batched() == 4;
-    const int nw = w4 ? 4 : 8;
-    const int row_blocks = (a.Npad + 16 * nw - 1) / (16 * nw);
+    // 8 waves of 16 rows per workgroup, the slice's activation fragments
+    // built once for them (LMX_MFMA=4: 4 waves; 2: 32 rows per wave)
+    const int mode = mfma_batched();
+    const int nw = mode == 4 ? 4 : 8, rt = mode == 2 ? 2 : 1;
+    const int row_blocks = (a.Npad + 16 * nw * rt - 1) / (16 * nw * rt);
     const dim3 grid(row_blocks * splits), block(kWave * nw);
-    if (w4) {
-      if (narrow) lut_gemv_mfma_kernel<NB, 1, 4><<<grid, block, 0, st>>>(a, row_blocks, splits);
-      else lut_gemv_mfma_kernel<NB, 2, 4><<<grid, block, 0, st>>>(a, row_blocks, splits);
-    } else {
-      if (narrow) lut_gemv_mfma_kernel<NB, 1, 8><<<grid, block, 0, st>>>(a, row_blocks, splits);
-      else lut_gemv_mfma_kernel<NB, 2, 8><<<grid, block, 0, st>>>(a, row_blocks, splits);
-    }
+#define LMX_MFMA_LAUNCH(NW, RT)                                                                   \
+  do {                                                                                            \
+    if (narrow) lut_gemv_mfma_kernel<NB, 1, NW, RT><<<grid, block, 0, st>>>(a, row_blocks, splits); \
+    else lut_gemv_mfma_kernel<NB, 2, NW, RT><<<grid, block, 0, st>>>(a, row_blocks, splits);        \
+  } while (0)
+    if (mode == 4) LMX_MFMA_LAUNCH(4, 1);
+    else if (mode == 2) LMX_MFMA_LAUNCH(8, 2);
+    else LMX_MFMA_LAUNCH(8, 1);
+#undef LMX_MFMA_LAUNCH
   } else if (narrow) {
     launch_batch_rg<FMT, NB, 1, 1>(a, splits, st);
   } else if (rg == 4) {
