@@ -1368,12 +1368,21 @@ __global__ __launch_bounds__(kWave * NW) void lut_gemv_mfma_kernel(GemvArgs a, i
       for (int u = 0; u < 3; ++u) acc[t][u] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int mm = 0; mm < 4; ++mm) {
-      // byte kq of word mm of planes 0..3 -> bytes 0..3
-      uint32_t wb[RT];
+      // byte kq of word mm of planes 0..3 -> bytes 0..3 (high nibbles group
+      // 8m + 2kq, low nibbles group 8m + 2kq + 1), then both nibble halves'
+      // 4 x 4 bit transposes at once: bit e of byte p (plane p, item e) ->
+      // bit p of byte e (in the same half)
+      uint32_t T[RT];
 #pragma unroll
-      for (int t = 0; t < RT; ++t)
-        wb[t] = __builtin_amdgcn_perm(w[t][c][1][mm], w[t][c][0][mm], sel01) |
-                __builtin_amdgcn_perm(w[t][c][3][mm], w[t][c][2][mm], sel23);
+      for (int t = 0; t < RT; ++t) {
+        uint32_t M = __builtin_amdgcn_perm(w[t][c][1][mm], w[t][c][0][mm], sel01) |
+                     __builtin_amdgcn_perm(w[t][c][3][mm], w[t][c][2][mm], sel23);
+        const uint32_t t1 = ((M >> 14) ^ M) & 0x0000CCCCu;
+        M ^= t1 ^ (t1 << 14);
+        const uint32_t t2 = ((M >> 7) ^ M) & 0x00AA00AAu;
+        M ^= t2 ^ (t2 << 7);
+        T[t] = M;
+      }
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const int kb = 2 * (4 * c + mm) + h;
@@ -1382,16 +1391,11 @@ __global__ __launch_bounds__(kWave * NW) void lut_gemv_mfma_kernel(GemvArgs a, i
         for (int u = 0; u < 3; ++u) bv[u] = __builtin_bit_cast(v4s, bfrag[kb * 3 + u][lane]);
 #pragma unroll
         for (int t = 0; t < RT; ++t) {
-          // group 8m + 2kq + h: the high nibble of each byte for h = 0
-          uint32_t M = h == 0 ? (wb[t] >> 4) & 0x0F0F0F0Fu : wb[t] & 0x0F0F0F0Fu;
-          // 4 x 4 bit transpose: bit e of byte p (plane p, item e) -> bit p of byte e
-          const uint32_t t1 = ((M >> 14) ^ M) & 0x00000C0Cu;
-          M ^= t1 ^ (t1 << 14);
-          const uint32_t t2 = ((M >> 7) ^ M) & 0x000A000Au;
-          M ^= t2 ^ (t2 << 7);
-          // byte e = code q of item e; A item = bf16(q + 16) = 0x4180 | q << 3
-          const uint32_t a01 = (__builtin_amdgcn_perm(0u, M, 0x0C010C00u) << 3) | 0x41804180u;
-          const uint32_t a23 = (__builtin_amdgcn_perm(0u, M, 0x0C030C02u) << 3) | 0x41804180u;
+          // byte e's nibble h = code q of item e; A item = bf16(q + 16) = 0x4180 | q << 3
+          const uint32_t p01 = __builtin_amdgcn_perm(0u, T[t], 0x0C010C00u);
+          const uint32_t p23 = __builtin_amdgcn_perm(0u, T[t], 0x0C030C02u);
+          const uint32_t a01 = ((h == 0 ? p01 >> 1 : p01 << 3) & 0x00780078u) | 0x41804180u;
+          const uint32_t a23 = ((h == 0 ? p23 >> 1 : p23 << 3) & 0x00780078u) | 0x41804180u;
           const v4s av = __builtin_bit_cast(v4s, make_uint2(a01, a23));
 #pragma unroll
           for (int u = 0; u < 3; ++u) acc[t][u] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(av, bv[u], acc[t][u], 0, 0, 0);
