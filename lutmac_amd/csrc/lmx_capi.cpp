@@ -178,6 +178,7 @@ void free_weight(lmx_weight *w) {
   if (w->d_counters) (void)hipFree(w->d_counters);
   if (w->d_xrot) (void)hipFree(w->d_xrot);
   if (w->d_bpartials) (void)hipFree(w->d_bpartials);
+  if (w->d_nib) (void)hipFree(w->d_nib);
   delete w;
 }
 
@@ -232,6 +233,23 @@ int upload(int fmt, size_t rows, size_t cols, size_t group, const uint8_t *plane
       return hip_fail(e, "hipMalloc (batched partials)");
     }
     w->bpartials_cap = n;
+    // 4-bit: the codes once more in the matrix-core kernel's layout (groups
+    // of 8 and 16 vectors; the same 4 bits per weight as the planes)
+    if (fmt == LMX_FMT_INT4 && mfma_batched()) {
+      std::vector<uint8_t> nib;
+      try {
+        nib.resize(w->Kp * w->Npad / 2);
+      } catch (const std::bad_alloc &) {
+        free_weight(w);
+        return fail(LMX_ERR_OUT_OF_MEMORY, "host staging allocation failed");
+      }
+      nibble_tiles(planes, rows, row_bytes, w->Npad, w->Kp, nib.data());
+      if ((e = hipMalloc(&w->d_nib, nib.size())) != hipSuccess ||
+          (e = hipMemcpy(w->d_nib, nib.data(), nib.size(), hipMemcpyHostToDevice)) != hipSuccess) {
+        free_weight(w);
+        return hip_fail(e, "hipMalloc (matrix-core codes)");
+      }
+    }
   }
   if ((e = hipMemcpy(w->d_planes, tiles.data(), w->tile_bytes, hipMemcpyHostToDevice)) != hipSuccess ||
       (e = hipMemcpy(w->d_scales, sc.data(), w->scale_bytes, hipMemcpyHostToDevice)) != hipSuccess ||
@@ -297,6 +315,7 @@ int gemv_batched(const lmx_weight *w, GemvArgs a, const float *x, float *y, size
     a.resid = resid ? resid + *done * w->rows : nullptr;
     a.cols = int(w->cols);
     a.partials = w->d_bpartials;
+    a.nib = w->d_nib;
     if (nb == 4 && a.epi != kEpiNormOut && a.epi != kEpiPartials) {   // one full-K launch where the plan allows
       const int q = launch_gemv_quad(w->format, a, stream);
       if (q != 1) {

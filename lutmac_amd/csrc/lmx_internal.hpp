@@ -40,10 +40,17 @@ void tile_planes(int fmt, const uint8_t *planes, size_t rows, size_t row_bytes,
                  size_t Npad, size_t Kp, uint8_t *tiles);
 void untile_planes(int fmt, const uint8_t *tiles, size_t rows, size_t row_bytes,
                    size_t Npad, size_t Kp, uint8_t *planes);
+// 4-bit planes [4][rows][row_bytes] -> the matrix-core kernel's code layout
+// [Kp/128][Npad][4 lane groups kq][8 k-blocks][2 bytes]: byte b of k-block
+// kb, group kq holds codes k = 16 kb + 4 kq + 2b (low nibble) and + 1 (high
+// nibble) of the chunk; columns past row_bytes*8 and rows past `rows` hold
+// code 8 (value 0).
+void nibble_tiles(const uint8_t *planes, size_t rows, size_t row_bytes, size_t Npad, size_t Kp, uint8_t *out);
 
 // ---- device launches (lmx_kernels.hip) -----------------------------------
 struct GemvArgs {
   const void *planes;      // tiled planes
+  const void *nib;         // int4 codes in the matrix-core layout (nibble_tiles), or null
   const float *scales;     // [S][n_groups][Npad]
   const float *x;          // [cols]
   float *y;                // [rows]
@@ -237,6 +244,7 @@ struct lmx_weight {
   float *d_xrot = nullptr;  // staging for LMX_ROTATE_FWHT_FULL (cols floats)
   bool batched = true;           // batch >= 2 through the batched kernel (LMX_BATCHED=0: one GEMV per vector)
   float *d_bpartials = nullptr;  // batched partials [16][Kp/256][Npad], allocated with the handle
+  void *d_nib = nullptr;         // int4 with the matrix-core kernel: codes in nibble_tiles layout
   size_t bpartials_cap = 0;      // floats
 };
 

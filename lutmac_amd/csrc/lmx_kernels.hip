@@ -1272,7 +1272,12 @@ __global__ __launch_bounds__((kWave * batch_waves<NB, VG, RG>())) void lut_gemv_
 // kb = 2m + h of a slice takes the 4-groups g = 8m + 2kq + h: lane kq's
 // byte kq of word m of each plane holds its nibbles of both h, and item e
 // is k = 4g + 3 - e (the nibble's bit e, MSB-first planes).
-template <int NB, int CH, int NW, int RT>
+// NIB: the codes come from the handle's nibble_tiles copy (a.nib): lane
+// (i, kq) reads its 16 bytes of each 128-chunk in one load, k-block kb's
+// items e = 0..3 are k = 16 kb + 4 kq + e (bytes 2 kb, 2 kb + 1: two codes
+// each), and bf16(q + 16) of a byte's two codes is one multiply by 0x8008
+// and one and-or, no transpose.
+template <int NB, int CH, int NW, int RT, bool NIB = false>
 __global__ __launch_bounds__(kWave * NW) void lut_gemv_mfma_kernel(GemvArgs a, int row_blocks, int splits) {
   typedef short v4s __attribute__((ext_vector_type(4)));
   typedef float v4f __attribute__((ext_vector_type(4)));
@@ -1297,9 +1302,16 @@ __global__ __launch_bounds__(kWave * NW) void lut_gemv_mfma_kernel(GemvArgs a, i
   }
   const uint32_t Npad = uint32_t(a.Npad);
 
-  // ---- the rows' planes (row li of each tile) and the D rows' scales ----
-  u32x4 w[RT][CH][4];
-  {
+  // ---- the rows' planes or codes (row li of each tile) and the D rows' scales ----
+  u32x4 w[RT][CH][NIB ? 1 : 4];
+  if constexpr (NIB) {
+    const u32x4 *__restrict__ nb = reinterpret_cast<const u32x4 *>(a.nib);
+#pragma unroll
+    for (int t = 0; t < RT; ++t)
+#pragma unroll
+      for (int c = 0; c < CH; ++c)
+        w[t][c][0] = __builtin_nontemporal_load(nb + ((uint32_t(c0 + c) * Npad + uint32_t(row0[t] + li)) * 4 + kq));
+  } else {
     const u32x4 *__restrict__ pl = reinterpret_cast<const u32x4 *>(a.planes);
 #pragma unroll
     for (int t = 0; t < RT; ++t)
@@ -1321,11 +1333,13 @@ __global__ __launch_bounds__(kWave * NW) void lut_gemv_mfma_kernel(GemvArgs a, i
   // ---- B fragments of the slice: wave w splits k-blocks w, w + NW, ... ----
 #pragma unroll
   for (int kb = wave; kb < KB; kb += NW) {
-    const int g = 8 * (kb >> 1) + 2 * kq + (kb & 1);
-    const int k = c0 * kChunk + 4 * g;
+    // plane layout: item e of k-block kb is k = 4g + 3 - e, g = 8 (kb / 2) + 2 kq + kb % 2;
+    // NIB: k = 16 kb + 4 kq + e
+    const int k = c0 * kChunk + (NIB ? 16 * kb + 4 * kq : 4 * (8 * (kb >> 1) + 2 * kq + (kb & 1)));
     float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     if (li < NB && k < a.cols) v = *reinterpret_cast<const float4 *>(a.x + size_t(li) * a.cols + k);
-    const float xe[4] = {v.w, v.z, v.y, v.x};   // item e: k = 4g + 3 - e
+    float xe[4] = {v.w, v.z, v.y, v.x};
+    if constexpr (NIB) xe[0] = v.x, xe[1] = v.y, xe[2] = v.z, xe[3] = v.w;
     {
       float xs = (v.x + v.y) + (v.z + v.w);
       xs += __shfl_xor(xs, 16, kWave);
@@ -1366,6 +1380,25 @@ __global__ __launch_bounds__(kWave * NW) void lut_gemv_mfma_kernel(GemvArgs a, i
     for (int t = 0; t < RT; ++t)
 #pragma unroll
       for (int u = 0; u < 3; ++u) acc[t][u] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    if constexpr (NIB) {
+#pragma unroll
+      for (int kb8 = 0; kb8 < 8; ++kb8) {
+        const int kb = 8 * c + kb8;
+        v4s bv[3];
+#pragma unroll
+        for (int u = 0; u < 3; ++u) bv[u] = __builtin_bit_cast(v4s, bfrag[kb * 3 + u][lane]);
+#pragma unroll
+        for (int t = 0; t < RT; ++t) {
+          const uint32_t wd = w[t][c][0][kb8 >> 1] >> (16 * (kb8 & 1));
+          // byte (q0 | q1 << 4) * 0x8008: q0 at bits 3-6, q1 at bits 19-22
+          const uint32_t a01 = ((wd & 0xFFu) * 0x8008u & 0x00780078u) | 0x41804180u;
+          const uint32_t a23 = (((wd >> 8) & 0xFFu) * 0x8008u & 0x00780078u) | 0x41804180u;
+          const v4s av = __builtin_bit_cast(v4s, make_uint2(a01, a23));
+#pragma unroll
+          for (int u = 0; u < 3; ++u) acc[t][u] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(av, bv[u], acc[t][u], 0, 0, 0);
+        }
+      }
+    } else {
 #pragma unroll
     for (int mm = 0; mm < 4; ++mm) {
       // byte kq of word mm of planes 0..3 -> bytes 0..3 (high nibbles group
@@ -1402,6 +1435,7 @@ __global__ __launch_bounds__(kWave * NW) void lut_gemv_mfma_kernel(GemvArgs a, i
         }
       }
     }
+    }   // NIB
     const int ch = c0 + c;
     if (ch < a.Kp / kChunk) {
       float xs = 0.0f;   // the chunk's sum of vector li's activations
@@ -1921,15 +1955,21 @@ static int launch_batch_nb(const GemvArgs &a, hipStream_t st) {
   if constexpr (FMT == LMX_FMT_INT4 && NB >= 8) mfma = a.rotate == LMX_ROTATE_NONE && mfma_batched() && a.xmode == kXModeNone;
   if (mfma) {
     // 8 waves of 16 rows per workgroup, the slice's activation fragments
-    // built once for them (LMX_MFMA=4: 4 waves; 2: 32 rows per wave)
+    // built once for them, the codes from the handle's nibble copy
+    // (LMX_MFMA=4: 4 waves; 2: 32 rows per wave; 3: codes from the planes)
     const int mode = mfma_batched();
     const int nw = mode == 4 ? 4 : 8, rt = mode == 2 ? 2 : 1;
     const int row_blocks = (a.Npad + 16 * nw * rt - 1) / (16 * nw * rt);
     const dim3 grid(row_blocks * splits), block(kWave * nw);
-#define LMX_MFMA_LAUNCH(NW, RT)                                                                   \
-  do {                                                                                            \
-    if (narrow) lut_gemv_mfma_kernel<NB, 1, NW, RT><<<grid, block, 0, st>>>(a, row_blocks, splits); \
-    else lut_gemv_mfma_kernel<NB, 2, NW, RT><<<grid, block, 0, st>>>(a, row_blocks, splits);        \
+#define LMX_MFMA_LAUNCH(NW, RT)                                                                           \
+  do {                                                                                                    \
+    if (a.nib && mode != 3) {                                                                             \
+      if (narrow) lut_gemv_mfma_kernel<NB, 1, NW, RT, true><<<grid, block, 0, st>>>(a, row_blocks, splits); \
+      else lut_gemv_mfma_kernel<NB, 2, NW, RT, true><<<grid, block, 0, st>>>(a, row_blocks, splits);        \
+    } else {                                                                                              \
+      if (narrow) lut_gemv_mfma_kernel<NB, 1, NW, RT><<<grid, block, 0, st>>>(a, row_blocks, splits);       \
+      else lut_gemv_mfma_kernel<NB, 2, NW, RT><<<grid, block, 0, st>>>(a, row_blocks, splits);              \
+    }                                                                                                     \
   } while (0)
     if (mode == 4) LMX_MFMA_LAUNCH(4, 1);
     else if (mode == 2) LMX_MFMA_LAUNCH(8, 2);

@@ -9,6 +9,7 @@
 // byte k/8), so a plane byte is bit-identical to the reference's sign/zero/
 // data bytes wherever the reference already stores planes.
 #include <cstring>
+#include <algorithm>
 #include <vector>
 
 #include "lmx_internal.hpp"
@@ -198,6 +199,40 @@ uint8_t pad_byte(int fmt, int plane) {
       (fmt == LMX_FMT_INT4 && plane == 3))
     return 0xFF;
   return 0x00;
+}
+
+void nibble_tiles(const uint8_t *planes, size_t rows, size_t row_bytes, size_t Npad, size_t Kp, uint8_t *out) {
+  const size_t Kc = Kp / kChunk;
+  // spread[b]: the 8 bits of a plane byte (MSB first: k = 8m + j at bit 7 - j,
+  // quantize.hpp:135-180) at bit 4j of a word of 8 nibbles
+  static const std::vector<uint32_t> spread = [] {
+    std::vector<uint32_t> t(256);
+    for (unsigned b = 0; b < 256; ++b)
+      for (int j = 0; j < 8; ++j) t[b] |= ((b >> (7 - j)) & 1u) << (4 * j);
+    return t;
+  }();
+  std::vector<uint8_t> q(Kp);
+  for (size_t r = 0; r < Npad; ++r) {
+    // the row's codes q = sum_p bit_p << p, 8 (value 0) past the columns
+    std::fill(q.begin(), q.end(), uint8_t(8));
+    if (r < rows) {
+      for (size_t m = 0; m < row_bytes; ++m) {
+        uint32_t v = 0;
+        for (int p = 0; p < 4; ++p) v |= spread[planes[(size_t(p) * rows + r) * row_bytes + m]] << p;
+        for (int j = 0; j < 8; ++j) q[8 * m + j] = uint8_t((v >> (4 * j)) & 15u);
+      }
+    }
+    for (size_t c = 0; c < Kc; ++c) {
+      uint8_t *dst = out + (c * Npad + r) * 64;
+      const uint8_t *qc = q.data() + c * kChunk;
+      for (int kq = 0; kq < 4; ++kq)
+        for (int kb = 0; kb < 8; ++kb)
+          for (int b = 0; b < 2; ++b) {
+            const int k = 16 * kb + 4 * kq + 2 * b;
+            dst[kq * 16 + kb * 2 + b] = uint8_t(qc[k] | (qc[k + 1] << 4));
+          }
+    }
+  }
 }
 
 void tile_planes(int fmt, const uint8_t *planes, size_t rows, size_t row_bytes,
