@@ -1466,6 +1466,21 @@ __global__ __launch_bounds__(kWave * NW) void lut_gemv_mfma_kernel(GemvArgs a, i
 // partials), RL split loads in flight per round: 16, or 48 where K has more
 // than 16 slices (K = 8960: one round trip instead of three).
 constexpr int kReduceThreads = 256;
+
+// The bias and residual terms of rows r0..r0+3 of vector n (0 past the rows
+// or without the operand), loaded before the partials and before any store:
+// resid may alias y, so a load placed after a store to y waits for the
+// loads before it, one memory round trip per row.
+__device__ __forceinline__ void load_row_terms(const float *__restrict__ bias, const float *resid, int n, int rows,
+                                               int r0, float (&b)[4], float (&rs)[4]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = r0 + i;
+    b[i] = bias && r < rows ? bias[r] : 0.0f;
+    rs[i] = resid && r < rows ? resid[size_t(n) * rows + r] : 0.0f;
+  }
+}
+
 template <int RL>
 __global__ __launch_bounds__(kReduceThreads) void batched_reduce_kernel(const float *__restrict__ partials,
                                                                         int splits, int Npad, int rows,
@@ -1473,6 +1488,8 @@ __global__ __launch_bounds__(kReduceThreads) void batched_reduce_kernel(const fl
                                                                         const float *resid, float *y) {
   const int r0 = 4 * int(blockIdx.x * kReduceThreads + threadIdx.x), n = blockIdx.y;
   if (r0 >= rows) return;
+  float b[4], rs[4];
+  load_row_terms(bias, resid, n, rows, r0, b, rs);
   const float4 *p = reinterpret_cast<const float4 *>(partials + size_t(n) * splits * Npad + r0);
   const size_t step = size_t(Npad) / 4;
   float4 s = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
@@ -1489,8 +1506,8 @@ __global__ __launch_bounds__(kReduceThreads) void batched_reduce_kernel(const fl
     const int r = r0 + i;
     if (r >= rows) break;
     float v = t[i];
-    if (bias) v += bias[r];
-    if (resid) v += resid[size_t(n) * rows + r];
+    if (bias) v += b[i];
+    if (resid) v += rs[i];
     y[size_t(n) * rows + r] = v;
   }
 }
@@ -1504,6 +1521,12 @@ __global__ __launch_bounds__(kReduceThreads) void batched_reduce_pair_kernel(con
                                                                              float *__restrict__ act) {
   const int j0 = 4 * int(blockIdx.x * kReduceThreads + threadIdx.x), n = blockIdx.y;
   if (j0 >= h) return;
+  float bg[4], bu[4];   // the bias terms, loaded before the partials
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    bg[i] = bias && j0 + i < h ? bias[j0 + i] : 0.0f;
+    bu[i] = bias && j0 + i < h ? bias[h + j0 + i] : 0.0f;
+  }
   const float4 *pg = reinterpret_cast<const float4 *>(partials + size_t(n) * splits * Npad + j0);
   const float4 *pu = reinterpret_cast<const float4 *>(partials + size_t(n) * splits * Npad + h + j0);
   const size_t step = size_t(Npad) / 4;
@@ -1528,7 +1551,7 @@ __global__ __launch_bounds__(kReduceThreads) void batched_reduce_pair_kernel(con
     const int j = j0 + i;
     if (j >= h) break;
     float a = gs[i], b = us[i];
-    if (bias) a += bias[j], b += bias[h + j];
+    if (bias) a += bg[i], b += bu[i];
     act[size_t(n) * h + j] = a / (1.0f + expf(-a)) * b;
   }
 }
@@ -1548,12 +1571,21 @@ __global__ __launch_bounds__(kNormReduceThreads) void batched_reduce_norm_kernel
     const float *resid, float *y, const float *__restrict__ w, float eps, float *__restrict__ y2) {
   constexpr int NT = 256;   // rmsnorm_rows_kernel's threads
   static_assert(kNormReduceThreads % NT == 0, "the norm runs on the first 256 threads");
+  constexpr int WJ = 4;   // norm weights a thread loads up front: rows up to 4 * kNormReduceThreads
   extern __shared__ float row[];   // [rows]
   __shared__ float red[NT / kWave];
   const int n = blockIdx.x;
   const float *pn = partials + size_t(n) * splits * Npad;
   const size_t step = size_t(Npad) / 4;
+  float wk[WJ];
+#pragma unroll
+  for (int j = 0; j < WJ; ++j) {
+    const int k = int(threadIdx.x) + j * kNormReduceThreads;
+    wk[j] = k < rows ? w[k] : 0.0f;
+  }
   for (int r0 = 4 * int(threadIdx.x); r0 < rows; r0 += 4 * kNormReduceThreads) {
+    float b[4], rs[4];
+    load_row_terms(bias, resid, n, rows, r0, b, rs);
     const float4 *p = reinterpret_cast<const float4 *>(pn + r0);
     float4 s = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     for (int k0 = 0; k0 < splits; k0 += kNormReduceLoads) {
@@ -1570,8 +1602,8 @@ __global__ __launch_bounds__(kNormReduceThreads) void batched_reduce_norm_kernel
       const int r = r0 + i;
       if (r >= rows) break;
       float v = t[i];
-      if (bias) v += bias[r];
-      if (resid) v += resid[size_t(n) * rows + r];
+      if (bias) v += b[i];
+      if (resid) v += rs[i];
       y[size_t(n) * rows + r] = v;
       row[r] = v;
     }
@@ -1584,7 +1616,13 @@ __global__ __launch_bounds__(kNormReduceThreads) void batched_reduce_norm_kernel
   if (threadIdx.x < NT && (threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = ss;
   __syncthreads();
   const float inv = 1.0f / sqrtf(((red[0] + red[1]) + (red[2] + red[3])) / float(rows) + eps);
-  for (int k = threadIdx.x; k < rows; k += kNormReduceThreads) y2[size_t(n) * rows + k] = row[k] * inv * w[k];
+#pragma unroll
+  for (int j = 0; j < WJ; ++j) {
+    const int k = int(threadIdx.x) + j * kNormReduceThreads;
+    if (k < rows) y2[size_t(n) * rows + k] = row[k] * inv * wk[j];
+  }
+  for (int k = int(threadIdx.x) + WJ * kNormReduceThreads; k < rows; k += kNormReduceThreads)
+    y2[size_t(n) * rows + k] = row[k] * inv * w[k];
 }
 
 // Four vectors through the full-K geometry of the lean kernel (CPS 1): a
@@ -1658,6 +1696,21 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_quad_kernel(GemvArgs a
     const int g = a.gshift >= 0 ? int(ch) >> a.gshift : int(ch) / a.group_chunks;
 #pragma unroll
     for (int t = 0; t < S; ++t) sc[t] = a.scales[(uint32_t(t * a.n_groups + g)) * Npad + uint32_t(lr)];
+  }
+  // the epilogue thread's bias and residual terms, requested behind the
+  // weights so their round trip overlaps the lookups
+  float eb0 = 0.0f, eb1 = 0.0f, er = 0.0f;
+  if constexpr (PAIR) {
+    if (threadIdx.x < HR * 4 && a.bias) {
+      const int j = blockIdx.x * HR + threadIdx.x % HR;
+      eb0 = a.bias[j], eb1 = a.bias[a.rows / 2 + j];
+    }
+  } else if (threadIdx.x < RW * 4) {
+    const int r = blockIdx.x * RW + threadIdx.x % RW, n = threadIdx.x / RW;
+    if (r < a.rows) {
+      if (a.bias) eb0 = a.bias[r];
+      if (a.resid) er = a.resid[size_t(n) * a.rows + r];   // read before this thread stores y (resid may be y)
+    }
   }
   __builtin_amdgcn_sched_barrier(0);
 
@@ -1796,7 +1849,7 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_quad_kernel(GemvArgs a
         g += red[(k * RW + t) * 4 + n];
         u += red[(k * RW + HR + t) * 4 + n];
       }
-      if (a.bias) g += a.bias[j], u += a.bias[h + j];
+      if (a.bias) g += eb0, u += eb1;
       a.y[size_t(n) * h + j] = silu(g) * u;
     }
   } else if (threadIdx.x < RW * 4) {
@@ -1806,8 +1859,8 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_quad_kernel(GemvArgs a
 #pragma unroll
     for (int k = 0; k < WAVES; ++k) v += red[(k * RW + t) * 4 + n];
     if (r < a.rows) {
-      if (a.bias) v += a.bias[r];
-      if (a.resid) v += a.resid[size_t(n) * a.rows + r];
+      if (a.bias) v += eb0;
+      if (a.resid) v += er;
       a.y[size_t(n) * a.rows + r] = v;
     }
   }
