@@ -378,12 +378,12 @@ __device__ __forceinline__ void merge_pass(Load ld, int c0, int nb, int lane, fl
 // the new key (knew, LDS) and value (vn, this lane's columns) for the chunk
 // that holds the position (own): scores, a partial softmax and the weighted
 // V sum (model.cpp:326-372, attention.cpp:23-42), returned as (m, l, o).
-// Every lane of the wave calls it.
+// pwrow is the wave's 64-float LDS scratch.  Every lane of the wave calls it.
 // LEAN unrolls the loops partially (fewer registers, for a caller that holds
 // the next chunk's rows in registers meanwhile).
 template <int HD, bool LEAN = false>
 __device__ __forceinline__ void chunk_attend(const float (*ks)[HD + 4], const float (*vs)[HD], const float *qrow,
-                                             const float *knew, const float (&vn)[HD / kWave], int t0,
+                                             const float *knew, const float (&vn)[HD / kWave], float *pwrow, int t0,
                                              int pos, bool own, float scale, int lane, float &m, float &l,
                                              float (&o)[HD / kWave]) {
   constexpr int VD = HD / kWave;
@@ -392,77 +392,51 @@ __device__ __forceinline__ void chunk_attend(const float (*ks)[HD + 4], const fl
   const int n = min(kAttnChunk, pos - t0 + 1);
   const int jnew = own ? pos - t0 : -1;
   const int nold = own ? n - 1 : n;
-  // Scores with the lanes as 16 positions x 4 quarters of the head
-  // dimension: in round r, lane (pi, qd) sums q . k over quarter qd of
-  // position 16 r + pi; the quarters then combine across lanes.  Each lane
-  // reads its quarter of q once instead of the whole q row per position
-  // (an LDS broadcast costs the CU's LDS bandwidth of a full read).  Rows
-  // past the position are read and their sums dropped.
-  constexpr int QD = HD / 4;   // dims per quarter
-  constexpr int QF = QD / 4;   // float4 per quarter
-  // stages of SB float4: a stage's LDS reads are all requested before its
-  // multiply-adds (the scheduler otherwise keeps two in flight)
-  constexpr int SB = LEAN ? (QF < 4 ? QF : 4) : QF;
-  static_assert(QF % SB == 0, "whole stages");
-  const int pi = lane & 15, qd = lane >> 4;
-  float4 q4[QF];
+  float sc = -INFINITY;
+  if (valid) {
+    const float *kv = lane == jnew ? knew : ks[lane];
+    float acc = 0.0f;
+    // Stages of SB float4 pairs: a stage's LDS reads are all requested
+    // before its multiply-adds (the scheduler otherwise keeps two reads in
+    // flight and the one wave per SIMD waits out the LDS latency on every
+    // pair); the sum runs in the same order as one read at a time.
+    constexpr int SB = LEAN ? 4 : 8;
+    static_assert((HD / 4) % SB == 0, "whole stages");
 #pragma unroll
-  for (int b = 0; b < QF; ++b) q4[b] = *reinterpret_cast<const float4 *>(qrow + qd * QD + 4 * b);
-  float acc[4];
+    for (int d0 = 0; d0 < HD / 4; d0 += SB) {
+      float4 k4[SB], q4[SB];
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int j = 16 * r + pi;
-    const float *kv = (j == jnew ? knew : ks[j]) + qd * QD;
-    float a = 0.0f;
-#pragma unroll
-    for (int b0 = 0; b0 < QF; b0 += SB) {
-      float4 k4[SB];
-#pragma unroll
-      for (int b = 0; b < SB; ++b) k4[b] = *reinterpret_cast<const float4 *>(kv + 4 * (b0 + b));
+      for (int b = 0; b < SB; ++b) {
+        k4[b] = *reinterpret_cast<const float4 *>(kv + 4 * (d0 + b));
+        q4[b] = *reinterpret_cast<const float4 *>(qrow + 4 * (d0 + b));
+      }
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int b = 0; b < SB; ++b) {
-        a += q4[b0 + b].x * k4[b].x;
-        a += q4[b0 + b].y * k4[b].y;
-        a += q4[b0 + b].z * k4[b].z;
-        a += q4[b0 + b].w * k4[b].w;
+        acc += q4[b].x * k4[b].x;
+        acc += q4[b].y * k4[b].y;
+        acc += q4[b].z * k4[b].z;
+        acc += q4[b].w * k4[b].w;
       }
       __builtin_amdgcn_sched_barrier(0);
     }
-    acc[r] = a;
+    sc = acc * scale;
   }
-  // (q0 + q1) + (q2 + q3) in every lane of a position (the adds commute)
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    acc[r] += __shfl_xor(acc[r], 16, kWave);
-    acc[r] += __shfl_xor(acc[r], 32, kWave);
-  }
-  // lane p = 16 qd + pi holds position p's sum in round qd
-  const float full = qd == 0 ? acc[0] : qd == 1 ? acc[1] : qd == 2 ? acc[2] : acc[3];
-  const float sc = valid ? full * scale : -INFINITY;
   m = lane_max<32>(sc, lane);
   const float e = valid ? expf(sc - m) : 0.0f;
   l = lane_sum<32>(e, lane);
-  const int pe = __float_as_int(lane < nold ? e : 0.0f);   // cached positions only
+  pwrow[lane] = lane < nold ? e : 0.0f;      // cached positions only
   const float enew = __shfl(e, jnew < 0 ? 0 : jnew, 64);
-  // weighted V sum: position j's weight read from lane j into a scalar
-  // register (an LDS broadcast would cost the CU's LDS bandwidth of a full
-  // read), 8 running sums per column
-  float s8[VD][8];
-#pragma unroll
-  for (int u = 0; u < VD; ++u)
-#pragma unroll
-    for (int i = 0; i < 8; ++i) s8[u][i] = 0.0f;
-  constexpr int kUnrollJ = LEAN ? 16 : kAttnChunk;
-#pragma unroll kUnrollJ
-  for (int j = 0; j < kAttnChunk; ++j) {
-    const float p = __int_as_float(__builtin_amdgcn_readlane(pe, j));
-#pragma unroll
-    for (int u = 0; u < VD; ++u) s8[u][j % 8] += p * vs[j][u * kWave + lane];
-  }
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
 #pragma unroll
   for (int u = 0; u < VD; ++u) {
-    o[u] = ((s8[u][0] + s8[u][1]) + (s8[u][2] + s8[u][3])) + ((s8[u][4] + s8[u][5]) + (s8[u][6] + s8[u][7]));
+    const int d = u * kWave + lane;
+    float s8[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    constexpr int kUnrollJ = LEAN ? 16 : kAttnChunk;
+#pragma unroll kUnrollJ
+    for (int j = 0; j < kAttnChunk; ++j) s8[j % 8] += pwrow[j] * vs[j][d];
+    o[u] = ((s8[0] + s8[1]) + (s8[2] + s8[3])) + ((s8[4] + s8[5]) + (s8[6] + s8[7]));
     if (own) o[u] += enew * vn[u];
   }
 }
@@ -516,6 +490,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void a
   __shared__ float ks[kAttnChunk][HD + 4];   // padded rows: lane j reads row j without bank conflicts
   __shared__ float vs[kAttnChunk][HD];
   __shared__ float qs[8][HD];
+  __shared__ float pw[8][kAttnChunk];
   __shared__ float knew[HD];
   __shared__ float qkvb[PARTS ? (8 + 2) * HD : 1];   // PARTS: the summed q (up to 8 heads), k and v rows
   __shared__ unsigned ticket;
@@ -717,7 +692,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void a
     if (wave < hpw && tq <= pos) {   // chunk 0 of a live unit always holds positions
       float mq, lq, oq[VD];
       const bool ownq = pos / kAttnChunk == unit * CPW + q;   // the chunk holds the new position
-      chunk_attend<HD, (CPW > 1)>(ks, vs, qs[wave], knew, vn, tq, pos, ownq, scale, lane, mq, lq, oq);
+      chunk_attend<HD, (CPW > 1)>(ks, vs, qs[wave], knew, vn, pw[wave], tq, pos, ownq, scale, lane, mq, lq, oq);
       if (q == 0) {
         m = mq, l = lq;
 #pragma unroll
