@@ -188,6 +188,10 @@ __global__ __launch_bounds__(1024) void argmax_rows_kernel(const float *__restri
   }
   key = wave_max_key(key, threadIdx.x & (kWave - 1));
   if ((threadIdx.x & (kWave - 1)) == 0) best[threadIdx.x / kWave] = key;
+  // the position, read before this part's slot and ticket: the last
+  // sequence advances it only after every part has taken its ticket
+  int pos = 0;
+  if (threadIdx.x == 0) pos = *pos_p;
   __syncthreads();
   if (threadIdx.x != 0) return;
   for (int w = 1; w < 16; ++w) key = best[w] > key ? best[w] : key;
@@ -197,15 +201,19 @@ __global__ __launch_bounds__(1024) void argmax_rows_kernel(const float *__restri
     const unsigned t =
         __hip_atomic_fetch_add(seq_tickets + b * kTicketPad, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (t != unsigned(parts - 1)) return;   // another part finishes the sequence
-    for (int q = 0; q < parts; ++q) {
-      const unsigned long long k =
-          __hip_atomic_load(slots + size_t(b) * parts + q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      key = k > key ? k : key;
+    for (int q0 = 0; q0 < parts; q0 += 16) {   // 16 slot loads in flight
+      unsigned long long kv[16];
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+        kv[j] = q0 + j < parts ? __hip_atomic_load(slots + size_t(b) * parts + q0 + j, __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT)
+                               : 0ull;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) key = kv[j] > key ? kv[j] : key;
     }
     __hip_atomic_store(seq_tickets + b * kTicketPad, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   const int idx = key ? int(0xFFFFFFFFu - uint32_t(key)) : 0;
-  const int pos = *pos_p;
   if (pos + 1 >= n_forced && pos + 1 <= max_pos) {
     tokens[size_t(b) * tstride + pos + 1] = idx;
     if (pc) pc[idx] += 1u;   // the sampled token joins the history
@@ -233,17 +241,40 @@ __global__ __launch_bounds__(1024) void finish_embed_kernel(const unsigned long 
                                                             int n_groups, int group_chunks, int cols,
                                                             float *__restrict__ out, unsigned *__restrict__ pcount) {
   constexpr int P = EmbFmt<FMT>::P, S = EmbFmt<FMT>::S;
+  constexpr int SL = 4;   // slot loads in flight per thread
   __shared__ unsigned long long best[16];
   __shared__ int next;
-  unsigned long long key = 0;
-  for (int i = threadIdx.x; i < n_slots; i += 1024) key = slots[i] > key ? slots[i] : key;
+  // rounds of SL slot loads per thread (clamped, then dropped past n_slots,
+  // so that no load waits in a branch)
+  const int last = max(n_slots - 1, 0);
+  const auto round = [&](int i0, unsigned long long(&sv)[SL]) {
+#pragma unroll
+    for (int j = 0; j < SL; ++j) sv[j] = slots[min(i0 + j * 1024, last)];
+  };
+  const auto fold = [&](int i0, const unsigned long long(&sv)[SL], unsigned long long key) {
+#pragma unroll
+    for (int j = 0; j < SL; ++j) key = i0 + j * 1024 < n_slots && sv[j] > key ? sv[j] : key;
+    return key;
+  };
+  unsigned long long sv[SL];
+  round(int(threadIdx.x), sv);
+  // the position, requested behind the first slots (its round trip no
+  // longer follows the reduction); thread 0 advances it below, after every
+  // read of it
+  __builtin_amdgcn_sched_barrier(0);
+  const int pos = *pos_p;
+  __builtin_amdgcn_sched_barrier(0);
+  unsigned long long key = fold(int(threadIdx.x), sv, 0ull);
+  for (int i0 = int(threadIdx.x) + 1024 * SL; i0 < n_slots; i0 += 1024 * SL) {
+    round(i0, sv);
+    key = fold(i0, sv, key);
+  }
   key = wave_max_key(key, threadIdx.x & (kWave - 1));
   if ((threadIdx.x & (kWave - 1)) == 0) best[threadIdx.x / kWave] = key;
   __syncthreads();
   if (threadIdx.x == 0) {
     for (int w = 1; w < 16; ++w) key = best[w] > key ? best[w] : key;
     const int idx = key ? int(0xFFFFFFFFu - uint32_t(key)) : 0;   // no finite maximum: index 0
-    const int pos = *pos_p;
     int t = idx;
     if (pos + 1 <= max_pos) {
       if (pos + 1 >= n_forced) {
@@ -258,16 +289,32 @@ __global__ __launch_bounds__(1024) void finish_embed_kernel(const unsigned long 
   }
   __syncthreads();
   const int t = min(max(next, 0), rows - 1);
-  for (int k = threadIdx.x; k < cols; k += 1024) {
-    const int c = k / kChunk, byte = (k % kChunk) / 8, bit = 7 - k % 8;
-    int b[P];
+  // two columns per thread and round, every load of a round issued first
+  for (int k0 = threadIdx.x; k0 < cols; k0 += 2048) {
+    int b[2][P];
+    float sc[2][S];
 #pragma unroll
-    for (int p = 0; p < P; ++p) b[p] = (planes[((size_t(c) * P + p) * Npad + t) * 16 + byte] >> bit) & 1;
-    const int g = c / group_chunks;
-    float sc[S];
+    for (int h = 0; h < 2; ++h) {
+      const int k = min(k0 + 1024 * h, cols - 1);
+      const int c = k / kChunk, byte = (k % kChunk) / 8, bit = 7 - k % 8;
 #pragma unroll
-    for (int i = 0; i < S; ++i) sc[i] = scales[(size_t(i) * n_groups + g) * Npad + t];
-    out[k] = weight_value<FMT>(b, sc);
+      for (int p = 0; p < P; ++p) b[h][p] = (planes[((size_t(c) * P + p) * Npad + t) * 16 + byte] >> bit) & 1;
+      const int g = c / group_chunks;
+#pragma unroll
+      for (int i = 0; i < S; ++i) sc[h][i] = scales[(size_t(i) * n_groups + g) * Npad + t];
+    }
+    // one wait for both columns: without a use here the compiler sinks the
+    // second column's loads into its store's branch, after the first store
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+#pragma unroll
+      for (int p = 0; p < P; ++p) asm volatile("" ::"v"(b[h][p]));
+#pragma unroll
+      for (int i = 0; i < S; ++i) asm volatile("" ::"v"(sc[h][i]));
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      if (k0 + 1024 * h < cols) out[k0 + 1024 * h] = weight_value<FMT>(b[h], sc[h]);
   }
 }
 
