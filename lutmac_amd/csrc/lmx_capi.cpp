@@ -234,7 +234,7 @@ int upload(int fmt, size_t rows, size_t cols, size_t group, const uint8_t *plane
     }
     w->bpartials_cap = n;
     // 4-bit: the codes once more in the matrix-core kernel's layout (groups
-    // of 8 and 16 vectors; the same 4 bits per weight as the planes)
+    // of 4, 8 and 16 vectors; the same 4 bits per weight as the planes)
     if (fmt == LMX_FMT_INT4 && mfma_batched()) {
       std::vector<uint8_t> nib;
       try {

@@ -181,8 +181,9 @@ int launch_gemv(int fmt, const GemvArgs &a, void *stream);
 // the 4 x 4 x 1 and 16 x 4 x 1 plans (default), 2 the 4 x 4 x 1 plan only,
 // 0 neither.
 int plane_split_level();
-// Batched unrotated 4-bit GEMVs of 8 or 16 vectors on the matrix cores
-// (LMX_MFMA, read per call): 1 (default), 0 the lookup-table kernel.
+// Batched unrotated 4-bit GEMVs of 8 or 16 vectors, and of 4 except for
+// split partials left to a consumer, on the matrix cores (LMX_MFMA, read per
+// call): 1 (default), 0 the lookup-table kernel.
 int mfma_batched();
 // Rows of one output half a workgroup covers with kEpiSiluPair for these
 // arguments (format, plan, transform), 0 when that epilogue is not served.

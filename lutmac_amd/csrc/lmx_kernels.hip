@@ -2017,7 +2017,8 @@ static int launch_batch_nb(const GemvArgs &a, hipStream_t st) {
                  : grid(2) >= kBatchMinGrid ? 2
                                             : 1;
   bool mfma = false;
-  if constexpr (FMT == LMX_FMT_INT4 && NB >= 8) mfma = a.rotate == LMX_ROTATE_NONE && mfma_batched() && a.xmode == kXModeNone;
+  if constexpr (FMT == LMX_FMT_INT4 && NB >= 4)
+    mfma = a.rotate == LMX_ROTATE_NONE && mfma_batched() && a.xmode == kXModeNone && (NB >= 8 || a.epi != kEpiPartials);
   if (mfma) {
     // 8 waves of 16 rows per workgroup, the slice's activation fragments
     // built once for them, the codes from the handle's nibble copy

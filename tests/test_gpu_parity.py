@@ -328,8 +328,9 @@ def test_batched_gemv(cuda, fmt, batch, rows, cols):
         assert rel_max_err(y[b], ref) < TOL, f"vector {b}"
 
 
-# Unrotated 4-bit groups of 8 and 16 vectors run on the matrix cores
-# (LMX_MFMA=1, the default: 8 waves per workgroup, the codes from the
+# Unrotated 4-bit groups of 8 and 16 vectors, and groups of 4 the
+# four-vector kernel does not take (K past 2048 here), run on the matrix
+# cores (LMX_MFMA=1, the default: 8 waves per workgroup, the codes from the
 # handle's nibble copy; 2: two row tiles per wave; 3: the codes from the
 # planes; 4: four waves; 0 the
 # lookup-table kernel): 128- and 256-wide
@@ -337,7 +338,7 @@ def test_batched_gemv(cuda, fmt, batch, rows, cols):
 # and one per row, a last group of fewer vectors (9, 21), against the oracle.
 @pytest.mark.parametrize("mfma", ["1", "2", "3", "4", "0"])
 @pytest.mark.parametrize("group", [128, 256, 0])
-@pytest.mark.parametrize("batch", [8, 16, 9, 21])
+@pytest.mark.parametrize("batch", [8, 16, 9, 21, 4, 12])
 @pytest.mark.parametrize("rows,cols", [(300, 640), (513, 1536), (2048, 2048), (4160, 4096)])
 def test_batched_int4_matrix_cores(cuda, monkeypatch, mfma, group, batch, rows, cols):
     monkeypatch.setenv("LMX_MFMA", mfma)
