@@ -1343,13 +1343,24 @@ __global__ __launch_bounds__(kWave * NW) void lut_gemv_mfma_kernel(GemvArgs a, i
   }
 
   // ---- B fragments of the slice: wave w splits k-blocks w, w + NW, ... ----
+  // Every activation load of the wave is requested before any split (fewer
+  // registers than splitting each block as it arrives).
+  constexpr int KBW = (KB + NW - 1) / NW;   // k-blocks per wave
+  float4 xv[KBW];
 #pragma unroll
-  for (int kb = wave; kb < KB; kb += NW) {
+  for (int i = 0; i < KBW; ++i) {
+    const int kb = wave + i * NW;
     // plane layout: item e of k-block kb is k = 4g + 3 - e, g = 8 (kb / 2) + 2 kq + kb % 2;
     // NIB: k = 16 kb + 4 kq + e
     const int k = c0 * kChunk + (NIB ? 16 * kb + 4 * kq : 4 * (8 * (kb >> 1) + 2 * kq + (kb & 1)));
-    float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    if (li < NB && k < a.cols) v = *reinterpret_cast<const float4 *>(a.x + size_t(li) * a.cols + k);
+    xv[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (kb < KB && li < NB && k < a.cols) xv[i] = *reinterpret_cast<const float4 *>(a.x + size_t(li) * a.cols + k);
+  }
+#pragma unroll
+  for (int i = 0; i < KBW; ++i) {
+    const int kb = wave + i * NW;
+    if (kb >= KB) break;   // wave-uniform
+    const float4 v = xv[i];
     float xe[4] = {v.w, v.z, v.y, v.x};
     if constexpr (NIB) xe[0] = v.x, xe[1] = v.y, xe[2] = v.z, xe[3] = v.w;
     {
