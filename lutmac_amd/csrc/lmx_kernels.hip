@@ -620,7 +620,7 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_plain_kernel(GemvArgs 
   __syncthreads();
   if constexpr (PAIR) {
     if (threadIdx.x < HR) {
-      const int j = blockIdx.x * HR + threadIdx.x, h = a.rows / 2;
+      const int j = blockIdx.x * HR + threadIdx.x;
       float g = 0.0f, u = 0.0f;
 #pragma unroll 8
       for (int k = 0; k < WAVES; ++k) {
