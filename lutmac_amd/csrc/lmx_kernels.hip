@@ -501,17 +501,16 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_plain_kernel(GemvArgs 
 #pragma unroll
     for (int t = 0; t < S; ++t) sc[c][t] = a.scales[(uint32_t(t * a.n_groups + g)) * Npad + uint32_t(lr)];
   }
-  // the epilogue thread's bias terms (the decoder's residual rides there),
-  // requested with the weights so that their round trip overlaps the lookups
-  float eb0 = 0.0f, eb1 = 0.0f;
-  if constexpr (PAIR) {
-    if (threadIdx.x < HR && a.bias) {
-      const int j = blockIdx.x * HR + threadIdx.x;
-      eb0 = a.bias[j], eb1 = a.bias[a.rows / 2 + j];
+  // the epilogue thread's bias term (the decoder's residual rides there),
+  // requested with the weights so that its round trip overlaps the lookups
+  // (not for the SiLU pair, whose gate|up carries no residual: two live
+  // registers there cost a workgroup per CU)
+  float eb0 = 0.0f;
+  if constexpr (!PAIR) {
+    if (threadIdx.x < RW && a.bias) {
+      const int r = blockIdx.x * RW + threadIdx.x;
+      if (r < a.rows) eb0 = a.bias[r];
     }
-  } else if (threadIdx.x < RW && a.bias) {
-    const int r = blockIdx.x * RW + threadIdx.x;
-    if (r < a.rows) eb0 = a.bias[r];
   }
   __builtin_amdgcn_sched_barrier(0);
 
@@ -627,7 +626,7 @@ __global__ __launch_bounds__(WAVES * kWave) void lut_gemv_plain_kernel(GemvArgs 
         g += red[k * RW + threadIdx.x];
         u += red[k * RW + HR + threadIdx.x];
       }
-      if (a.bias) g += eb0, u += eb1;
+      if (a.bias) g += a.bias[j], u += a.bias[a.rows / 2 + j];
       a.y[j] = silu(g) * u;
     }
   } else if (threadIdx.x < RW) {
