@@ -1289,7 +1289,7 @@ __global__ __launch_bounds__((kWave * batch_waves<NB, VG, RG>())) void lut_gemv_
 // each), and bf16(q + 16) of a byte's two codes is one multiply by 0x8008
 // and one and-or, no transpose.
 template <int NB, int CH, int NW, int RT, bool NIB = false>
-__global__ __launch_bounds__(kWave * NW) void lut_gemv_mfma_kernel(GemvArgs a, int row_blocks, int splits) {
+__global__ __launch_bounds__(kWave * NW) void lut_gemv_mfma_kernel(GemvArgs a, int row_blocks, int splits, int xmap) {
   typedef short v4s __attribute__((ext_vector_type(4)));
   typedef float v4f __attribute__((ext_vector_type(4)));
   constexpr int KB = 8 * CH;   // 16-k blocks per slice
@@ -1298,7 +1298,16 @@ __global__ __launch_bounds__(kWave * NW) void lut_gemv_mfma_kernel(GemvArgs a, i
   __shared__ uint2 bfrag[KB * 3][kWave];   // B fragments: [k-block][part][lane], 4 bf16 each
   __shared__ float xsb[KB][16];            // sum of each k-block's activations per vector
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
-  const int rb = blockIdx.x % row_blocks, split = blockIdx.x / row_blocks;
+  int rb = blockIdx.x % row_blocks, split = blockIdx.x / row_blocks;
+  if (xmap) {
+    // XCD-aware: workgroup i runs on XCD i % 8, and XCD x takes the slices
+    // congruent to x mod 8 (every row block of them), so a slice's
+    // activations are fetched into one XCD's L2 instead of all eight
+    const int q = int(blockIdx.x) / 8;
+    split = int(blockIdx.x) % 8 + 8 * (q / row_blocks);
+    rb = q % row_blocks;
+    if (split >= splits) return;   // padding: the whole workgroup, before any barrier
+  }
   const int c0 = split * CH;
   const int kq = lane >> 4, li = lane & 15;
   // tile t of the wave: rows row0[t] .. + 15; tiles past Npad redo the last
@@ -2036,15 +2045,22 @@ static int launch_batch_nb(const GemvArgs &a, hipStream_t st) {
     const int mode = mfma_batched();
     const int nw = mode == 4 ? 4 : 8, rt = mode == 2 ? 2 : 1;
     const int row_blocks = (a.Npad + 16 * nw * rt - 1) / (16 * nw * rt);
-    const dim3 grid(row_blocks * splits), block(kWave * nw);
+    // XCD-aware slices where there are many (each XCD's L2 would otherwise
+    // fetch every slice's activations; LMX_MFMA_XCD=0 turns it off)
+    static const bool xcd_env = [] {
+      const char *e = std::getenv("LMX_MFMA_XCD");
+      return !(e && std::atoi(e) == 0);
+    }();
+    const int xmap = xcd_env && splits >= 16 ? 1 : 0;
+    const dim3 grid(xmap ? 8 * ((splits + 7) / 8) * row_blocks : row_blocks * splits), block(kWave * nw);
 #define LMX_MFMA_LAUNCH(NW, RT)                                                                           \
   do {                                                                                                    \
     if (a.nib && mode != 3) {                                                                             \
-      if (narrow) lut_gemv_mfma_kernel<NB, 1, NW, RT, true><<<grid, block, 0, st>>>(a, row_blocks, splits); \
-      else lut_gemv_mfma_kernel<NB, 2, NW, RT, true><<<grid, block, 0, st>>>(a, row_blocks, splits);        \
+      if (narrow) lut_gemv_mfma_kernel<NB, 1, NW, RT, true><<<grid, block, 0, st>>>(a, row_blocks, splits, xmap); \
+      else lut_gemv_mfma_kernel<NB, 2, NW, RT, true><<<grid, block, 0, st>>>(a, row_blocks, splits, xmap);        \
     } else {                                                                                              \
-      if (narrow) lut_gemv_mfma_kernel<NB, 1, NW, RT><<<grid, block, 0, st>>>(a, row_blocks, splits);       \
-      else lut_gemv_mfma_kernel<NB, 2, NW, RT><<<grid, block, 0, st>>>(a, row_blocks, splits);              \
+      if (narrow) lut_gemv_mfma_kernel<NB, 1, NW, RT><<<grid, block, 0, st>>>(a, row_blocks, splits, xmap);       \
+      else lut_gemv_mfma_kernel<NB, 2, NW, RT><<<grid, block, 0, st>>>(a, row_blocks, splits, xmap);              \
     }                                                                                                     \
   } while (0)
     if (mode == 4) LMX_MFMA_LAUNCH(4, 1);
